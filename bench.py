@@ -1,0 +1,193 @@
+"""Benchmark: temporal-attention aggregated edges/s, forward + backward, fanout 10, on one GPU.
+
+One step = one training step of a 2-layer TGAT attention stack (modules.py:48-64 with the
+layers of layers.py:53-240) over one synthetic MFG of config C3: 4000 roots x 3 = 12000
+top-layer destinations, fanout [10, 10] (bottom block 132000 destinations / 1.32M edges, top
+block 12000 / 120000), node rows gathered from a 1M x 100 table and edge rows from a
+10M x 172 table by uniform random ids, dt ~ Exp(mean 1e4), time dim 100, 2 heads, hidden
+100, float32, dropout 0.1 / attention dropout 0.1 (config/TGAT.yml), Adam. Inputs are
+resident in HBM before timing; the step covers everything from the blocks' row offsets to
+the optimizer update.
+
+Prints one JSON line (see keys below). ``roofline`` is the fused kernel with the largest
+total time, timed by HIP events around each launch; ``cpu_baseline`` is the CPU
+restatement in oracle/ timed on the host cores over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "temporal-attn aggregated edges/s fwd+bwd (fanout 10); HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--roots", type=int, default=4000)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-roots", type=int, default=200,
+                    help="roots of the bounded CPU sample (same MFG shape, fewer roots)")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(roots: int, reps: int, seed: int) -> dict:
+    """The CPU restatement (oracle/ref_cpu.py, float32, torch on the host cores) of the same
+    2-layer forward + backward on a bounded sample: ``roots`` roots instead of 4000."""
+    import torch
+
+    from fast_amd.tgat import TGATEncoder
+    from fast_amd.workloads import two_layer
+    from oracle.ref_cpu import layer_params, tgat_layer
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    torch.manual_seed(seed)
+    enc = TGATEncoder(100, 172, 100, 2, 100, num_layers=2, dropout=0.0, att_dropout=0.0)
+    inp = two_layer(roots=roots, n_nodes=1_000_000, n_edge_rows=1_000_000, seed=seed,
+                    device="cpu")
+    b0, b1 = inp.blocks
+    s0, d0 = b0.edges()
+    s1, d1 = b1.edges()
+
+    def step():
+        P0 = {k: (v.float().detach().requires_grad_(True) if isinstance(v, torch.Tensor) else v)
+              for k, v in layer_params(enc.layers["l0h0"]).items()}
+        P1 = {k: (v.float().detach().requires_grad_(True) if isinstance(v, torch.Tensor) else v)
+              for k, v in layer_params(enc.layers["l1h0"]).items()}
+        h0 = b0.node_table[b0.srcdata["ID"]]
+        f0 = b0.edge_table[b0.edata["ID"]]
+        r0 = tgat_layer(P0, h0, f0, b0.edata["dt"], s0, d0, b0.num_dst_nodes(), dtype=torch.float32)
+        f1 = b1.edge_table[b1.edata["ID"]]
+        r1 = tgat_layer(P1, r0, f1, b1.edata["dt"], s1, d1, b1.num_dst_nodes(), dtype=torch.float32)
+        r1.backward(inp.dout)
+
+    step()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    t = times[len(times) // 2]
+    edges = sum(inp.edges_per_layer)
+    return {"value": edges / t, "unit": "edges/s", "cores": cores, "kind": "port",
+            "sample": (f"2-layer TGAT fwd+bwd, {roots} roots x3 (blocks {b0.num_dst_nodes()}/"
+                       f"{inp.edges_per_layer[0]} and {b1.num_dst_nodes()}/{inp.edges_per_layer[1]}"
+                       f" dst/edges), float32, median of {reps} after 1 warm-up: "
+                       f"{t * 1e3:.1f} ms/step; CPU: {cpu_model()}")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding is design-only (DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import fast_amd
+    from fast_amd import tgat
+    from fast_amd.tgat import TGATEncoder
+    from fast_amd.workloads import two_layer
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    enc = TGATEncoder(100, 172, 100, 2, 100, num_layers=2, dropout=0.1, att_dropout=0.1).to(dev)
+    enc.train()
+    opt = torch.optim.Adam(enc.parameters(), lr=1e-4)
+    inp = two_layer(roots=args.roots, seed=args.seed, device=dev)
+    blocks = inp.blocks
+    edges = sum(inp.edges_per_layer)
+
+    def step():
+        for b in blocks:
+            b._rowptr = None  # a new batch's offsets are derived inside the step
+        opt.zero_grad(set_to_none=True)
+        out = enc(blocks)
+        out.backward(inp.dout)
+        opt.step()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = tgat.KernelTimer()
+    tgat.timer = timer
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    tgat.timer = None
+    ms = (t1 - t0) * 1e3 / args.steps
+    kern = timer.summary()
+    dom_name = max(kern, key=lambda k: kern[k]["ms"])
+    dom = kern[dom_name]
+    fused_ms = sum(d["ms"] for d in kern.values()) / args.steps
+
+    line = {
+        "metric": METRIC,
+        "value": edges / (ms * 1e-3),
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) tables, uniform ids, Exp(1e4) dt; random-init weights)",
+        "config": {
+            "workload": (f"C3: 2-layer TGAT attention fwd+bwd+Adam, {args.roots} roots x3, fanout "
+                         f"[10,10], blocks {blocks[0].num_dst_nodes()}/{inp.edges_per_layer[0]} and "
+                         f"{blocks[1].num_dst_nodes()}/{inp.edges_per_layer[1]} dst/edges, node "
+                         "table 1M x 100, edge table 10M x 172, time 100, 2 heads, hidden 100"),
+            "edges_per_step": edges,
+            "fused_kernel_edges_per_s": edges / (fused_ms * 1e-3),
+            "fused_kernels_ms_per_step": fused_ms,
+            "kernels": {k: {"launches": v["launches"], "avg_us": round(v["avg_us"], 2),
+                            "GB/s": round(v["GB/s"], 1)} for k, v in kern.items()},
+        },
+        "roofline": {
+            "kernel": dom_name,
+            "bound": "hbm",
+            "achieved": dom["GB/s"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dom["GB/s"] / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_roots, args.cpu_reps, args.seed)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

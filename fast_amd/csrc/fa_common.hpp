@@ -1,0 +1,110 @@
+// Shared device/host helpers for the gfx950 kernels of libfastagg_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fastagg.h"
+
+namespace fa {
+
+constexpr int kWave = 64;          // CDNA wavefront width
+constexpr int kBlock = 256;        // 4 waves per workgroup for the row kernels
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions. Lanes are combined inside each row of 16 with DPP (quad_perm,
+// row_half_mirror, row_mirror), then the four row results are read with readlane and
+// added in a fixed order, so every lane gets the same, order-deterministic value.
+// All 64 lanes must be active.
+// ---------------------------------------------------------------------------
+namespace dpp {
+constexpr int kQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+}  // namespace dpp
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<dpp::kQuadSwap1>(v);
+  v += dpp_mov<dpp::kQuadSwap2>(v);
+  v += dpp_mov<dpp::kRowHalfMirror>(v);
+  v += dpp_mov<dpp::kRowMirror>(v);
+  return v;
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<dpp::kQuadSwap1>(v));
+  v = fmaxf(v, dpp_mov<dpp::kQuadSwap2>(v));
+  v = fmaxf(v, dpp_mov<dpp::kRowHalfMirror>(v));
+  v = fmaxf(v, dpp_mov<dpp::kRowMirror>(v));
+  return v;
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)),
+               fmaxf(lane_read(v, 32), lane_read(v, 48)));
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// Broadcast a wave-uniform integer into a scalar register.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+__device__ __forceinline__ float dot4(const float4& a, const float4& b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+__device__ __forceinline__ void fma4(float4& acc, float s, const float4& x) {
+  acc.x = fmaf(s, x.x, acc.x);
+  acc.y = fmaf(s, x.y, acc.y);
+  acc.z = fmaf(s, x.z, acc.z);
+  acc.w = fmaf(s, x.w, acc.w);
+}
+
+__device__ __forceinline__ void scale4(float4& acc, float s) {
+  acc.x *= s;
+  acc.y *= s;
+  acc.z *= s;
+  acc.w *= s;
+}
+
+__device__ __forceinline__ float leaky(float z, float slope) { return z > 0.f ? z : z * slope; }
+
+// Time-encoding argument w*t + b with the product and the sum rounded separately,
+// matching an unfused multiply followed by an add. HIP's __fmul_rn/__fadd_rn are plain
+// operators that -ffp-contract=fast would fuse into one FMA (a different rounding of an
+// argument of size ~1e4), so contraction is switched off here.
+__device__ __forceinline__ float time_arg(float t, float w, float b) {
+#pragma clang fp contract(off)
+  return t * w + b;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : static_cast<int>(e);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+}  // namespace fa

@@ -1,0 +1,740 @@
+// PyTorch-ROCm binding "fastAgg": the operator names, positional argument order, tensor
+// layouts and return types of the FAST reference module
+// (getFastAgg/cuda_operators/operators.cpp:606-625), implemented by the C ABI of
+// libfastagg_hip.so (include/fastagg.h), plus the fused TGAT operators of this build.
+//
+// Every op validates its tensors (device, contiguity, dtype, shape) before any launch,
+// allocates its outputs with torch on the inputs' device, enqueues on torch's current
+// stream and never synchronises. Outputs that the reference returns as fresh zeros are
+// allocated as zeros here too.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <cstdlib>
+#include <optional>
+#include <vector>
+
+#include "fastagg.h"
+
+namespace {
+
+// Same checks and messages as the reference (operators.cpp:4-6).
+#define CHECK_CUDA(x) TORCH_CHECK((x).is_cuda(), #x " must be a CUDA tensor")
+#define CHECK_CONTIGUOUS(x) TORCH_CHECK((x).is_contiguous(), #x " must be contiguous")
+#define CHECK_INPUT(x) \
+  CHECK_CUDA(x);       \
+  CHECK_CONTIGUOUS(x)
+#define CHECK_DTYPE(x, t) \
+  TORCH_CHECK((x).scalar_type() == (t), #x " must have dtype ", (t), ", got ", (x).scalar_type())
+#define CHECK_DIM(x, d) TORCH_CHECK((x).dim() == (d), #x " must be ", (d), "-D, got ", (x).dim(), "-D")
+#define CHECK_SAME_DEVICE(a, b) \
+  TORCH_CHECK((a).device() == (b).device(), #a " and " #b " must be on the same device")
+
+hipStream_t stream_of(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+void check_status(int st, const char* op) {
+  TORCH_CHECK(st == FA_OK, "fastAgg.", op, ": ", fa_status_string(st), " (status ", st, ")");
+}
+
+// Optional NaN report on an output (FASTAGG_DEBUG_NAN=1), in place of the reference's
+// unconditional device-to-host copies; it synchronises, so it is off by default.
+void debug_nan(const at::Tensor& t, const char* op) {
+  static const bool on = [] {
+    const char* v = std::getenv("FASTAGG_DEBUG_NAN");
+    return v && v[0] == '1';
+  }();
+  if (on && t.numel() > 0 && at::isnan(t).any().item<bool>())
+    TORCH_WARN("fastAgg.", op, ": output contains NaN");
+}
+
+int64_t num_segments(const at::Tensor& indptr) { return indptr.numel() > 0 ? indptr.numel() - 1 : 0; }
+
+// ----------------------------------------------------------------------------------
+// Segmented softmax (edge_softmax.cu)
+// ----------------------------------------------------------------------------------
+at::Tensor softmax_fwd_impl(const at::Tensor& indptr, const at::Tensor& x, int64_t heads, int mode,
+                            const char* op) {
+  CHECK_DTYPE(indptr, at::kInt);
+  CHECK_DIM(x, 2);
+  CHECK_SAME_DEVICE(indptr, x);
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "input_feat must be float32 or float64");
+  TORCH_CHECK(heads >= 0 && heads <= x.size(1), op, ": num_heads (", heads,
+              ") must lie in [0, input_feat.size(1)=", x.size(1), "]");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  auto y = at::zeros({x.size(0), heads}, x.options());
+  const int64_t S = num_segments(indptr);
+  int st;
+  if (x.scalar_type() == at::kFloat)
+    st = fa_edge_softmax_fwd_f32(indptr.data_ptr<int32_t>(), S, x.size(0), x.data_ptr<float>(),
+                                 x.size(1), heads, y.data_ptr<float>(), heads, mode, stream_of(x));
+  else
+    st = fa_edge_softmax_fwd_f64(indptr.data_ptr<int32_t>(), S, x.size(0), x.data_ptr<double>(),
+                                 x.size(1), heads, y.data_ptr<double>(), heads, mode, stream_of(x));
+  check_status(st, op);
+  debug_nan(y, op);
+  return y;
+}
+
+at::Tensor softmax_bwd_impl(const at::Tensor& indptr, const at::Tensor& dy, const at::Tensor& y,
+                            int64_t heads, const char* op) {
+  CHECK_DTYPE(indptr, at::kInt);
+  CHECK_DIM(dy, 2);
+  CHECK_SAME_DEVICE(indptr, dy);
+  CHECK_SAME_DEVICE(y, dy);
+  TORCH_CHECK(dy.scalar_type() == at::kFloat || dy.scalar_type() == at::kDouble,
+              "d_output must be float32 or float64");
+  TORCH_CHECK(y.scalar_type() == dy.scalar_type(), "output and d_output must share a dtype");
+  TORCH_CHECK(y.dim() == 2 && y.size(0) == dy.size(0) && y.size(1) >= heads,
+              op, ": output must be [E, >=num_heads] with E = d_output.size(0)");
+  TORCH_CHECK(heads >= 0 && heads <= dy.size(1), op, ": num_heads (", heads,
+              ") must lie in [0, d_output.size(1)=", dy.size(1), "]");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(dy.device());
+  auto dx = at::zeros({dy.size(0), dy.size(1)}, dy.options());
+  const int64_t S = num_segments(indptr);
+  int st;
+  if (dy.scalar_type() == at::kFloat)
+    st = fa_edge_softmax_bwd_f32(indptr.data_ptr<int32_t>(), S, dy.size(0), dy.data_ptr<float>(),
+                                 dy.size(1), y.data_ptr<float>(), y.size(1), heads,
+                                 dx.data_ptr<float>(), dx.size(1), stream_of(dy));
+  else
+    st = fa_edge_softmax_bwd_f64(indptr.data_ptr<int32_t>(), S, dy.size(0), dy.data_ptr<double>(),
+                                 dy.size(1), y.data_ptr<double>(), y.size(1), heads,
+                                 dx.data_ptr<double>(), dx.size(1), stream_of(dy));
+  check_status(st, op);
+  debug_nan(dx, op);
+  return dx;
+}
+
+// forward_edge_softmax (operators.cpp:167-205): output [E, num_heads].
+std::vector<at::Tensor> forward_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                             at::Tensor input_feat, int64_t node_num_per_block,
+                                             int64_t num_heads) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(input_feat);
+  (void)node_num_per_block;  // launch tuning in the reference; no effect on the result
+  return {softmax_fwd_impl(indptr, input_feat, num_heads, 0, "forward_edge_softmax")};
+}
+
+// backward_edge_softmax (operators.cpp:385-427): d_input [E, d_output.size(1)], heads < num_heads.
+std::vector<at::Tensor> backward_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                              at::Tensor d_output, at::Tensor output,
+                                              int64_t node_num_per_block, int64_t num_heads) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(d_output);
+  CHECK_INPUT(output);
+  (void)node_num_per_block;
+  return {softmax_bwd_impl(indptr, d_output, output, num_heads, "backward_edge_softmax")};
+}
+
+// forward_csr_edge_softmax (operators.cpp:246-284): every head, any degree.
+std::vector<at::Tensor> forward_csr_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                                 at::Tensor input_feat, int64_t node_num_per_block,
+                                                 int64_t reduce_size) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(input_feat);
+  (void)node_num_per_block;
+  (void)reduce_size;
+  CHECK_DIM(input_feat, 2);
+  return {softmax_fwd_impl(indptr, input_feat, input_feat.size(1), 1, "forward_csr_edge_softmax")};
+}
+
+// backward_csr_edge_softmax (operators.cpp:470-512): every head of d_output.
+std::vector<at::Tensor> backward_csr_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                                  at::Tensor d_output, at::Tensor output,
+                                                  int64_t node_num_per_block, int64_t reduce_size) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(d_output);
+  CHECK_INPUT(output);
+  (void)node_num_per_block;
+  (void)reduce_size;
+  CHECK_DIM(d_output, 2);
+  return {softmax_bwd_impl(indptr, d_output, output, d_output.size(1), "backward_csr_edge_softmax")};
+}
+
+// forward/backward_balanced_edge_softmax (operators.cpp:207-245, 428-469): batches of edges
+// (int64 indptr [B+1]) with a 2-D int64 local-node-id table indices [B, maxN].
+void check_balanced(const at::Tensor& indptr, const at::Tensor& indices, const at::Tensor& x) {
+  CHECK_DTYPE(indptr, at::kLong);
+  CHECK_DTYPE(indices, at::kLong);
+  CHECK_DIM(indices, 2);
+  CHECK_DIM(x, 2);
+  CHECK_DTYPE(x, at::kFloat);
+  CHECK_SAME_DEVICE(indptr, x);
+  CHECK_SAME_DEVICE(indices, x);
+  TORCH_CHECK(indptr.numel() >= indices.size(0) + 1,
+              "indptr must hold indices.size(0)+1 batch offsets");
+}
+
+std::vector<at::Tensor> forward_balanced_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                                      at::Tensor input_feat,
+                                                      int64_t edge_num_per_block,
+                                                      int64_t reduce_size) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(input_feat);
+  (void)edge_num_per_block;
+  (void)reduce_size;
+  check_balanced(indptr, indices, input_feat);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(input_feat.device());
+  auto y = at::zeros_like(input_feat);
+  const int st = fa_group_softmax_fwd_f32(
+      indptr.data_ptr<int64_t>(), indices.size(0), indices.data_ptr<int64_t>(), indices.size(1),
+      input_feat.size(0), input_feat.data_ptr<float>(), input_feat.size(1), input_feat.size(1),
+      y.data_ptr<float>(), y.size(1), stream_of(input_feat));
+  check_status(st, "forward_balanced_edge_softmax");
+  debug_nan(y, "forward_balanced_edge_softmax");
+  return {y};
+}
+
+std::vector<at::Tensor> backward_balanced_edge_softmax(at::Tensor indptr, at::Tensor indices,
+                                                       at::Tensor d_output, at::Tensor output,
+                                                       int64_t node_num_per_block,
+                                                       int64_t reduce_size) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(d_output);
+  CHECK_INPUT(output);
+  (void)node_num_per_block;
+  (void)reduce_size;
+  check_balanced(indptr, indices, d_output);
+  CHECK_DTYPE(output, at::kFloat);
+  TORCH_CHECK(output.sizes() == d_output.sizes(), "output and d_output must have the same shape");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(d_output.device());
+  auto dx = at::zeros_like(d_output);
+  const int st = fa_group_softmax_bwd_f32(
+      indptr.data_ptr<int64_t>(), indices.size(0), indices.data_ptr<int64_t>(), indices.size(1),
+      d_output.size(0), d_output.data_ptr<float>(), d_output.size(1), output.data_ptr<float>(),
+      output.size(1), d_output.size(1), dx.data_ptr<float>(), dx.size(1), stream_of(d_output));
+  check_status(st, "backward_balanced_edge_softmax");
+  debug_nan(dx, "backward_balanced_edge_softmax");
+  return {dx};
+}
+
+// ----------------------------------------------------------------------------------
+// Sum aggregation (aggregate_acc_kernel.cu, aggregate_shd_kernel.cu)
+// ----------------------------------------------------------------------------------
+void check_edge_pair(const at::Tensor& a, const at::Tensor& b, const at::Tensor& x) {
+  CHECK_DTYPE(a, at::kLong);
+  CHECK_DTYPE(b, at::kLong);
+  CHECK_DIM(a, 1);
+  CHECK_DIM(b, 1);
+  TORCH_CHECK(a.numel() == b.numel(), "edge id arrays must have the same length");
+  CHECK_DIM(x, 2);
+  CHECK_DTYPE(x, at::kFloat);
+  CHECK_SAME_DEVICE(a, x);
+  CHECK_SAME_DEVICE(b, x);
+}
+
+// forward_tgat (operators.cpp:146-165): out[src_edges[e]] += input_feat[dst_edges[e]]
+// for every edge (the reference argument names: src_edges holds destination ids).
+std::vector<at::Tensor> forward_tgat(at::Tensor src_edges, at::Tensor dst_edges,
+                                     at::Tensor input_feat, int64_t dst_num, int64_t aggNodePB,
+                                     int64_t aggFeat) {
+  CHECK_INPUT(src_edges);
+  CHECK_INPUT(dst_edges);
+  CHECK_INPUT(input_feat);
+  (void)aggNodePB;
+  (void)aggFeat;
+  check_edge_pair(src_edges, dst_edges, input_feat);
+  TORCH_CHECK(dst_num >= 0, "dst_num must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(input_feat.device());
+  auto out = at::zeros({dst_num, input_feat.size(1)}, input_feat.options());
+  const int st = fa_edge_scatter_sum_f32(
+      src_edges.data_ptr<int64_t>(), dst_edges.data_ptr<int64_t>(), src_edges.numel(), nullptr, 0,
+      input_feat.data_ptr<float>(), input_feat.size(1), input_feat.size(0),
+      static_cast<int32_t>(input_feat.size(1)), out.data_ptr<float>(), out.size(1), dst_num,
+      stream_of(input_feat));
+  check_status(st, "forward_tgat");
+  return {out};
+}
+
+// backward_tgat (operators.cpp:364-384): d_out[dst_edges[e]] += d_input[src_edges[e]].
+std::vector<at::Tensor> backward_tgat(at::Tensor src_edges, at::Tensor dst_edges, at::Tensor d_input,
+                                      int64_t src_num, int64_t aggNodePB, int64_t aggFeat) {
+  CHECK_INPUT(src_edges);
+  CHECK_INPUT(dst_edges);
+  CHECK_INPUT(d_input);
+  (void)aggNodePB;
+  (void)aggFeat;
+  check_edge_pair(src_edges, dst_edges, d_input);
+  TORCH_CHECK(src_num >= 0, "src_num must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(d_input.device());
+  auto out = at::zeros({src_num, d_input.size(1)}, d_input.options());
+  const int st = fa_edge_scatter_sum_f32(
+      dst_edges.data_ptr<int64_t>(), src_edges.data_ptr<int64_t>(), src_edges.numel(), nullptr, 0,
+      d_input.data_ptr<float>(), d_input.size(1), d_input.size(0),
+      static_cast<int32_t>(d_input.size(1)), out.data_ptr<float>(), out.size(1), src_num,
+      stream_of(d_input));
+  check_status(st, "backward_tgat");
+  return {out};
+}
+
+// forward_tgat_shd (operators.cpp:120-145): CSR segment sum written to the segment's dst.
+std::vector<at::Tensor> forward_tgat_shd(at::Tensor indptr, at::Tensor indices, at::Tensor src_edges,
+                                         at::Tensor dst_edges, at::Tensor input_feat,
+                                         int64_t dst_nodes, int64_t aggNodePB, int64_t aggFeat) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(src_edges);
+  CHECK_INPUT(dst_edges);
+  CHECK_INPUT(input_feat);
+  (void)aggNodePB;
+  (void)aggFeat;
+  CHECK_DTYPE(indptr, at::kInt);
+  CHECK_SAME_DEVICE(indptr, input_feat);
+  check_edge_pair(src_edges, dst_edges, input_feat);
+  TORCH_CHECK(dst_nodes >= 0, "dst_nodes must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(input_feat.device());
+  auto out = at::zeros({dst_nodes, input_feat.size(1)}, input_feat.options());
+  const int st = fa_segment_sum_f32(
+      indptr.data_ptr<int32_t>(), num_segments(indptr), src_edges.data_ptr<int64_t>(),
+      dst_edges.data_ptr<int64_t>(), src_edges.numel(), input_feat.data_ptr<float>(),
+      input_feat.size(1), input_feat.size(0), static_cast<int32_t>(input_feat.size(1)),
+      out.data_ptr<float>(), out.size(1), dst_nodes, stream_of(input_feat));
+  check_status(st, "forward_tgat_shd");
+  return {out};
+}
+
+// backward_tgat_shd (operators.cpp:337-363): the transpose of forward_tgat_shd,
+// d_out[src_edges[e]] += d_input[dst_edges[e]] over the edges of the segments (the
+// reference argument names: dst_edges holds destination ids here).
+std::vector<at::Tensor> backward_tgat_shd(at::Tensor indptr, at::Tensor indices,
+                                          at::Tensor dst_edges, at::Tensor src_edges,
+                                          at::Tensor d_input, int64_t src_nodes, int64_t aggNodePB,
+                                          int64_t aggFeat) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(dst_edges);
+  CHECK_INPUT(src_edges);
+  CHECK_INPUT(d_input);
+  (void)aggNodePB;
+  (void)aggFeat;
+  CHECK_DTYPE(indptr, at::kInt);
+  CHECK_SAME_DEVICE(indptr, d_input);
+  check_edge_pair(dst_edges, src_edges, d_input);
+  TORCH_CHECK(src_nodes >= 0, "src_nodes must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(d_input.device());
+  auto out = at::zeros({src_nodes, d_input.size(1)}, d_input.options());
+  const int64_t S = num_segments(indptr);
+  const int st = fa_edge_scatter_sum_f32(
+      src_edges.data_ptr<int64_t>(), dst_edges.data_ptr<int64_t>(), src_edges.numel(),
+      S > 0 ? indptr.data_ptr<int32_t>() : nullptr, S, d_input.data_ptr<float>(),
+      d_input.size(1), d_input.size(0), static_cast<int32_t>(d_input.size(1)),
+      out.data_ptr<float>(), out.size(1), src_nodes, stream_of(d_input));
+  check_status(st, "backward_tgat_shd");
+  return {out};
+}
+
+// ----------------------------------------------------------------------------------
+// Fused LeakyReLU + softmax + dropout + aggregation (fused_attention.cu)
+// ----------------------------------------------------------------------------------
+void check_fused(const at::Tensor& scores_like, const at::Tensor& V, const at::Tensor& indptr,
+                 const at::Tensor& dst_eid, const at::Tensor& src_eid, int64_t num_heads) {
+  CHECK_INPUT(V);
+  CHECK_INPUT(dst_eid);
+  CHECK_INPUT(src_eid);
+  CHECK_DIM(scores_like, 2);
+  CHECK_DTYPE(scores_like, at::kFloat);
+  CHECK_DIM(V, 3);
+  CHECK_DTYPE(V, at::kFloat);
+  CHECK_DTYPE(indptr, at::kInt);
+  CHECK_DTYPE(dst_eid, at::kLong);
+  CHECK_DTYPE(src_eid, at::kLong);
+  TORCH_CHECK(dst_eid.numel() == scores_like.size(0) && src_eid.numel() == scores_like.size(0),
+              "dst_eid / src_eid must have one entry per edge");
+  TORCH_CHECK(num_heads == scores_like.size(1), "num_heads must equal the score width");
+  TORCH_CHECK(V.size(0) == scores_like.size(0) && V.size(1) == num_heads,
+              "V_val must be [E, num_heads, dh]");
+  TORCH_CHECK(num_heads <= 64, "at most 64 heads are supported");
+  for (const at::Tensor* t : {&V, &indptr, &dst_eid, &src_eid}) CHECK_SAME_DEVICE((*t), scores_like);
+}
+
+// forward_fused_attn (operators.cpp:285-333) -> [out_agg, attn, edge_mask].
+std::vector<at::Tensor> forward_fused_attn(at::Tensor input_feat, at::Tensor V_val, at::Tensor indptr,
+                                           at::Tensor indices, at::Tensor dst_eid,
+                                           at::Tensor src_eid, int64_t node_num, int64_t num_heads,
+                                           double negative_slope, double attn_drop) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(input_feat);
+  check_fused(input_feat, V_val, indptr, dst_eid, src_eid, num_heads);
+  TORCH_CHECK(node_num >= 0, "node_num must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(input_feat.device());
+  const int64_t E = input_feat.size(0), H = num_heads, dh = V_val.size(2);
+  auto attn = at::zeros({E, H}, input_feat.options());
+  auto out = at::zeros({node_num, H * dh}, input_feat.options());
+  // Dropout mask U[0,1) from torch's generator (the reference draws it with cuRAND).
+  auto edge_mask = at::rand({E, H}, input_feat.options());
+  const int st = fa_fused_attn_fwd_f32(
+      indptr.data_ptr<int32_t>(), num_segments(indptr), dst_eid.data_ptr<int64_t>(),
+      src_eid.data_ptr<int64_t>(), E, node_num, input_feat.data_ptr<float>(),
+      V_val.data_ptr<float>(), static_cast<int32_t>(H), static_cast<int32_t>(dh),
+      static_cast<float>(negative_slope), static_cast<float>(attn_drop),
+      edge_mask.data_ptr<float>(), attn.data_ptr<float>(), out.data_ptr<float>(),
+      stream_of(input_feat));
+  check_status(st, "forward_fused_attn");
+  debug_nan(out, "forward_fused_attn");
+  return {out, attn, edge_mask};
+}
+
+// backward_fused_attn (operators.cpp:513-565) -> [d_input, grad_V]; d_input is the
+// gradient with respect to the LeakyReLU output.
+std::vector<at::Tensor> backward_fused_attn(at::Tensor d_output, at::Tensor V_val, at::Tensor output,
+                                            at::Tensor edge_mask, at::Tensor indptr,
+                                            at::Tensor indices, at::Tensor dst_eid,
+                                            at::Tensor src_eid, int64_t node_num, int64_t num_heads,
+                                            double negative_slope, double attn_drop) {
+  CHECK_INPUT(indptr);
+  CHECK_INPUT(indices);
+  CHECK_INPUT(d_output);
+  CHECK_INPUT(output);
+  CHECK_INPUT(edge_mask);
+  (void)negative_slope;
+  check_fused(output, V_val, indptr, dst_eid, src_eid, num_heads);
+  CHECK_DTYPE(edge_mask, at::kFloat);
+  TORCH_CHECK(edge_mask.sizes() == output.sizes(), "edge_mask must match output");
+  CHECK_DIM(d_output, 2);
+  CHECK_DTYPE(d_output, at::kFloat);
+  TORCH_CHECK(d_output.size(1) == num_heads * V_val.size(2), "d_output must be [N, num_heads*dh]");
+  CHECK_SAME_DEVICE(d_output, output);
+  CHECK_SAME_DEVICE(edge_mask, output);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(output.device());
+  const int64_t E = output.size(0), H = num_heads, dh = V_val.size(2);
+  auto d_input = at::zeros({E, H}, output.options());
+  auto grad_V = at::zeros({E, H, dh}, output.options());
+  const int st = fa_fused_attn_bwd_f32(
+      indptr.data_ptr<int32_t>(), num_segments(indptr), dst_eid.data_ptr<int64_t>(),
+      src_eid.data_ptr<int64_t>(), E, d_output.size(0), node_num, d_output.data_ptr<float>(),
+      V_val.data_ptr<float>(), output.data_ptr<float>(), edge_mask.data_ptr<float>(),
+      static_cast<int32_t>(H), static_cast<int32_t>(dh), static_cast<float>(attn_drop),
+      d_input.data_ptr<float>(), grad_V.data_ptr<float>(), stream_of(output));
+  check_status(st, "backward_fused_attn");
+  debug_nan(d_input, "backward_fused_attn");
+  return {d_input, grad_V};
+}
+
+// ----------------------------------------------------------------------------------
+// Bookkeeping (utils.cu)
+// ----------------------------------------------------------------------------------
+// exclusive_sum (operators.cpp:580-586): int32 [n] -> int32 [n+1] = [0, cumsum].
+at::Tensor exclusive_sum(at::Tensor in_degs) {
+  CHECK_INPUT(in_degs);
+  CHECK_DTYPE(in_degs, at::kInt);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(in_degs.device());
+  const int64_t n = in_degs.numel();
+  auto out = at::empty({n + 1}, in_degs.options());
+  const size_t sb = fa_exclusive_sum_scratch_bytes(n);
+  auto scratch = at::empty({static_cast<int64_t>(sb)}, in_degs.options().dtype(at::kByte));
+  const int st = fa_exclusive_sum_i32(in_degs.data_ptr<int32_t>(), n, out.data_ptr<int32_t>(),
+                                      scratch.data_ptr(), sb, stream_of(in_degs));
+  check_status(st, "exclusive_sum");
+  return out;
+}
+
+// cal_deg (operators.cpp:588-595): int32 histogram of edges over [0, nodes_num).
+at::Tensor cal_deg(at::Tensor edges, int64_t nodes_num) {
+  CHECK_INPUT(edges);
+  CHECK_DTYPE(edges, at::kInt);
+  TORCH_CHECK(nodes_num >= 0, "nodes_num must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(edges.device());
+  auto deg = at::zeros({nodes_num}, edges.options());
+  const int st = fa_degree_count_i32(edges.data_ptr<int32_t>(), edges.numel(),
+                                     deg.data_ptr<int32_t>(), nodes_num, stream_of(edges));
+  check_status(st, "cal_deg");
+  return deg;
+}
+
+// getBalancedPtr (operators.cpp:597-604): int32 mask [n-1].
+at::Tensor getBalancedPtr(at::Tensor densePtr, int64_t threshold) {
+  CHECK_INPUT(densePtr);
+  CHECK_DTYPE(densePtr, at::kInt);
+  TORCH_CHECK(densePtr.numel() >= 1, "densePtr must hold at least one offset");
+  TORCH_CHECK(threshold != 0, "threshold must be non-zero");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(densePtr.device());
+  const int64_t n = densePtr.numel();
+  auto mask = at::zeros({n - 1}, densePtr.options());
+  const int st = fa_balance_mask_i32(densePtr.data_ptr<int32_t>(), n, static_cast<int32_t>(threshold),
+                                     mask.data_ptr<int32_t>(), stream_of(densePtr));
+  check_status(st, "getBalancedPtr");
+  return mask;
+}
+
+// ----------------------------------------------------------------------------------
+// Fused TGAT operators of this build (no reference counterpart)
+// ----------------------------------------------------------------------------------
+int64_t tgat_kspace(int64_t dn, int64_t de, int64_t dt_dim) {
+  return fa_tgat_kspace(static_cast<int32_t>(dn), static_cast<int32_t>(de), static_cast<int32_t>(dt_dim));
+}
+
+// int32 [n_dst+1] full-CSR offsets from dst-sorted int64 destination ids.
+at::Tensor rowptr_from_dst(at::Tensor dst, int64_t n_dst) {
+  CHECK_INPUT(dst);
+  CHECK_DTYPE(dst, at::kLong);
+  CHECK_DIM(dst, 1);
+  TORCH_CHECK(n_dst >= 0, "n_dst must be >= 0");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(dst.device());
+  auto rowptr = at::empty({n_dst + 1}, dst.options().dtype(at::kInt));
+  const int st = fa_rowptr_from_sorted_dst_i64(dst.data_ptr<int64_t>(), dst.numel(), n_dst,
+                                               rowptr.data_ptr<int32_t>(), stream_of(dst));
+  check_status(st, "rowptr_from_dst");
+  return rowptr;
+}
+
+void check_table(const at::Tensor& t, const char* name) {
+  CHECK_CUDA(t);
+  TORCH_CHECK(t.dim() == 2, name, " must be 2-D");
+  TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+  TORCH_CHECK(t.size(1) == 0 || t.stride(1) == 1, name, " rows must be contiguous");
+}
+
+const int64_t* opt_index(const std::optional<at::Tensor>& idx, int64_t n, const at::Tensor& ref,
+                         const char* name) {
+  if (!idx.has_value()) return nullptr;
+  const at::Tensor& t = *idx;
+  CHECK_INPUT(t);
+  CHECK_DTYPE(t, at::kLong);
+  TORCH_CHECK(t.numel() == n, name, " must have one entry per edge");
+  CHECK_SAME_DEVICE(t, ref);
+  return t.data_ptr<int64_t>();
+}
+
+fa_tgat_graph make_graph(const at::Tensor& rowptr, const at::Tensor& node_tab,
+                         const std::optional<at::Tensor>& node_idx, const at::Tensor& edge_tab,
+                         const std::optional<at::Tensor>& edge_idx, const at::Tensor& dt,
+                         const at::Tensor& time_w, const at::Tensor& time_b) {
+  CHECK_INPUT(rowptr);
+  CHECK_DTYPE(rowptr, at::kInt);
+  CHECK_INPUT(dt);
+  CHECK_DTYPE(dt, at::kFloat);
+  CHECK_INPUT(time_w);
+  CHECK_INPUT(time_b);
+  CHECK_DTYPE(time_w, at::kFloat);
+  CHECK_DTYPE(time_b, at::kFloat);
+  check_table(node_tab, "node_tab");
+  check_table(edge_tab, "edge_tab");
+  TORCH_CHECK(time_w.numel() == time_b.numel(), "time_w and time_b must have the same length");
+  const int64_t E = dt.numel();
+  for (const at::Tensor* t : {&node_tab, &edge_tab, &dt, &time_w, &time_b})
+    CHECK_SAME_DEVICE((*t), rowptr);
+  fa_tgat_graph g{};
+  g.n_dst = rowptr.numel() - 1;
+  g.n_edges = E;
+  g.rowptr = rowptr.data_ptr<int32_t>();
+  g.node_tab = node_tab.data_ptr<float>();
+  g.ld_node = node_tab.size(1) > 0 ? node_tab.stride(0) : 0;
+  g.n_node = node_tab.size(0);
+  g.dn = static_cast<int32_t>(node_tab.size(1));
+  g.node_idx = opt_index(node_idx, E, rowptr, "node_idx");
+  g.edge_tab = edge_tab.data_ptr<float>();
+  g.ld_edge = edge_tab.size(1) > 0 ? edge_tab.stride(0) : 0;
+  g.n_edge_rows = edge_tab.size(0);
+  g.de = static_cast<int32_t>(edge_tab.size(1));
+  g.edge_idx = opt_index(edge_idx, E, rowptr, "edge_idx");
+  g.dt = dt.data_ptr<float>();
+  g.time_w = time_w.data_ptr<float>();
+  g.time_b = time_b.data_ptr<float>();
+  g.dt_dim = static_cast<int32_t>(time_w.numel());
+  TORCH_CHECK(g.n_dst >= 0, "rowptr must hold n_dst+1 offsets");
+  return g;
+}
+
+void check_kspace(const at::Tensor& t, const fa_tgat_graph& g, int64_t heads, const char* name) {
+  CHECK_INPUT(t);
+  CHECK_DTYPE(t, at::kFloat);
+  const int64_t kp = fa_tgat_kspace(g.dn, g.de, g.dt_dim);
+  TORCH_CHECK(t.dim() == 3 && t.size(0) == heads && t.size(1) == g.n_dst && t.size(2) == kp, name,
+              " must be [heads, n_dst, ", kp, "]");
+}
+
+// -> [xbar [H, N, Kp], scores [E, H], stats [N, H, 2]]
+std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
+                                      std::optional<at::Tensor> node_idx, at::Tensor edge_tab,
+                                      std::optional<at::Tensor> edge_idx, at::Tensor dt,
+                                      at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
+                                      double slope, std::optional<at::Tensor> drop) {
+  fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
+  const int64_t H = qt.size(0);
+  check_kspace(qt, g, H, "qt");
+  const float* dptr = nullptr;
+  if (drop.has_value()) {
+    CHECK_INPUT((*drop));
+    CHECK_DTYPE((*drop), at::kFloat);
+    TORCH_CHECK(drop->dim() == 2 && drop->size(0) == g.n_edges && drop->size(1) == H,
+                "drop must be [E, heads]");
+    dptr = drop->data_ptr<float>();
+  }
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(qt.device());
+  auto xbar = at::empty_like(qt);
+  auto scores = at::empty({g.n_edges, H}, qt.options());
+  auto stats = at::empty({g.n_dst, H, 2}, qt.options());
+  const int st = fa_tgat_attn_fwd_f32(&g, static_cast<int32_t>(H), qt.data_ptr<float>(),
+                                      qt.stride(0), static_cast<float>(slope), dptr,
+                                      xbar.data_ptr<float>(), xbar.stride(0),
+                                      scores.data_ptr<float>(), stats.data_ptr<float>(),
+                                      stream_of(qt));
+  check_status(st, "tgat_attn_fwd");
+  return {xbar, scores, stats};
+}
+
+// -> [dqt, d_node (or empty), d_time_w, d_time_b]
+std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
+                                      std::optional<at::Tensor> node_idx, at::Tensor edge_tab,
+                                      std::optional<at::Tensor> edge_idx, at::Tensor dt,
+                                      at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
+                                      double slope, std::optional<at::Tensor> drop,
+                                      at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
+                                      bool need_d_node) {
+  fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
+  const int64_t H = qt.size(0);
+  check_kspace(qt, g, H, "qt");
+  check_kspace(dxbar, g, H, "dxbar");
+  CHECK_INPUT(scores);
+  CHECK_INPUT(stats);
+  TORCH_CHECK(scores.numel() == g.n_edges * H && stats.numel() == g.n_dst * H * 2,
+              "scores / stats do not match the graph");
+  const float* dptr = nullptr;
+  if (drop.has_value()) {
+    CHECK_INPUT((*drop));
+    CHECK_DTYPE((*drop), at::kFloat);
+    TORCH_CHECK(drop->numel() == g.n_edges * H, "drop must be [E, heads]");
+    dptr = drop->data_ptr<float>();
+  }
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(qt.device());
+  auto dqt = at::empty_like(qt);
+  at::Tensor d_node;
+  if (need_d_node) d_node = at::empty({g.n_edges, g.dn}, qt.options());
+  auto d_tw = at::empty({g.dt_dim}, qt.options());
+  auto d_tb = at::empty({g.dt_dim}, qt.options());
+  const size_t sb = fa_tgat_attn_bwd_scratch_bytes(g.n_dst, g.dt_dim);
+  auto scratch = at::empty({static_cast<int64_t>(sb)}, qt.options().dtype(at::kByte));
+  const int st = fa_tgat_attn_bwd_f32(
+      &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(0), static_cast<float>(slope),
+      dptr, scores.data_ptr<float>(), stats.data_ptr<float>(), dxbar.data_ptr<float>(),
+      dxbar.stride(0), dqt.data_ptr<float>(), dqt.stride(0),
+      need_d_node && g.n_edges > 0 && g.dn > 0 ? d_node.data_ptr<float>() : nullptr,
+      need_d_node ? g.dn : 0, d_tw.data_ptr<float>(), d_tb.data_ptr<float>(), scratch.data_ptr(),
+      sb, stream_of(qt));
+  check_status(st, "tgat_attn_bwd");
+  return {dqt, need_d_node ? d_node : at::Tensor(), d_tw, d_tb};
+}
+
+at::Tensor tgat_attn_weights(at::Tensor dst, at::Tensor scores, at::Tensor stats) {
+  CHECK_INPUT(dst);
+  CHECK_INPUT(scores);
+  CHECK_INPUT(stats);
+  CHECK_DTYPE(dst, at::kLong);
+  CHECK_DTYPE(scores, at::kFloat);
+  CHECK_DTYPE(stats, at::kFloat);
+  CHECK_DIM(scores, 2);
+  TORCH_CHECK(dst.numel() == scores.size(0), "dst must have one entry per edge");
+  TORCH_CHECK(stats.dim() == 3 && stats.size(1) == scores.size(1) && stats.size(2) == 2,
+              "stats must be [n_dst, heads, 2]");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+  auto att = at::empty_like(scores);
+  const int st = fa_tgat_attn_weights_f32(dst.data_ptr<int64_t>(), scores.size(0), stats.size(0),
+                                          static_cast<int32_t>(scores.size(1)),
+                                          scores.data_ptr<float>(), stats.data_ptr<float>(),
+                                          att.data_ptr<float>(), stream_of(scores));
+  check_status(st, "tgat_attn_weights");
+  return att;
+}
+
+at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n) {
+  check_table(tab, "tab");
+  const int64_t* ip = nullptr;
+  if (idx.has_value()) {
+    CHECK_INPUT((*idx));
+    CHECK_DTYPE((*idx), at::kLong);
+    n = idx->numel();
+    ip = idx->data_ptr<int64_t>();
+  }
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(tab.device());
+  auto out = at::empty({n, tab.size(1)}, tab.options());
+  const int st = fa_gather_rows_f32(tab.data_ptr<float>(), tab.size(1) > 0 ? tab.stride(0) : 0,
+                                    tab.size(0), ip, n, static_cast<int32_t>(tab.size(1)),
+                                    out.data_ptr<float>(), tab.size(1), stream_of(tab));
+  check_status(st, "gather_rows");
+  return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(fastAgg, m) {
+  namespace py = pybind11;
+  m.doc() = "MI355X-native FAST temporal-attention aggregation operators (gfx950 HIP kernels)";
+  // utilities
+  m.def("cal_deg", &cal_deg, "cal_deg (HIP)", py::arg("edges"), py::arg("nodes_num"));
+  m.def("exclusive_sum", &exclusive_sum, "exclusive_sum (HIP)", py::arg("in_degs"));
+  m.def("getBalancedPtr", &getBalancedPtr, "balanced_ptr (HIP)", py::arg("densePtr"),
+        py::arg("threshold"));
+  // global-based
+  m.def("forward_tgat", &forward_tgat, "forward_tgat (HIP)", py::arg("src_edges"),
+        py::arg("dst_edges"), py::arg("input_feat"), py::arg("dst_num"), py::arg("aggNodePB"),
+        py::arg("aggFeat"));
+  m.def("backward_tgat", &backward_tgat, "backward_tgat (HIP)", py::arg("src_edges"),
+        py::arg("dst_edges"), py::arg("d_input"), py::arg("src_num"), py::arg("aggNodePB"),
+        py::arg("aggFeat"));
+  m.def("forward_edge_softmax", &forward_edge_softmax, "esm (HIP)", py::arg("indptr"),
+        py::arg("indices"), py::arg("input_feat"), py::arg("node_num_per_block"),
+        py::arg("num_heads"));
+  m.def("backward_edge_softmax", &backward_edge_softmax, "esm (HIP)", py::arg("indptr"),
+        py::arg("indices"), py::arg("d_output"), py::arg("output"), py::arg("node_num_per_block"),
+        py::arg("num_heads"));
+  // csr-based
+  m.def("forward_tgat_shd", &forward_tgat_shd, "forward_tgat_shd (HIP)", py::arg("indptr"),
+        py::arg("indices"), py::arg("src_edges"), py::arg("dst_edges"), py::arg("input_feat"),
+        py::arg("dst_nodes"), py::arg("aggNodePB"), py::arg("aggFeat"));
+  m.def("backward_tgat_shd", &backward_tgat_shd, "backward_tgat_shd (HIP)", py::arg("indptr"),
+        py::arg("indices"), py::arg("dst_edges"), py::arg("src_edges"), py::arg("d_input"),
+        py::arg("src_nodes"), py::arg("aggNodePB"), py::arg("aggFeat"));
+  m.def("forward_balanced_edge_softmax", &forward_balanced_edge_softmax, "esm_csr (HIP)",
+        py::arg("indptr"), py::arg("indices"), py::arg("input_feat"),
+        py::arg("edge_num_per_block"), py::arg("reduce_size"));
+  m.def("backward_balanced_edge_softmax", &backward_balanced_edge_softmax, "esm_csr (HIP)",
+        py::arg("indptr"), py::arg("indices"), py::arg("d_output"), py::arg("output"),
+        py::arg("node_num_per_block"), py::arg("reduce_size"));
+  m.def("forward_csr_edge_softmax", &forward_csr_edge_softmax, "esm_online (HIP)",
+        py::arg("indptr"), py::arg("indices"), py::arg("input_feat"),
+        py::arg("node_num_per_block"), py::arg("reduce_size"));
+  m.def("backward_csr_edge_softmax", &backward_csr_edge_softmax, "esm_online (HIP)",
+        py::arg("indptr"), py::arg("indices"), py::arg("d_output"), py::arg("output"),
+        py::arg("node_num_per_block"), py::arg("reduce_size"));
+  // fused
+  m.def("forward_fused_attn", &forward_fused_attn, "fused attn (HIP)", py::arg("input_feat"),
+        py::arg("V_val"), py::arg("indptr"), py::arg("indices"), py::arg("dst_eid"),
+        py::arg("src_eid"), py::arg("node_num"), py::arg("num_heads"), py::arg("negative_slope"),
+        py::arg("attn_drop"));
+  m.def("backward_fused_attn", &backward_fused_attn, "fused attn (HIP)", py::arg("d_output"),
+        py::arg("V_val"), py::arg("output"), py::arg("edge_mask"), py::arg("indptr"),
+        py::arg("indices"), py::arg("dst_eid"), py::arg("src_eid"), py::arg("node_num"),
+        py::arg("num_heads"), py::arg("negative_slope"), py::arg("attn_drop"));
+  // fused TGAT operators of this build
+  m.def("tgat_kspace", &tgat_kspace, "padded K-space width of one key/value input row",
+        py::arg("dn"), py::arg("de"), py::arg("dt_dim"));
+  m.def("rowptr_from_dst", &rowptr_from_dst, "full-CSR offsets from dst-sorted edge ids",
+        py::arg("dst"), py::arg("n_dst"));
+  m.def("tgat_attn_fwd", &tgat_attn_fwd,
+        "fused gather + time encoding + score + segment softmax + aggregation (forward)",
+        py::arg("rowptr"), py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"),
+        py::arg("edge_idx"), py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"),
+        py::arg("slope"), py::arg("drop"));
+  m.def("tgat_attn_bwd", &tgat_attn_bwd, "backward of tgat_attn_fwd", py::arg("rowptr"),
+        py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"), py::arg("edge_idx"),
+        py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"), py::arg("slope"),
+        py::arg("drop"), py::arg("scores"), py::arg("stats"), py::arg("dxbar"),
+        py::arg("need_d_node"));
+  m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
+        py::arg("dst"), py::arg("scores"), py::arg("stats"));
+  m.def("gather_rows", &gather_rows, "row gather tab[idx]", py::arg("tab"), py::arg("idx"),
+        py::arg("n"));
+  m.attr("abi_version") = fa_abi_version();
+}

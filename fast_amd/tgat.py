@@ -1,0 +1,436 @@
+"""TGAT temporal attention on the fused gfx950 kernels.
+
+``TransfomerAttentionLayer`` has the constructor, parameters (names, shapes, creation
+order, initialisation) and ``forward(b, _layers, _hist)`` of the reference layer
+(layers.py:53-240, TGAT/TGN branch) and computes the same function. Its data path differs:
+
+  reference                                   this layer
+  K = w_k(cat[h_src, f, cos(w dt+b)])  [E,D]  qt[h,v] = Q[v,h] W_k[h] (+ b_k column)   [H,N,Kp]
+  V = w_v(cat[...])                    [E,D]  xbar[h,v] = sum_e a'[e,h] x_e (one kernel) [H,N,Kp]
+  score = sum(Q[dst]*K), softmax, V*att,      out[v,h] = W_v[h] xbar[h,v] (+ b_v * sum a')
+  update_all(copy_u, sum)
+
+so the K/V projections run over the N destinations instead of the E edges, and the
+neighbour gather, time encoding, scoring, segment softmax and weighted reduction happen in
+one pass over the gathered rows x_e (never written to memory).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import fastAgg
+
+
+# ---------------------------------------------------------------------------------------
+# Message-flow-graph block
+# ---------------------------------------------------------------------------------------
+class Block:
+    """Destination-sorted bipartite block with the subset of the DGL block API that the
+    TGAT layer uses (``num_dst_nodes``, ``num_src_nodes``, ``num_edges``, ``edges``,
+    ``srcdata``, ``dstdata``, ``edata``).
+
+    Layout contract of the FAST sampler (sampler_core.cpp:159-181, 185-456; utils.py:67-87):
+    source nodes ``0..N-1`` are the destinations themselves and edge ``e`` comes from source
+    node ``N + e``; edges are grouped by ascending destination.
+
+    Node features come either from ``srcdata['h']`` (dense, one row per source node) or
+    from ``node_table`` gathered by ``srcdata['ID']``; edge features from ``edata['f']`` or
+    ``edge_table`` gathered by ``edata['ID']``. ``indptr`` optionally holds the sampler's
+    compressed int32 CSR (``cntE``).
+    """
+
+    def __init__(self, src: torch.Tensor, dst: torch.Tensor, num_src: int, num_dst: int,
+                 indptr: Optional[torch.Tensor] = None):
+        self._src = src
+        self._dst = dst
+        self._num_src = int(num_src)
+        self._num_dst = int(num_dst)
+        self.indptr = indptr
+        self.srcdata: dict = {}
+        self.dstdata: dict = {}
+        self.edata: dict = {}
+        self.node_table: Optional[torch.Tensor] = None
+        self.edge_table: Optional[torch.Tensor] = None
+        self._rowptr: Optional[torch.Tensor] = None
+
+    @classmethod
+    def from_fanout(cls, num_dst: int, degrees: torch.Tensor) -> "Block":
+        """Block in the sampler layout for per-destination degrees (int64 [num_dst])."""
+        dev = degrees.device
+        dst = torch.repeat_interleave(torch.arange(num_dst, device=dev), degrees)
+        E = int(dst.numel())
+        src = torch.arange(num_dst, num_dst + E, device=dev)
+        counts = degrees[degrees > 0].to(torch.int64)
+        indptr = torch.zeros(counts.numel() + 1, dtype=torch.int32, device=dev)
+        if counts.numel():
+            indptr[1:] = torch.cumsum(counts, 0).to(torch.int32)
+        return cls(src, dst, num_dst + E, num_dst, indptr)
+
+    def num_dst_nodes(self) -> int:
+        return self._num_dst
+
+    def num_src_nodes(self) -> int:
+        return self._num_src
+
+    def num_edges(self) -> int:
+        return int(self._dst.numel())
+
+    def edges(self):
+        return self._src, self._dst
+
+    @property
+    def device(self) -> torch.device:
+        return self._dst.device
+
+    def rowptr(self) -> torch.Tensor:
+        """int32 [N+1] offsets of every destination's edges (zero-degree ones included)."""
+        if self._rowptr is None:
+            self._rowptr = fastAgg.rowptr_from_dst(self._dst, self._num_dst)
+        return self._rowptr
+
+    def to(self, device) -> "Block":
+        def mv(t):
+            return t.to(device) if isinstance(t, torch.Tensor) else t
+        b = Block(mv(self._src), mv(self._dst), self._num_src, self._num_dst, mv(self.indptr))
+        b.srcdata = {k: mv(v) for k, v in self.srcdata.items()}
+        b.dstdata = {k: mv(v) for k, v in self.dstdata.items()}
+        b.edata = {k: mv(v) for k, v in self.edata.items()}
+        b.node_table = mv(self.node_table)
+        b.edge_table = mv(self.edge_table)
+        return b
+
+    # -- feature access -----------------------------------------------------------------
+    def dst_node_feats(self) -> Optional[torch.Tensor]:
+        N = self._num_dst
+        if "h" in self.srcdata:
+            return self.srcdata["h"][:N]
+        if self.node_table is not None:
+            ids = self.srcdata["ID"][:N]
+            return fastAgg.gather_rows(self.node_table, ids, N)
+        return None
+
+    def src_node_source(self):
+        """(table, per-edge row index or None) of the node rows feeding the edges."""
+        N = self._num_dst
+        if "h" in self.srcdata:
+            return self.srcdata["h"][N:], None
+        if self.node_table is not None:
+            return self.node_table, self.srcdata["ID"][N:]
+        return None, None
+
+    def edge_source(self):
+        if "f" in self.edata:
+            return self.edata["f"], None
+        if self.edge_table is not None:
+            return self.edge_table, self.edata["ID"]
+        return None, None
+
+
+# ---------------------------------------------------------------------------------------
+# Time encoding
+# ---------------------------------------------------------------------------------------
+def time_encoding_weight(dim: int) -> torch.Tensor:
+    """w_j = 1 / 10**linspace(0, 9, dim) in float32, shape [dim, 1] (layers.py:14)."""
+    return torch.from_numpy(1 / 10 ** np.linspace(0, 9, dim, dtype=np.float32)).reshape(dim, -1)
+
+
+class TimeEncode(torch.nn.Module):
+    """cos(w * t + b) with w, b trainable (layers.py:8-29). The argument is evaluated as a
+    rounded product followed by a rounded sum, the same as the fused kernels."""
+
+    def __init__(self, dim: int):
+        super().__init__()
+        self.dim = dim
+        self.w = torch.nn.Linear(1, dim)
+        self.w.weight = torch.nn.Parameter(time_encoding_weight(dim))
+        self.w.bias = torch.nn.Parameter(torch.zeros(dim))
+
+    def forward(self, t: torch.Tensor) -> torch.Tensor:
+        return torch.cos(t.reshape(-1, 1) * self.w.weight.view(1, -1) + self.w.bias)
+
+
+# ---------------------------------------------------------------------------------------
+# K-space helpers
+# ---------------------------------------------------------------------------------------
+def kspace_width(dn: int, de: int, dt: int) -> int:
+    return int(fastAgg.tgat_kspace(dn, de, dt))
+
+
+def to_kspace(W: torch.Tensor, b: torch.Tensor, dn: int, de: int, dt: int) -> torch.Tensor:
+    """[D, dn+de+dt] weight and [D] bias -> [D, Kp] with each part padded to a multiple of
+    4 columns, the bias at column Kb and zeros after it (the layout the kernels use)."""
+    pieces = []
+    off = 0
+    for d in (dn, de, dt):
+        if d:
+            pieces.append(W[:, off:off + d])
+            off += d
+        pad = (-d) % 4
+        if pad:
+            pieces.append(W.new_zeros(W.shape[0], pad))
+    pieces.append(b[:, None])
+    pieces.append(W.new_zeros(W.shape[0], 3))
+    return torch.cat(pieces, dim=1)
+
+
+def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, heads: int,
+                       node_idx: bool, edge_idx: bool, d_node: bool = False) -> dict:
+    """Algorithmic HBM bytes of one launch of the fused forward / backward kernel (float32):
+    every byte the kernel must read or write once, gathered rows counted once per use.
+
+    per edge : node id (8, when gathered) + edge id (8, when gathered) + dt (4)
+               + node row (4*dn) + edge row (4*de) + score (4*heads, written / read)
+               [+ d_node row (4*dn) written in backward when requested]
+    per dst  : forward  qt read + xbar written (2 * 4*heads*Kp) + stats written (8*heads)
+               backward qt, dxbar read + dqt written (3 * 4*heads*Kp) + stats read (8*heads)
+    plus the row offsets 4*(n_dst+1) and the time parameters 8*dt."""
+    kp = kspace_width(dn, de, dt)
+    edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + 4 * dn + 4 * de
+    common = 4 * (n_dst + 1) + 8 * dt
+    fwd = common + n_edges * (edge_in + 4 * heads) + n_dst * (2 * 4 * heads * kp + 8 * heads)
+    bwd = (common + n_edges * (edge_in + 4 * heads + (4 * dn if d_node else 0))
+           + n_dst * (3 * 4 * heads * kp + 8 * heads))
+    return {"fwd": fwd, "bwd": bwd}
+
+
+class KernelTimer:
+    """Records a HIP event pair around every fused-kernel call on torch's current stream
+    (the stream the kernels are enqueued on) with the launch's algorithmic bytes."""
+
+    def __init__(self):
+        self.records = []   # (name, start_event, end_event, bytes)
+        self.enabled = True
+
+    def begin(self):
+        if not self.enabled:
+            return None
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def end(self, name, start, nbytes):
+        if start is None:
+            return
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.records.append((name, start, ev, nbytes))
+
+    def reset(self):
+        self.records = []
+
+    def summary(self) -> dict:
+        """Per kernel: launches, total ms, total algorithmic bytes, GB/s (call after a
+        device synchronisation)."""
+        out = {}
+        for name, s, e, nb in self.records:
+            d = out.setdefault(name, {"launches": 0, "ms": 0.0, "bytes": 0})
+            d["launches"] += 1
+            d["ms"] += s.elapsed_time(e)
+            d["bytes"] += nb
+        for d in out.values():
+            d["GB/s"] = d["bytes"] / (d["ms"] * 1e-3) / 1e9 if d["ms"] > 0 else 0.0
+            d["avg_us"] = 1e3 * d["ms"] / max(1, d["launches"])
+        return out
+
+
+timer: Optional[KernelTimer] = None  # set by a benchmark to time the fused kernels
+
+
+class _Graph:
+    """Non-differentiable per-block operands of the fused kernels."""
+
+    __slots__ = ("rowptr", "node_idx", "edge_tab", "edge_idx", "dt")
+
+    def __init__(self, rowptr, node_idx, edge_tab, edge_idx, dt):
+        self.rowptr = rowptr
+        self.node_idx = node_idx
+        self.edge_tab = edge_tab
+        self.edge_idx = edge_idx
+        self.dt = dt
+
+
+class TgatAttention(torch.autograd.Function):
+    """xbar = fused gather/time-encode/score/softmax/reduce (see module docstring).
+
+    Differentiable inputs: ``qt`` [H,N,Kp], ``time_w`` [Dt], ``time_b`` [Dt] and
+    ``node_src`` (the node rows feeding the edges: one row per edge when ``node_idx`` is
+    None, else a table gathered by ``node_idx``)."""
+
+    @staticmethod
+    def forward(ctx, qt, time_w, time_b, node_src, g: _Graph, slope: float, drop):
+        t0 = timer.begin() if timer is not None else None
+        xbar, scores, stats = fastAgg.tgat_attn_fwd(g.rowptr, node_src, g.node_idx, g.edge_tab,
+                                                    g.edge_idx, g.dt, time_w, time_b, qt,
+                                                    float(slope), drop)
+        if t0 is not None:
+            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
+                                    g.node_idx is not None, g.edge_idx is not None)["fwd"]
+            timer.end("tgat_fwd", t0, nb)
+        ctx.g = g
+        ctx.slope = float(slope)
+        ctx.has_drop = drop is not None
+        saved = [qt, time_w, time_b, node_src, scores, stats]
+        if drop is not None:
+            saved.append(drop)
+        ctx.save_for_backward(*saved)
+        return xbar
+
+    @staticmethod
+    def backward(ctx, dxbar):
+        saved = ctx.saved_tensors
+        qt, time_w, time_b, node_src, scores, stats = saved[:6]
+        drop = saved[6] if ctx.has_drop else None
+        g = ctx.g
+        need_node = ctx.needs_input_grad[3] and node_src.shape[1] > 0
+        dxbar = dxbar.contiguous()
+        t0 = timer.begin() if timer is not None else None
+        dqt, d_node, d_tw, d_tb = fastAgg.tgat_attn_bwd(g.rowptr, node_src, g.node_idx,
+                                                        g.edge_tab, g.edge_idx, g.dt, time_w,
+                                                        time_b, qt, ctx.slope, drop, scores,
+                                                        stats, dxbar, need_node)
+        if t0 is not None:
+            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
+                                    g.node_idx is not None, g.edge_idx is not None,
+                                    need_node)["bwd"]
+            timer.end("tgat_bwd", t0, nb)
+        d_src = None
+        if need_node:
+            if g.node_idx is None:
+                d_src = d_node
+            else:
+                d_src = torch.zeros_like(node_src).index_add_(0, g.node_idx, d_node)
+        return dqt, d_tw, d_tb, d_src, None, None, None
+
+
+# ---------------------------------------------------------------------------------------
+# Layer
+# ---------------------------------------------------------------------------------------
+class TransfomerAttentionLayer(torch.nn.Module):
+    """Temporal graph attention layer (layers.py:53-240), TGAT/TGN branch, on the fused
+    kernels. The constructor creates the same modules in the same order as the reference,
+    so a given seed yields the same initial weights and the state dicts are interchangeable.
+    """
+
+    def __init__(self, dim_node_feat, dim_edge_feat, dim_time, num_head, dropout, att_dropout,
+                 dim_out, combined=False):
+        super().__init__()
+        if combined:
+            raise NotImplementedError("the 'combined' projection variant is not built")
+        if dim_out % num_head:
+            raise ValueError("dim_out must be divisible by num_head")
+        self.num_head = num_head
+        self.dim_node_feat = dim_node_feat
+        self.dim_edge_feat = dim_edge_feat
+        self.dim_time = dim_time
+        self.dim_out = dim_out
+        self.dropout = torch.nn.Dropout(dropout)
+        self.att_dropout = torch.nn.Dropout(att_dropout)
+        self.negative_slope = 0.2
+        self.att_act = torch.nn.LeakyReLU(self.negative_slope)
+        self.combined = combined
+        if dim_time > 0:
+            self.time_enc = TimeEncode(dim_time)
+        if dim_node_feat + dim_time > 0:
+            self.w_q = torch.nn.Linear(dim_node_feat + dim_time, dim_out)
+        self.w_k = torch.nn.Linear(dim_node_feat + dim_edge_feat + dim_time, dim_out)
+        self.w_v = torch.nn.Linear(dim_node_feat + dim_edge_feat + dim_time, dim_out)
+        self.w_out = torch.nn.Linear(dim_node_feat + dim_out, dim_out)
+        self.layer_norm = torch.nn.LayerNorm(dim_out)
+
+    def _queries(self, hdst: Optional[torch.Tensor], N: int, device) -> torch.Tensor:
+        Dn, Dt, D = self.dim_node_feat, self.dim_time, self.dim_out
+        if Dn == 0 and Dt == 0:  # layers.py:137-140
+            return torch.ones(N, D, device=device)
+        Wq, bq = self.w_q.weight, self.w_q.bias
+        bias = bq
+        if Dt > 0:
+            # time encoding of dt = 0 for every destination (layers.py:109-110): cos(b)
+            zt = torch.cos(self.time_enc.w.bias)
+            bias = bq + torch.mv(Wq[:, Dn:], zt)
+        if Dn > 0:
+            return F.linear(hdst, Wq[:, :Dn], bias)
+        return bias.expand(N, D)
+
+    def forward(self, b: Block, _layers: int = 0, _hist: int = 0) -> torch.Tensor:
+        drop = None
+        p = self.att_dropout.p
+        if self.training and p > 0 and b.num_edges() > 0:
+            drop = torch.empty(b.num_edges(), self.num_head, device=b.device)
+            drop.bernoulli_(1 - p).div_(1 - p)
+        return self.attend(b, drop)
+
+    def attend(self, b: Block, drop: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The layer with an explicit attention-dropout multiplier ``drop`` [E, heads]
+        (0 or 1/(1-p) per entry; None = no attention dropout)."""
+        Dn, De, Dt = self.dim_node_feat, self.dim_edge_feat, self.dim_time
+        H, D = self.num_head, self.dim_out
+        dh = D // H
+        N, E = b.num_dst_nodes(), b.num_edges()
+        dev = b.device
+        if E == 0:  # layers.py:101-102
+            return torch.zeros((N, D), device=dev)
+        hdst = b.dst_node_feats() if Dn > 0 else None
+        Q = self._queries(hdst, N, dev)
+        kp = kspace_width(Dn, De, Dt)
+        wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt)
+        qt = torch.bmm(Q.view(N, H, dh).transpose(0, 1), wk.view(H, dh, kp))
+
+        node_src, node_idx = b.src_node_source() if Dn > 0 else (None, None)
+        edge_tab, edge_idx = b.edge_source() if De > 0 else (None, None)
+        if node_src is None:
+            node_src = torch.empty(E, 0, device=dev)
+        if edge_tab is None:
+            edge_tab = torch.empty(E, 0, device=dev)
+        elif edge_tab.requires_grad:
+            raise NotImplementedError("gradients with respect to edge features are not built")
+        if Dt > 0:
+            tw = self.time_enc.w.weight.view(-1)
+            tb = self.time_enc.w.bias
+            dt = b.edata["dt"]
+        else:
+            tw = tb = torch.empty(0, device=dev)
+            dt = torch.zeros(E, device=dev)
+        g = _Graph(b.rowptr(), node_idx, edge_tab, edge_idx, dt)
+        xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop)
+
+        wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt)
+        out = torch.bmm(xbar, wv.view(H, dh, kp).transpose(1, 2).contiguous())  # [H, N, dh]
+        agg = out.transpose(0, 1).reshape(N, D)
+        Wo = self.w_out.weight
+        if Dn > 0:
+            rst = torch.addmm(F.linear(hdst, Wo[:, D:], self.w_out.bias), agg, Wo[:, :D].t())
+        else:
+            rst = F.linear(agg, Wo, self.w_out.bias)
+        rst = F.relu(self.dropout(rst))
+        return self.layer_norm(rst)
+
+
+class TGATEncoder(torch.nn.Module):
+    """Stack of temporal attention layers fed bottom-up (modules.py:29-35, 48-64): the
+    output of layer l becomes ``srcdata['h']`` of the block of layer l+1."""
+
+    def __init__(self, dim_node, dim_edge, dim_time, num_head, dim_out, num_layers=2,
+                 dropout=0.1, att_dropout=0.1):
+        super().__init__()
+        self.layers = torch.nn.ModuleDict()
+        self.layers["l0h0"] = TransfomerAttentionLayer(dim_node, dim_edge, dim_time, num_head,
+                                                       dropout, att_dropout, dim_out)
+        for l in range(1, num_layers):
+            self.layers[f"l{l}h0"] = TransfomerAttentionLayer(dim_out, dim_edge, dim_time,
+                                                              num_head, dropout, att_dropout,
+                                                              dim_out)
+        self.num_layers = num_layers
+
+    def forward(self, blocks) -> torch.Tensor:
+        rst = None
+        for l in range(self.num_layers):
+            rst = self.layers[f"l{l}h0"](blocks[l], l, 0)
+            if l != self.num_layers - 1:
+                blocks[l + 1].srcdata["h"] = rst
+        return rst

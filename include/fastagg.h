@@ -1,0 +1,235 @@
+/*
+ * fastagg.h - C ABI of the MI355X (gfx950) temporal-attention aggregation library
+ * (libfastagg_hip.so).
+ *
+ * Every entry point:
+ *   - takes device pointers, element counts, leading dimensions (in elements) and a
+ *     hipStream_t; no torch types cross this boundary;
+ *   - enqueues its kernels on `stream` and returns without synchronising;
+ *   - allocates nothing: scratch, when needed, is passed in by the caller and its size is
+ *     given by the matching *_scratch_bytes() query;
+ *   - returns FA_OK (0), a negative FA_E* argument error, or a positive hipError_t from
+ *     the launch.
+ *
+ * Index conventions follow the FAST reference (getFastAgg/cuda_operators):
+ *   indptr / CSR offsets are int32, per-edge node ids are int64, features are row-major.
+ *
+ * "Segment" = the run of edges that share one destination node in a CSR over edges
+ * sorted by destination ("cntE" from getSamplerCore/sampler_core.cpp:384-409).
+ */
+#ifndef FASTAGG_H
+#define FASTAGG_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FA_OK = 0,
+  FA_EINVAL = -1,       /* bad size, null pointer or inconsistent dimensions */
+  FA_EUNSUPPORTED = -2, /* shape outside what the kernels are built for (e.g. heads) */
+  FA_EALIGN = -3,       /* pointer or leading dimension not 16-byte aligned */
+  FA_ESCRATCH = -4      /* caller scratch too small */
+};
+
+/* Human-readable text for a status returned by any entry point. */
+const char* fa_status_string(int status);
+/* Library ABI version (major*100 + minor). */
+int fa_abi_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * Segment bookkeeping (bit-exact integer work)
+ * ------------------------------------------------------------------------------- */
+
+/* out[0] = 0, out[i+1] = out[i] + in[i] for i < n (int32 wrap-around), n+1 outputs.
+ * Replaces exclusive_sum_cuda (getFastAgg/cuda_operators/utils.cu:16-40) and the
+ * binding fastAgg.exclusive_sum (operators.cpp:580-586). */
+size_t fa_exclusive_sum_scratch_bytes(int64_t n);
+int fa_exclusive_sum_i32(const int32_t* in, int64_t n, int32_t* out, void* scratch,
+                         size_t scratch_bytes, hipStream_t stream);
+
+/* deg[ids[i]] += 1 for every i with 0 <= ids[i] < n_nodes; deg must be zeroed by the
+ * caller. Replaces cal_deg_cuda (utils.cu:42-78) / fastAgg.cal_deg (operators.cpp:588-595). */
+int fa_degree_count_i32(const int32_t* ids, int64_t n_ids, int32_t* deg, int64_t n_nodes,
+                        hipStream_t stream);
+
+/* mask[i] = (P_i / threshold > P'_i / threshold) for i < n-1 where deg_i =
+ * dense_ptr[i+1]-dense_ptr[i], P_i the inclusive prefix of deg inside the aligned block of
+ * 256 entries holding i, P'_i the same prefix without deg_i; C (truncating) division.
+ * Replaces getBalancedPtrKernel / get_balanced_cuda (utils.cu:81-141) and
+ * fastAgg.getBalancedPtr (operators.cpp:597-604). threshold must be non-zero. */
+int fa_balance_mask_i32(const int32_t* dense_ptr, int64_t n, int32_t threshold, int32_t* mask,
+                        hipStream_t stream);
+
+/* rowptr[v] = first edge e with dst[e] >= v, for v = 0..n_dst (rowptr has n_dst+1 entries),
+ * for dst sorted ascending. The full-CSR form of the sampler's compressed cntE: it also
+ * covers zero-degree destinations. Used by the fused TGAT kernels (no reference
+ * counterpart; derives the segment->destination map of layers.py:174-183). */
+int fa_rowptr_from_sorted_dst_i64(const int64_t* dst, int64_t n_edges, int64_t n_dst,
+                                  int32_t* rowptr, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------
+ * Segmented edge softmax (drop-in kernels of edge_softmax.cu)
+ * ------------------------------------------------------------------------------- */
+
+/* For each segment s < n_seg (edges indptr[s]..indptr[s+1]) and head h < heads:
+ *   mode 0 (reciprocal): y = exp(x - max) * (1 / sum)   forward_edge_softmax
+ *   mode 1 (division)  : y = exp(x - max) / sum         forward_csr_edge_softmax
+ * with max seeded at -1e38, sum over the segment in edge order. Entries outside every
+ * segment are not written. Replaces forward_edge_softmax_cuda (edge_softmax.cu:55-78,
+ * 255-293) and forward_csr_edge_softmax_cuda (edge_softmax.cu:178-206, 450-518). */
+int fa_edge_softmax_fwd_f32(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
+                            const float* x, int64_t ldx, int32_t heads, float* y, int64_t ldy,
+                            int32_t mode, hipStream_t stream);
+int fa_edge_softmax_fwd_f64(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
+                            const double* x, int64_t ldx, int32_t heads, double* y,
+                            int64_t ldy, int32_t mode, hipStream_t stream);
+
+/* dx = y * (dy - sum_segment(y * dy)) per segment and head h < heads.
+ * Replaces backward_edge_softmax_cuda (edge_softmax.cu:79-106, 295-329) and
+ * backward_csr_edge_softmax_cuda (edge_softmax.cu:207-235, 520-577). */
+int fa_edge_softmax_bwd_f32(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
+                            const float* dy, int64_t lddy, const float* y, int64_t ldy,
+                            int32_t heads, float* dx, int64_t lddx, hipStream_t stream);
+int fa_edge_softmax_bwd_f64(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
+                            const double* dy, int64_t lddy, const double* y, int64_t ldy,
+                            int32_t heads, double* dx, int64_t lddx, hipStream_t stream);
+
+/* Grouped ("balanced") softmax: batch b covers edges batch_ptr[b]..batch_ptr[b+1]; the
+ * j-th edge of batch b belongs to group key[b*ld_key + j] (0 <= key < ld_key; edges with
+ * j >= ld_key or an out-of-range key are skipped). Softmax (division form) / its gradient
+ * over the edges of each (batch, key, head). Replaces
+ * forward/backward_balanced_edge_softmax_cuda (edge_softmax.cu:107-176, 330-448). */
+int fa_group_softmax_fwd_f32(const int64_t* batch_ptr, int64_t n_batch, const int64_t* key,
+                             int64_t ld_key, int64_t n_edges, const float* x, int64_t ldx,
+                             int32_t heads, float* y, int64_t ldy, hipStream_t stream);
+int fa_group_softmax_bwd_f32(const int64_t* batch_ptr, int64_t n_batch, const int64_t* key,
+                             int64_t ld_key, int64_t n_edges, const float* dy, int64_t lddy,
+                             const float* y, int64_t ldy, int32_t heads, float* dx,
+                             int64_t lddx, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------
+ * Sum aggregation over edges (drop-in kernels of aggregate_*_kernel.cu)
+ * ------------------------------------------------------------------------------- */
+
+/* out[dst[e], :] += x[src[e], :] for e < n_edges (COO, any order; ids outside
+ * [0, n_out) / [0, n_x) are skipped). When indptr is not NULL only the edges
+ * indptr[0] <= e < indptr[n_seg] are used. out must be zeroed by the caller. Runs of equal
+ * consecutive dst are reduced in registers, so for dst-sorted input every output row
+ * receives at most two partial sums (deterministic).
+ * Replaces computation_aware_forward_tgat_cuda (aggregate_acc_kernel.cu:36-94), with
+ * every edge covered. Also the backward of forward_tgat / forward_tgat_shd with the
+ * roles of dst and src swapped (aggregate_acc_kernel.cu:97-161,
+ * aggregate_shd_kernel.cu:212-368). */
+int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_edges,
+                            const int32_t* indptr, int64_t n_seg, const float* x, int64_t ldx,
+                            int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,
+                            hipStream_t stream);
+
+/* CSR segment sum: for segment s, out[dst[indptr[s]], :] = sum_e x[src[e], :] over the
+ * segment (edges of a segment share one destination). Rows of out outside every segment
+ * are not written. Replaces computation_aware_forward_tgat_shd_cuda
+ * (aggregate_shd_kernel.cu:37-94, 161-209). */
+int fa_segment_sum_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
+                       const int64_t* src, int64_t n_edges, const float* x, int64_t ldx,
+                       int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,
+                       hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------
+ * Fused LeakyReLU + segment softmax + dropout + aggregation (drop-in fused_attention.cu)
+ * ------------------------------------------------------------------------------- */
+
+/* Segment s (edges indptr[s]..indptr[s+1], destination dst[indptr[s]]):
+ *   attn[e,h] = softmax_s(leaky_relu(score[e,h], slope))
+ *   keep      = mask[e,h] > p ? 1/(1-p) : 0
+ *   out[dst,h*dh+d] = sum_e attn[e,h]*keep*V[src[e]-n_dst, h, d]
+ * out rows outside every segment are not written (caller zero-fills).
+ * Replaces forward_fused_attn_cuda (fused_attention.cu:68-138, 203-328). */
+int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
+                          const int64_t* src, int64_t n_edges, int64_t n_dst,
+                          const float* score, const float* V, int32_t heads, int32_t dh,
+                          float slope, float p, const float* mask, float* attn, float* out,
+                          hipStream_t stream);
+/* Gradients of fa_fused_attn_fwd_f32 given dout [n_dst, heads*dh]:
+ *   grad_V[src[e]-n_dst,h,:] = attn*keep*dout[dst,h,:]
+ *   d_act[e,h] = attn*(da - sum_s attn*da), da = keep * dout[dst,h,:].V[...]
+ * i.e. the gradient with respect to the LeakyReLU *output*; the caller applies
+ * leaky_relu'(score). grad_V must be zeroed by the caller.
+ * Replaces backward_fused_attn_cuda (fused_attention.cu:139-200, 330-446). */
+int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
+                          const int64_t* src, int64_t n_edges, int64_t n_dst, int64_t n_src,
+                          const float* dout, const float* V, const float* attn,
+                          const float* mask, int32_t heads, int32_t dh, float p,
+                          float* d_act, float* grad_V, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------
+ * Fused TGAT temporal attention (the hot path of layers.py:98-240, TGAT branch)
+ *
+ * Per edge e the key/value input row is x_e = [h_src(e) | f(e) | cos(w*dt_e + b) | 1]
+ * in "K-space": node features padded to Pn = roundup(Dn,4), edge features to
+ * Pe = roundup(De,4), time encoding to Pt = roundup(Dt,4), then the constant 1 at
+ * column Kb = Pn+Pe+Pt, zero-padded to Kp = roundup(Kb+1,4).
+ * K and V are never formed per edge: with q~[h,v,:] = Q[v,h,:] W_k,aug[h] (bias in
+ * column Kb) the score is q~.x_e, and the aggregation returns
+ * xbar[h,v,:] = sum_e a'[e,h] x_e (column Kb = sum_e a'), to which the caller applies
+ * W_v,aug. Destination v owns edges rowptr[v]..rowptr[v+1] (clamped to [0, n_edges]).
+ * ------------------------------------------------------------------------------- */
+
+typedef struct fa_tgat_graph {
+  int64_t n_dst;           /* destinations (including zero-degree ones) */
+  int64_t n_edges;
+  const int32_t* rowptr;   /* [n_dst+1] full CSR over dst-sorted edges */
+  /* node part: row of edge e = node_idx ? node_idx[e] : e; rows >= n_node read as 0 */
+  const float* node_tab; int64_t ld_node; int64_t n_node; int32_t dn; const int64_t* node_idx;
+  /* edge part: row of edge e = edge_idx ? edge_idx[e] : e; rows >= n_edge_rows read as 0 */
+  const float* edge_tab; int64_t ld_edge; int64_t n_edge_rows; int32_t de;
+  const int64_t* edge_idx;
+  /* time part */
+  const float* dt;         /* [n_edges] */
+  const float* time_w;     /* [dt_dim] */
+  const float* time_b;     /* [dt_dim] */
+  int32_t dt_dim;
+} fa_tgat_graph;
+
+/* K-space width Kp for the given dims (all > = 0). */
+int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim);
+
+/* Forward. qt: [heads][n_dst][Kp] (head stride qt_hs, row stride Kp);
+ * drop: optional [n_edges][heads] multipliers (dropout keep/(1-p)), may be NULL.
+ * Outputs: xbar [heads][n_dst][Kp] (head stride xbar_hs), scores [n_edges][heads]
+ * (post-LeakyReLU), stats [n_dst][heads][2] = (max, sum of exp). */
+int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                         int64_t qt_hs, float slope, const float* drop, float* xbar,
+                         int64_t xbar_hs, float* scores, float* stats, hipStream_t stream);
+
+/* Normalised attention att[e,h] = exp(score - max[dst]) / sum[dst] (pre-dropout), for
+ * callers that want the weights themselves. dst: [n_edges] int64 in [0, n_dst). */
+int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst, int32_t heads,
+                             const float* scores, const float* stats, float* att,
+                             hipStream_t stream);
+
+/* Backward. dxbar: gradient of xbar (same layout, head stride dxbar_hs).
+ * Outputs: dqt (layout of qt, head stride dqt_hs); d_node [n_edges][ld_dnode] gradient of
+ * the node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be
+ * NULL when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
+size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
+int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                         int64_t qt_hs, float slope, const float* drop, const float* scores,
+                         const float* stats, const float* dxbar, int64_t dxbar_hs, float* dqt,
+                         int64_t dqt_hs, float* d_node, int64_t ld_dnode, float* d_time_w,
+                         float* d_time_b, void* scratch, size_t scratch_bytes,
+                         hipStream_t stream);
+
+/* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
+int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,
+                       int64_t n, int32_t dim, float* out, int64_t ld_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTAGG_H */

@@ -1,0 +1,303 @@
+"""CPU restatement of FAST's temporal-attention aggregation path.
+
+TEST INFRASTRUCTURE ONLY. This is the checker the gfx950 kernels are compared against; only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it. Nothing in ``fast_amd`` uses it.
+
+Two parts:
+  * ``C`` - ctypes bindings of ``oracle/fastagg_ref.c``, the scalar restatement of the
+    fastAgg operators (getFastAgg/cuda_operators/*), numpy in / numpy out;
+  * torch functions restating ``layers.py``'s TGAT layer with DGL semantics
+    (``dgl.ops.edge_softmax`` at layers.py:192, ``update_all(copy_u, sum)`` at
+    layers.py:207), in float32 or float64, differentiable with torch autograd.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(_HERE, "_build", "liboracle.so")
+
+
+def build_c(force: bool = False) -> str:
+    """Compile the C restatement (gcc, contraction off)."""
+    src = os.path.join(_HERE, "fastagg_ref.c")
+    if force or not os.path.exists(LIB) or os.path.getmtime(LIB) < os.path.getmtime(src):
+        os.makedirs(os.path.dirname(LIB), exist_ok=True)
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared",
+                        "-std=c11", src, "-lm", "-o", LIB], check=True)
+    return LIB
+
+
+class _C:
+    def __init__(self):
+        self._lib = None
+
+    @property
+    def lib(self):
+        if self._lib is None:
+            self._lib = ctypes.CDLL(build_c())
+        return self._lib
+
+    @staticmethod
+    def _p(a):
+        return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+    def _call(self, name, *args):
+        conv = []
+        for a in args:
+            if isinstance(a, np.ndarray) or a is None:
+                conv.append(self._p(a))
+            elif isinstance(a, float):
+                conv.append(ctypes.c_float(a))
+            else:
+                conv.append(ctypes.c_int64(a))
+        getattr(self.lib, name)(*conv)
+
+    # --- bookkeeping (bit-exact) ---------------------------------------------------------
+    def exclusive_sum(self, x):
+        x = np.ascontiguousarray(x, dtype=np.int32)
+        out = np.empty(x.size + 1, np.int32)
+        self._call("ref_exclusive_sum_i32", x, x.size, out)
+        return out
+
+    def cal_deg(self, ids, n_nodes):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(n_nodes, np.int32)
+        self._call("ref_degree_count_i32", ids, ids.size, out, n_nodes)
+        return out
+
+    def balance_mask(self, ptr, threshold):
+        ptr = np.ascontiguousarray(ptr, dtype=np.int32)
+        out = np.zeros(max(ptr.size - 1, 0), np.int32)
+        self.lib.ref_balance_mask_i32(self._p(ptr), ctypes.c_int64(ptr.size),
+                                      ctypes.c_int32(threshold), self._p(out))
+        return out
+
+    def rowptr(self, dst, n_dst):
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        out = np.empty(n_dst + 1, np.int32)
+        self._call("ref_rowptr_from_sorted_dst", dst, dst.size, n_dst, out)
+        return out
+
+    # --- softmax -----------------------------------------------------------------------
+    def edge_softmax_fwd(self, indptr, x, heads, mode):
+        indptr = np.ascontiguousarray(indptr, dtype=np.int32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros((x.shape[0], heads), np.float32)
+        self.lib.ref_edge_softmax_fwd_f32(self._p(indptr), ctypes.c_int64(max(indptr.size - 1, 0)),
+                                          ctypes.c_int64(x.shape[0]), self._p(x),
+                                          ctypes.c_int64(x.shape[1]), ctypes.c_int32(heads),
+                                          self._p(y), ctypes.c_int64(heads), ctypes.c_int32(mode))
+        return y
+
+    def edge_softmax_bwd(self, indptr, dy, y, heads):
+        indptr = np.ascontiguousarray(indptr, dtype=np.int32)
+        dy = np.ascontiguousarray(dy, dtype=np.float32)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        dx = np.zeros_like(dy)
+        self.lib.ref_edge_softmax_bwd_f32(self._p(indptr), ctypes.c_int64(max(indptr.size - 1, 0)),
+                                          ctypes.c_int64(dy.shape[0]), self._p(dy),
+                                          ctypes.c_int64(dy.shape[1]), self._p(y),
+                                          ctypes.c_int64(y.shape[1]), ctypes.c_int32(heads),
+                                          self._p(dx), ctypes.c_int64(dx.shape[1]))
+        return dx
+
+    def group_softmax_fwd(self, bptr, key, x):
+        bptr = np.ascontiguousarray(bptr, dtype=np.int64)
+        key = np.ascontiguousarray(key, dtype=np.int64)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros_like(x)
+        self.lib.ref_group_softmax_fwd_f32(self._p(bptr), ctypes.c_int64(key.shape[0]),
+                                           self._p(key), ctypes.c_int64(key.shape[1]),
+                                           ctypes.c_int64(x.shape[0]), self._p(x),
+                                           ctypes.c_int64(x.shape[1]), ctypes.c_int32(x.shape[1]),
+                                           self._p(y), ctypes.c_int64(y.shape[1]))
+        return y
+
+    def group_softmax_bwd(self, bptr, key, dy, y):
+        bptr = np.ascontiguousarray(bptr, dtype=np.int64)
+        key = np.ascontiguousarray(key, dtype=np.int64)
+        dy = np.ascontiguousarray(dy, dtype=np.float32)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        dx = np.zeros_like(dy)
+        self.lib.ref_group_softmax_bwd_f32(self._p(bptr), ctypes.c_int64(key.shape[0]),
+                                           self._p(key), ctypes.c_int64(key.shape[1]),
+                                           ctypes.c_int64(dy.shape[0]), self._p(dy),
+                                           ctypes.c_int64(dy.shape[1]), self._p(y),
+                                           ctypes.c_int64(y.shape[1]), ctypes.c_int32(dy.shape[1]),
+                                           self._p(dx), ctypes.c_int64(dx.shape[1]))
+        return dx
+
+    # --- aggregation -------------------------------------------------------------------
+    def edge_scatter_sum(self, dst, src, x, n_out, indptr=None):
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        src = np.ascontiguousarray(src, dtype=np.int64)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros((n_out, x.shape[1]), np.float32)
+        ip = None if indptr is None else np.ascontiguousarray(indptr, dtype=np.int32)
+        nseg = 0 if ip is None else ip.size - 1
+        self.lib.ref_edge_scatter_sum_f32(self._p(dst), self._p(src), ctypes.c_int64(dst.size),
+                                          self._p(ip), ctypes.c_int64(nseg), self._p(x),
+                                          ctypes.c_int64(x.shape[1]), ctypes.c_int64(x.shape[0]),
+                                          ctypes.c_int32(x.shape[1]), self._p(out),
+                                          ctypes.c_int64(out.shape[1]), ctypes.c_int64(n_out))
+        return out
+
+    def segment_sum(self, indptr, dst, src, x, n_out):
+        indptr = np.ascontiguousarray(indptr, dtype=np.int32)
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        src = np.ascontiguousarray(src, dtype=np.int64)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.zeros((n_out, x.shape[1]), np.float32)
+        self.lib.ref_segment_sum_f32(self._p(indptr), ctypes.c_int64(indptr.size - 1), self._p(dst),
+                                     self._p(src), ctypes.c_int64(dst.size), self._p(x),
+                                     ctypes.c_int64(x.shape[1]), ctypes.c_int64(x.shape[0]),
+                                     ctypes.c_int32(x.shape[1]), self._p(out),
+                                     ctypes.c_int64(out.shape[1]), ctypes.c_int64(n_out))
+        return out
+
+    def fused_attn_fwd(self, indptr, dst, src, n_dst, score, V, slope, p, mask):
+        indptr = np.ascontiguousarray(indptr, dtype=np.int32)
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        src = np.ascontiguousarray(src, dtype=np.int64)
+        score = np.ascontiguousarray(score, dtype=np.float32)
+        V = np.ascontiguousarray(V, dtype=np.float32)
+        mask = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
+        E, H = score.shape
+        dh = V.shape[2]
+        attn = np.zeros((E, H), np.float32)
+        out = np.zeros((n_dst, H * dh), np.float32)
+        self.lib.ref_fused_attn_fwd_f32(self._p(indptr), ctypes.c_int64(indptr.size - 1), self._p(dst),
+                                        self._p(src), ctypes.c_int64(E), ctypes.c_int64(n_dst),
+                                        self._p(score), self._p(V), ctypes.c_int32(H),
+                                        ctypes.c_int32(dh), ctypes.c_float(slope), ctypes.c_float(p),
+                                        self._p(mask), self._p(attn), self._p(out))
+        return out, attn
+
+    def fused_attn_bwd(self, indptr, dst, src, n_dst, n_src, dout, V, attn, mask, p):
+        indptr = np.ascontiguousarray(indptr, dtype=np.int32)
+        dst = np.ascontiguousarray(dst, dtype=np.int64)
+        src = np.ascontiguousarray(src, dtype=np.int64)
+        dout = np.ascontiguousarray(dout, dtype=np.float32)
+        V = np.ascontiguousarray(V, dtype=np.float32)
+        attn = np.ascontiguousarray(attn, dtype=np.float32)
+        mask = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32)
+        E, H = attn.shape
+        dh = V.shape[2]
+        d_act = np.zeros((E, H), np.float32)
+        grad_V = np.zeros_like(V)
+        self.lib.ref_fused_attn_bwd_f32(self._p(indptr), ctypes.c_int64(indptr.size - 1), self._p(dst),
+                                        self._p(src), ctypes.c_int64(E), ctypes.c_int64(n_dst),
+                                        ctypes.c_int64(n_src), self._p(dout), self._p(V),
+                                        self._p(attn), self._p(mask), ctypes.c_int32(H),
+                                        ctypes.c_int32(dh), ctypes.c_float(p), self._p(d_act),
+                                        self._p(grad_V))
+        return d_act, grad_V
+
+
+C = _C()
+
+
+# ---------------------------------------------------------------------------------------
+# torch restatement of the TGAT layer
+# ---------------------------------------------------------------------------------------
+def time_encoding_weight(dim: int) -> torch.Tensor:
+    """w = 1/10**linspace(0, 9, dim) in float32 (layers.py:14)."""
+    return torch.from_numpy(1 / 10 ** np.linspace(0, 9, dim, dtype=np.float32))
+
+
+def time_encode(dt: torch.Tensor, w: torch.Tensor, b: torch.Tensor, dtype=torch.float64):
+    """cos(w*t + b) (layers.py:17-29). The argument is the float32 value of the reference's
+    Linear(1, Dt) (rounded product, then rounded sum); the cosine and everything after it
+    are evaluated in ``dtype``. Differentiable in w and b."""
+    t = dt.to(torch.float32).reshape(-1, 1)
+    arg32 = (t * w.to(torch.float32).reshape(1, -1)) + b.to(torch.float32).reshape(1, -1)
+    if dtype == torch.float32:
+        return torch.cos(arg32)
+    # Same forward value as cos(arg32) evaluated in dtype; gradients of the exact
+    # expression in dtype.
+    arg = t.to(dtype) * w.to(dtype).reshape(1, -1) + b.to(dtype).reshape(1, -1)
+    arg = arg + (arg32.to(dtype) - arg).detach()
+    return torch.cos(arg)
+
+
+def edge_softmax(scores: torch.Tensor, dst: torch.Tensor, num_dst: int) -> torch.Tensor:
+    """Softmax over the incoming edges of every destination (dgl.ops.edge_softmax,
+    layers.py:192): exp(x - max) / sum per destination and head."""
+    H = scores.shape[1]
+    idx = dst.view(-1, 1).expand(-1, H)
+    mx = torch.full((num_dst, H), -float("inf"), dtype=scores.dtype)
+    mx = mx.scatter_reduce(0, idx, scores, reduce="amax", include_self=True)
+    ex = torch.exp(scores - mx[dst].detach())
+    den = torch.zeros((num_dst, H), dtype=scores.dtype).index_add(0, dst, ex)
+    return ex / den[dst]
+
+
+def copy_u_sum(v_src: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, num_dst: int):
+    """update_all(copy_u('v','m'), sum('m','h')) (layers.py:207): out[d] = sum of source
+    rows over the incoming edges; zero-degree destinations get 0."""
+    out = torch.zeros((num_dst, v_src.shape[1]), dtype=v_src.dtype)
+    return out.index_add(0, dst, v_src[src])
+
+
+def layer_params(layer) -> dict:
+    """CPU float64 copies (leaf tensors) of a TransfomerAttentionLayer's parameters."""
+    out = {}
+    for name, p in layer.named_parameters():
+        out[name] = p.detach().to("cpu", torch.float64).clone().requires_grad_(True)
+    out["_eps"] = layer.layer_norm.eps
+    out["_heads"] = layer.num_head
+    out["_dims"] = (layer.dim_node_feat, layer.dim_edge_feat, layer.dim_time, layer.dim_out)
+    return out
+
+
+def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src: torch.Tensor,
+               dst: torch.Tensor, num_dst: int, slope: float = 0.2, att_drop=None,
+               dtype=torch.float64) -> torch.Tensor:
+    """layers.py:98-240, TGAT branch with DGL semantics, eval-mode dropout except for an
+    optional attention multiplier ``att_drop`` [E,H] (keep/(1-p) or 0).
+
+    h: [N+E, Dn] source-node features (row N+e feeds edge e); f: [E, De]; dt: [E];
+    src/dst: int64 [E] source / destination ids.
+    """
+    Dn, De, Dt, D = P["_dims"]
+    H = P["_heads"]
+    N, E = num_dst, dst.numel()
+    if E == 0:  # layers.py:101-102
+        return torch.zeros((N, D), dtype=dtype)
+    cast = lambda t: t.to(dtype)
+    hq = [cast(h[:N])] if Dn else []
+    hk = [cast(h[N:])] if Dn else []
+    if De:
+        hk.append(cast(f))
+    if Dt:
+        tw, tb = P["time_enc.w.weight"].view(-1), P["time_enc.w.bias"]
+        hk.append(time_encode(dt, tw, tb, dtype))
+        hq.append(time_encode(torch.zeros(N), tw, tb, dtype))
+    if Dn + Dt > 0:
+        Q = torch.nn.functional.linear(torch.cat(hq, 1), cast(P["w_q.weight"]), cast(P["w_q.bias"]))
+    else:
+        Q = torch.ones((N, D), dtype=dtype)
+    kv = torch.cat(hk, 1)
+    Q = Q[dst]
+    K = torch.nn.functional.linear(kv, cast(P["w_k.weight"]), cast(P["w_k.bias"]))
+    V = torch.nn.functional.linear(kv, cast(P["w_v.weight"]), cast(P["w_v.bias"]))
+    Q, K, V = Q.view(E, H, -1), K.view(E, H, -1), V.view(E, H, -1)
+    scores = torch.nn.functional.leaky_relu((Q * K).sum(2), slope)
+    att = edge_softmax(scores, dst, N)
+    if att_drop is not None:
+        att = att * cast(att_drop)
+    v = (V * att[:, :, None]).reshape(E, -1)
+    v_src = torch.cat([torch.zeros((N, v.shape[1]), dtype=dtype), v], 0)
+    agg = copy_u_sum(v_src, src, dst, N)
+    rst = torch.cat([agg, cast(h[:N])], 1) if Dn else agg
+    rst = torch.nn.functional.linear(rst, cast(P["w_out.weight"]), cast(P["w_out.bias"]))
+    rst = torch.relu(rst)
+    return torch.nn.functional.layer_norm(rst, (D,), cast(P["layer_norm.weight"]),
+                                          cast(P["layer_norm.bias"]), P["_eps"])

@@ -1,0 +1,234 @@
+"""GPU parity of the drop-in fastAgg operators against the CPU restatement (oracle/).
+
+Integer bookkeeping is compared bit-exactly; float results within FP32_TOL relative
+(infinity-norm over the tensor)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.ref_cpu import C
+from tests._util import FP32_TOL, assert_equal, assert_rel
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fa():
+    import fast_amd
+
+    return fast_amd.fastAgg
+
+
+def _csr(degrees, rng=None):
+    deg = np.asarray(degrees, dtype=np.int64)
+    nz = deg[deg > 0]
+    indptr = np.concatenate([[0], np.cumsum(nz)]).astype(np.int32)
+    dst = np.repeat(np.arange(deg.size), deg).astype(np.int64)
+    return indptr, dst
+
+
+DEGREE_SETS = {
+    "fanout10": [10] * 300,
+    "ragged": [0, 1, 2, 3, 5, 0, 17, 20, 64, 65, 100, 1, 0, 7],
+    "single": [1],
+}
+
+
+# ---------------------------------------------------------------------------------------
+# bookkeeping (bit-exact)
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("n", [0, 1, 7, 2047, 2048, 2049, 100_003, 1_000_000])
+def test_exclusive_sum(fa, dev, n):
+    rng = np.random.default_rng(n)
+    x = rng.integers(0, 50, size=n).astype(np.int32)
+    got = fa.exclusive_sum(torch.from_numpy(x).to(dev))
+    assert_equal(got, C.exclusive_sum(x), "exclusive_sum")
+
+
+def test_exclusive_sum_wraps(fa, dev):
+    x = np.full(5000, 2**30, dtype=np.int32)
+    got = fa.exclusive_sum(torch.from_numpy(x).to(dev))
+    assert_equal(got, C.exclusive_sum(x), "exclusive_sum wrap")
+
+
+@pytest.mark.parametrize("n_ids,n_nodes", [(0, 5), (1000, 17), (300_000, 1000), (5000, 1)])
+def test_cal_deg(fa, dev, n_ids, n_nodes):
+    rng = np.random.default_rng(n_ids)
+    ids = rng.integers(-3, n_nodes + 3, size=n_ids).astype(np.int32)
+    got = fa.cal_deg(torch.from_numpy(ids).to(dev), n_nodes)
+    assert_equal(got, C.cal_deg(ids, n_nodes), "cal_deg")
+
+
+@pytest.mark.parametrize("n,threshold", [(1, 3), (2, 1), (300, 7), (1025, 16), (70_001, 5),
+                                         (513, -4)])
+def test_get_balanced_ptr(fa, dev, n, threshold):
+    rng = np.random.default_rng(n)
+    ptr = np.concatenate([[0], np.cumsum(rng.integers(0, 20, size=n - 1))]).astype(np.int32)
+    got = fa.getBalancedPtr(torch.from_numpy(ptr).to(dev), threshold)
+    assert_equal(got, C.balance_mask(ptr, threshold), "getBalancedPtr")
+
+
+def test_get_balanced_ptr_nonmonotone(fa, dev):
+    rng = np.random.default_rng(5)
+    ptr = rng.integers(-100, 100, size=600).astype(np.int32)
+    got = fa.getBalancedPtr(torch.from_numpy(ptr).to(dev), 9)
+    assert_equal(got, C.balance_mask(ptr, 9), "getBalancedPtr non-monotone")
+
+
+@pytest.mark.parametrize("name", list(DEGREE_SETS))
+def test_rowptr_from_dst(fa, dev, name):
+    deg = DEGREE_SETS[name]
+    _, dst = _csr(deg)
+    got = fa.rowptr_from_dst(torch.from_numpy(dst).to(dev), len(deg))
+    assert_equal(got, C.rowptr(dst, len(deg)), "rowptr")
+
+
+def test_unique2indptr_matches_cnte(fa, dev):
+    from fast_amd.efficientGOP import unique2indptr
+
+    deg = DEGREE_SETS["ragged"]
+    indptr, dst = _csr(deg)
+    got = unique2indptr(torch.from_numpy(dst).to(dev), len(deg))
+    assert_equal(got, indptr, "unique2indptr")
+
+
+# ---------------------------------------------------------------------------------------
+# segmented softmax
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", list(DEGREE_SETS))
+@pytest.mark.parametrize("heads", [1, 2, 8])
+def test_edge_softmax_fwd_bwd(fa, dev, name, heads):
+    indptr, dst = _csr(DEGREE_SETS[name])
+    E = dst.size
+    rng = np.random.default_rng(heads)
+    x = (rng.standard_normal((E, heads)) * 3).astype(np.float32)
+    dy = rng.standard_normal((E, heads)).astype(np.float32)
+    ti, tx = torch.from_numpy(indptr).to(dev), torch.from_numpy(x).to(dev)
+    y = fa.forward_edge_softmax(ti, ti, tx, 512, heads)[0]
+    y_ref = C.edge_softmax_fwd(indptr, x, heads, 0)
+    assert_rel(y, y_ref, 1e-6, "forward_edge_softmax")
+    dx = fa.backward_edge_softmax(ti, ti, torch.from_numpy(dy).to(dev), y, 512, heads)[0]
+    assert_rel(dx, C.edge_softmax_bwd(indptr, dy, y.cpu().numpy(), heads), 1e-6,
+               "backward_edge_softmax")
+    yc = fa.forward_csr_edge_softmax(ti, ti, tx, 32, 16)[0]
+    assert_rel(yc, C.edge_softmax_fwd(indptr, x, heads, 1), 1e-6, "forward_csr_edge_softmax")
+    dxc = fa.backward_csr_edge_softmax(ti, ti, torch.from_numpy(dy).to(dev), yc, 32, 16)[0]
+    assert_rel(dxc, C.edge_softmax_bwd(indptr, dy, yc.cpu().numpy(), heads), 1e-6,
+               "backward_csr_edge_softmax")
+
+
+def test_edge_softmax_partial_heads(fa, dev):
+    """num_heads below the input width: only the first num_heads columns (edge_softmax.cu:66)."""
+    indptr, dst = _csr([3, 4, 0, 2])
+    x = np.random.default_rng(0).standard_normal((dst.size, 4)).astype(np.float32)
+    ti = torch.from_numpy(indptr).to(dev)
+    y = fa.forward_edge_softmax(ti, ti, torch.from_numpy(x).to(dev), 512, 2)[0]
+    assert tuple(y.shape) == (dst.size, 2)
+    assert_rel(y, C.edge_softmax_fwd(indptr, x, 2, 0), 1e-6, "partial heads")
+
+
+def test_edge_softmax_f64(fa, dev):
+    indptr, dst = _csr(DEGREE_SETS["ragged"])
+    x = torch.randn(dst.size, 2, dtype=torch.float64)
+    y = fa.forward_edge_softmax(torch.from_numpy(indptr).to(dev), torch.from_numpy(indptr).to(dev),
+                                x.to(dev), 512, 2)[0].cpu()
+    ref = torch.zeros_like(x)
+    for s in range(indptr.size - 1):
+        lb, le = indptr[s], indptr[s + 1]
+        ref[lb:le] = torch.softmax(x[lb:le], 0)
+    assert_rel(y, ref, 1e-13, "f64 softmax")
+
+
+def test_balanced_softmax(fa, dev):
+    rng = np.random.default_rng(3)
+    B, maxn, H = 40, 16, 2
+    counts = rng.integers(0, maxn + 1, size=B)
+    bptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    E = int(bptr[-1])
+    key = rng.integers(0, 5, size=(B, maxn)).astype(np.int64)
+    key[0, 0] = -1   # skipped entry
+    x = rng.standard_normal((E, H)).astype(np.float32)
+    dy = rng.standard_normal((E, H)).astype(np.float32)
+    tb, tk = torch.from_numpy(bptr).to(dev), torch.from_numpy(key).to(dev)
+    y = fa.forward_balanced_edge_softmax(tb, tk, torch.from_numpy(x).to(dev), 64, 16)[0]
+    y_ref = C.group_softmax_fwd(bptr, key, x)
+    assert_rel(y, y_ref, 1e-6, "forward_balanced_edge_softmax")
+    dx = fa.backward_balanced_edge_softmax(tb, tk, torch.from_numpy(dy).to(dev), y, 64, 16)[0]
+    assert_rel(dx, C.group_softmax_bwd(bptr, key, dy, y.cpu().numpy()), 1e-6,
+               "backward_balanced_edge_softmax")
+
+
+# ---------------------------------------------------------------------------------------
+# aggregation
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", list(DEGREE_SETS))
+@pytest.mark.parametrize("dim", [1, 100, 300])
+def test_tgat_aggregation(fa, dev, name, dim):
+    deg = DEGREE_SETS[name]
+    indptr, dst = _csr(deg)
+    N, E = len(deg), dst.size
+    src = np.arange(N, N + E, dtype=np.int64)
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal((N + E, dim)).astype(np.float32)
+    dout = rng.standard_normal((N, dim)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    # forward_tgat: out[dst] += x[src]; the reference passes (edges()[1], edges()[0], ...).
+    out = fa.forward_tgat(t(dst), t(src), t(x), N, 8, 128)[0]
+    ref = C.edge_scatter_sum(dst, src, x, N)
+    assert_rel(out, ref, FP32_TOL, "forward_tgat")
+    out_s = fa.forward_tgat_shd(t(indptr), t(indptr), t(dst), t(src), t(x), N, 8, 32)[0]
+    assert_rel(out_s, C.segment_sum(indptr, dst, src, x, N), FP32_TOL, "forward_tgat_shd")
+    # backward: d_x[src] += d_out[dst]
+    dx = fa.backward_tgat(t(dst), t(src), t(dout), N + E, 8, 128)[0]
+    assert_rel(dx, C.edge_scatter_sum(src, dst, dout, N + E), FP32_TOL, "backward_tgat")
+    dxs = fa.backward_tgat_shd(t(indptr), t(indptr), t(dst), t(src), t(dout), N + E, 8, 32)[0]
+    assert_rel(dxs, C.edge_scatter_sum(src, dst, dout, N + E, indptr), FP32_TOL,
+               "backward_tgat_shd")
+    # empty destinations stay exactly zero
+    empty = np.asarray(deg) == 0
+    assert torch.count_nonzero(out[torch.from_numpy(empty).to(dev)]) == 0
+
+
+def test_tgat_aggregation_unsorted(fa, dev):
+    rng = np.random.default_rng(11)
+    E, N, S = 5000, 300, 900
+    dst = rng.integers(0, N, size=E).astype(np.int64)
+    src = rng.integers(0, S, size=E).astype(np.int64)
+    x = rng.standard_normal((S, 64)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    out = fa.forward_tgat(t(dst), t(src), t(x), N, 8, 128)[0]
+    assert_rel(out, C.edge_scatter_sum(dst, src, x, N), FP32_TOL, "unsorted forward_tgat")
+
+
+# ---------------------------------------------------------------------------------------
+# fused LeakyReLU + softmax + dropout + aggregation
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("p", [0.0, 0.3])
+def test_fused_attn(fa, dev, p):
+    deg = DEGREE_SETS["ragged"]
+    indptr, dst = _csr(deg)
+    N, E, H, dh = len(deg), dst.size, 2, 50
+    src = np.arange(N, N + E, dtype=np.int64)
+    rng = np.random.default_rng(7)
+    score = rng.standard_normal((E, H)).astype(np.float32)
+    V = rng.standard_normal((E, H, dh)).astype(np.float32)
+    dout = rng.standard_normal((N, H * dh)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    out, attn, mask = fa.forward_fused_attn(t(score), t(V), t(indptr), t(indptr), t(dst), t(src),
+                                            N, H, 0.2, p)
+    out_ref, attn_ref = C.fused_attn_fwd(indptr, dst, src, N, score, V, 0.2, p, mask.cpu().numpy())
+    assert_rel(attn, attn_ref, 1e-6, "fused attn")
+    assert_rel(out, out_ref, FP32_TOL, "fused out")
+    d_act, gV = fa.backward_fused_attn(t(dout), t(V), attn, mask, t(indptr), t(indptr), t(dst),
+                                       t(src), N + E, H, 0.2, p)
+    d_ref, gV_ref = C.fused_attn_bwd(indptr, dst, src, N, N + E, dout, V, attn.cpu().numpy(),
+                                     mask.cpu().numpy(), p)
+    assert_rel(d_act, d_ref, FP32_TOL, "fused d_act")
+    assert_rel(gV, gV_ref, FP32_TOL, "fused grad_V")
+
+
+def test_inputs_must_be_on_gpu(fa):
+    x = torch.zeros(4, 2)
+    ip = torch.tensor([0, 2, 4], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        fa.forward_edge_softmax(ip, ip, x, 512, 2)

@@ -1,0 +1,150 @@
+"""GPU parity of the fused TGAT layer (fast_amd.tgat) with the CPU restatement of
+layers.py:98-240 (oracle.ref_cpu.tgat_layer) evaluated in float64 on the same float32
+inputs: layer output and every gradient within FP32_TOL relative (infinity norm)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.ref_cpu import layer_params, tgat_layer
+from tests._util import FP32_TOL, assert_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _mask(E, H, p, seed):
+    g = torch.Generator().manual_seed(seed)
+    keep = (torch.rand(E, H, generator=g) >= p).float()
+    return keep / (1 - p)
+
+
+def _check_layer(dev, dn, de, dt, H, D, degrees, seed=0, time_bias=False, p_drop=0.0,
+                 tol=FP32_TOL):
+    from fast_amd.tgat import TransfomerAttentionLayer
+    from fast_amd.workloads import single_layer
+
+    torch.manual_seed(seed)
+    layer = TransfomerAttentionLayer(dn, de, dt, H, 0.0, 0.0, D)
+    if time_bias and dt > 0:
+        with torch.no_grad():
+            layer.time_enc.w.bias.uniform_(-3.0, 3.0)
+    layer = layer.to(dev)
+    N = len(degrees)
+    inp = single_layer(N, dn=dn, de=de, dt_dim=dt, heads=H, dim_out=D, seed=seed + 1,
+                       degrees=np.asarray(degrees))
+    cpu = inp.block
+    blk = cpu.to(dev)
+    blk.srcdata["h"].requires_grad_(True)
+    E = cpu.num_edges()
+    drop = _mask(E, H, p_drop, seed + 2) if p_drop > 0 else None
+    out = layer.attend(blk, None if drop is None else drop.to(dev))
+    out.backward(inp.dout.to(dev))
+
+    P = layer_params(layer)
+    h64 = cpu.srcdata["h"].double().requires_grad_(True)
+    src, dst = cpu.edges()
+    ref = tgat_layer(P, h64, cpu.edata["f"], cpu.edata["dt"], src, dst, N, att_drop=drop)
+    ref.backward(inp.dout.double())
+    errs = {"out": assert_rel(out, ref, tol, "layer output")}
+    for name, prm in layer.named_parameters():
+        if P[name].grad is None:
+            continue
+        errs[name] = assert_rel(prm.grad, P[name].grad, tol, f"grad {name}")
+    if dn > 0:
+        errs["h"] = assert_rel(blk.srcdata["h"].grad, h64.grad, tol, "grad h")
+    return errs
+
+
+@pytest.mark.parametrize("dims", [(100, 172, 100, 2, 100), (7, 5, 3, 1, 4), (8, 0, 4, 2, 8),
+                                  (0, 12, 9, 4, 16), (13, 6, 0, 8, 64), (100, 172, 100, 8, 256)])
+def test_layer_small(dev, dims):
+    dn, de, dt, H, D = dims
+    degrees = [0, 1, 2, 3, 10, 10, 17, 0, 20, 5, 64, 70, 1]
+    _check_layer(dev, dn, de, dt, H, D, degrees)
+
+
+def test_layer_time_bias_and_dropout(dev):
+    _check_layer(dev, 100, 172, 100, 2, 100, [10] * 50 + [0, 3, 20], time_bias=True, p_drop=0.1)
+
+
+def test_layer_c1_shape(dev):
+    """Config 1 shape: 1800 destinations x fanout 10."""
+    _check_layer(dev, 100, 172, 100, 2, 100, [10] * 1800, seed=3)
+
+
+def test_layer_c2_shape(dev):
+    """Config 2 shape: 12000 destinations x fanout 10 (forward + backward)."""
+    _check_layer(dev, 100, 172, 100, 2, 100, [10] * 12000, seed=4)
+
+
+def test_layer_ragged(dev):
+    from fast_amd.workloads import ragged_degrees
+
+    _check_layer(dev, 100, 172, 100, 2, 100, ragged_degrees(3000, seed=0), seed=5)
+
+
+def test_gathered_tables_match_dense(dev):
+    """Rows gathered inside the kernel from node / edge tables by id give the layer the
+    same values as pre-gathered dense features (utils.py:161,187)."""
+    from fast_amd.tgat import Block, TransfomerAttentionLayer
+
+    torch.manual_seed(0)
+    N, fan, dn, de = 300, 10, 100, 172
+    layer = TransfomerAttentionLayer(dn, de, 100, 2, 0.0, 0.0, 100).to(dev)
+    g = torch.Generator().manual_seed(9)
+    ntab = torch.randn(500, dn, generator=g)
+    etab = torch.randn(4000, de, generator=g)
+    blk = Block.from_fanout(N, torch.full((N,), fan, dtype=torch.int64))
+    E = blk.num_edges()
+    nid = torch.randint(0, 500, (N + E,), generator=g)
+    eid = torch.randint(0, 4000, (E,), generator=g)
+    dt = torch.empty(E).exponential_(1e-4, generator=g)
+    a = blk.to(dev)
+    a.node_table, a.edge_table = ntab.to(dev), etab.to(dev)
+    a.srcdata["ID"], a.edata["ID"], a.edata["dt"] = nid.to(dev), eid.to(dev), dt.to(dev)
+    b = blk.to(dev)
+    b.srcdata["h"], b.edata["f"], b.edata["dt"] = ntab[nid].to(dev), etab[eid].to(dev), dt.to(dev)
+    with torch.no_grad():
+        oa, ob = layer(a), layer(b)
+    assert torch.equal(oa, ob)
+
+
+def test_two_layer_stack(dev):
+    """2-layer TGAT (modules.py:48-64) on gathered tables vs the float64 restatement."""
+    from fast_amd.tgat import TGATEncoder
+    from fast_amd.workloads import two_layer
+
+    torch.manual_seed(0)
+    enc = TGATEncoder(100, 172, 100, 2, 100, num_layers=2, dropout=0.0, att_dropout=0.0)
+    enc = enc.to(dev)
+    inp = two_layer(roots=30, n_nodes=2000, n_edge_rows=20000, seed=1, device="cpu")
+    blocks = [b.to(dev) for b in inp.blocks]
+    out = enc(blocks)
+    out.backward(inp.dout.to(dev))
+
+    b0, b1 = inp.blocks
+    P0 = layer_params(enc.layers["l0h0"])
+    P1 = layer_params(enc.layers["l1h0"])
+    h0 = b0.node_table[b0.srcdata["ID"]]
+    f0 = b0.edge_table[b0.edata["ID"]]
+    s0, d0 = b0.edges()
+    r0 = tgat_layer(P0, h0, f0, b0.edata["dt"], s0, d0, b0.num_dst_nodes())
+    f1 = b1.edge_table[b1.edata["ID"]]
+    s1, d1 = b1.edges()
+    r1 = tgat_layer(P1, r0, f1, b1.edata["dt"], s1, d1, b1.num_dst_nodes())
+    r1.backward(inp.dout.double())
+    assert_rel(out, r1, FP32_TOL, "2-layer output")
+    for lname, P in (("l0h0", P0), ("l1h0", P1)):
+        for name, prm in enc.layers[lname].named_parameters():
+            assert_rel(prm.grad, P[name].grad, FP32_TOL, f"grad {lname}.{name}")
+
+
+def test_zero_edge_block(dev):
+    from fast_amd.tgat import Block, TransfomerAttentionLayer
+
+    layer = TransfomerAttentionLayer(4, 4, 4, 2, 0.0, 0.0, 4).to(dev)
+    blk = Block.from_fanout(5, torch.zeros(5, dtype=torch.int64)).to(dev)
+    blk.srcdata["h"] = torch.randn(5, 4, device=dev)
+    blk.edata["f"] = torch.randn(0, 4, device=dev)
+    blk.edata["dt"] = torch.zeros(0, device=dev)
+    out = layer(blk)
+    assert out.shape == (5, 4) and torch.count_nonzero(out) == 0

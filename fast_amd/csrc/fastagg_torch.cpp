@@ -591,11 +591,12 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
                                       at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
                                       double slope, std::optional<at::Tensor> drop,
-                                      at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
-                                      bool need_d_node) {
+                                      at::Tensor xbar, at::Tensor scores, at::Tensor stats,
+                                      at::Tensor dxbar, bool need_d_node) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
   const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
+  check_kspace(xbar, g, H, "xbar");
   check_kspace(dxbar, g, H, "dxbar");
   CHECK_INPUT(scores);
   CHECK_INPUT(stats);
@@ -618,7 +619,8 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
   auto scratch = at::empty({static_cast<int64_t>(sb)}, qt.options().dtype(at::kByte));
   const int st = fa_tgat_attn_bwd_f32(
       &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(0), static_cast<float>(slope),
-      dptr, scores.data_ptr<float>(), stats.data_ptr<float>(), dxbar.data_ptr<float>(),
+      dptr, xbar.data_ptr<float>(), xbar.stride(0), scores.data_ptr<float>(),
+      stats.data_ptr<float>(), dxbar.data_ptr<float>(),
       dxbar.stride(0), dqt.data_ptr<float>(), dqt.stride(0),
       need_d_node && g.n_edges > 0 && g.dn > 0 ? d_node.data_ptr<float>() : nullptr,
       need_d_node ? g.dn : 0, d_tw.data_ptr<float>(), d_tb.data_ptr<float>(), scratch.data_ptr(),
@@ -730,7 +732,7 @@ PYBIND11_MODULE(fastAgg, m) {
   m.def("tgat_attn_bwd", &tgat_attn_bwd, "backward of tgat_attn_fwd", py::arg("rowptr"),
         py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"), py::arg("edge_idx"),
         py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"), py::arg("slope"),
-        py::arg("drop"), py::arg("scores"), py::arg("stats"), py::arg("dxbar"),
+        py::arg("drop"), py::arg("xbar"), py::arg("scores"), py::arg("stats"), py::arg("dxbar"),
         py::arg("need_d_node"));
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
         py::arg("dst"), py::arg("scores"), py::arg("stats"));

@@ -11,6 +11,19 @@
 // "K-space" (float4 chunks): node chunks [0,cn), edge chunks [cn,cn+ce), time chunks
 // [cn+ce, cn+ce+ct), then one bias chunk (1,0,0,0). One wavefront per destination;
 // lane l owns chunks l, l+64, ... (NS slots).
+//
+// Latency structure: the per-edge ids, dt, dropout multipliers (and scores in backward) of
+// up to 64 edges are loaded with one coalesced vector load per array and broadcast with
+// readlane; row gathers run two batches deep (the next batch's loads are in flight while
+// the current one is scored); time encodings are evaluated by all 64 lanes (dims lane,
+// lane+64, ...) into a per-wave LDS tile.
+//
+// Backward, per destination, in one pass over the edges:
+//   T_h     = dxbar[h] . xbar[h]                      (= sum_e a*drop*(dxbar[h] . x_e))
+//   da'     = dxbar[h] . x_e
+//   dz      = a * (drop*da' - T_h) * leaky'(s)
+//   dqt[h] += dz * x_e
+//   dx_e    = sum_h a*drop*dxbar[h] + dz*qt[h]        -> node-row gradient, time-encoding grads
 #include <float.h>
 
 #include "fa_common.hpp"
@@ -20,7 +33,18 @@ namespace {
 
 enum ChunkKind : int { kNode = 0, kEdge = 1, kTime = 2, kBias = 3, kNone = 4 };
 
-constexpr int kBatch = 4;             // edges gathered per batch (loads in flight)
+// Tunables (build-time): edges per batch (two batches are in flight), and the minimum
+// waves per SIMD the compiler must allow for the forward / backward kernels.
+#ifndef FA_TGAT_BATCH
+#define FA_TGAT_BATCH 2
+#endif
+#ifndef FA_TGAT_FWD_WAVES
+#define FA_TGAT_FWD_WAVES 1
+#endif
+#ifndef FA_TGAT_BWD_WAVES
+#define FA_TGAT_BWD_WAVES 1
+#endif
+constexpr int kBatch = FA_TGAT_BATCH;
 constexpr int kBwdMaxBlocks = 2048;   // backward grid cap (time-grad partial rows)
 
 struct TgatParams {
@@ -31,11 +55,12 @@ struct TgatParams {
   int node_vec, edge_vec, dnode_vec;  // rows 16-byte aligned: float4 access allowed
   const float* dt; const float* time_w; const float* time_b; int dt_dim;
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
+  int tvs;                            // LDS row stride of the time tiles (4*ct)
   int64_t kp;                         // row stride of qt / xbar = 4*cp
   const float* qt; int64_t qt_hs;
   float slope;
   const float* drop;
-  // forward outputs
+  // forward outputs / backward input
   float* xbar; int64_t xbar_hs;
   float* scores; float* stats;
   // backward
@@ -45,7 +70,7 @@ struct TgatParams {
   float* partial;                     // [gridDim.x][2][dt_dim]
 };
 
-// What lane `lane` holds in slot k: kind, element offset inside its part, valid count.
+// What a lane holds in slot k: kind, element offset inside its part, valid count.
 struct Slot {
   int kind, off, valid;
 };
@@ -80,56 +105,159 @@ __device__ __forceinline__ float4 load_row_chunk(const float* row, int off, int 
   return v;
 }
 
-// Time-encoding chunk: cos(w_j * t + b_j) for the slot's (up to) 4 dims.
-__device__ __forceinline__ float4 time_chunk(float t, const float4& w, const float4& b, int valid) {
-  float4 v = f4_zero();
-  if (valid > 0) v.x = cosf(time_arg(t, w.x, b.x));
-  if (valid > 1) v.y = cosf(time_arg(t, w.y, b.y));
-  if (valid > 2) v.z = cosf(time_arg(t, w.z, b.z));
-  if (valid > 3) v.w = cosf(time_arg(t, w.w, b.w));
-  return v;
+// Orders this wave's LDS accesses across lanes of the same wave.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// Gathers the NS chunks this lane owns of x_e for edge e.
+__device__ __forceinline__ int lane_int(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
+__device__ __forceinline__ float lane_flt(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// Per-lane constants: slot kinds and the time parameters of the dims this lane encodes.
 template <int NS>
-__device__ __forceinline__ void gather_x(const TgatParams& P, const Slot (&sl)[NS],
-                                         const float4 (&tw)[NS], const float4 (&tb)[NS],
-                                         int64_t e, float4 (&x)[NS]) {
-  // Row ids are wave-uniform; out-of-range rows read as zeros.
-  const int64_t nrow = P.node_idx ? P.node_idx[e] : e;
-  const int64_t erow = P.edge_idx ? P.edge_idx[e] : e;
-  const bool nok = nrow >= 0 && nrow < P.n_node;
-  const bool eok = erow >= 0 && erow < P.n_erow;
-  const float* nptr = P.node_tab + (nok ? nrow : 0) * P.ld_node;
-  const float* eptr = P.edge_tab + (eok ? erow : 0) * P.ld_edge;
-  const float t = P.dt_dim > 0 ? P.dt[e] : 0.f;
+struct LaneCtx {
+  Slot sl[NS];
+  float w0, b0, w1, b1;   // time dims j = lane and lane + 64
+};
+
+template <int NS>
+__device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) {
+  const int lane = lane_id();
 #pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    const Slot s = sl[k];
-    if (s.kind == kNode) x[k] = nok ? load_row_chunk(nptr, s.off, s.valid, P.node_vec) : f4_zero();
-    else if (s.kind == kEdge) x[k] = eok ? load_row_chunk(eptr, s.off, s.valid, P.edge_vec) : f4_zero();
-    else if (s.kind == kTime) x[k] = time_chunk(t, tw[k], tb[k], s.valid);
-    else if (s.kind == kBias) x[k] = make_float4(1.f, 0.f, 0.f, 0.f);
-    else x[k] = f4_zero();
+  for (int k = 0; k < NS; ++k) L.sl[k] = classify(P, lane + k * kWave);
+  L.w0 = lane < P.dt_dim ? P.time_w[lane] : 0.f;
+  L.b0 = lane < P.dt_dim ? P.time_b[lane] : 0.f;
+  L.w1 = lane + kWave < P.dt_dim ? P.time_w[lane + kWave] : 0.f;
+  L.b1 = lane + kWave < P.dt_dim ? P.time_b[lane + kWave] : 0.f;
+}
+
+// Zeroes the padding dims [dt_dim, tvs) of `rows` rows of this wave's time tiles.
+__device__ __forceinline__ void zero_time_pad(const TgatParams& P, float* tile, int rows) {
+  const int lane = lane_id();
+  const int pad = P.tvs - P.dt_dim;
+  if (pad <= 0) return;
+  for (int i = lane; i < rows * pad; i += kWave) tile[(i / pad) * P.tvs + P.dt_dim + i % pad] = 0.f;
+}
+
+// Per-lane metadata of up to 64 consecutive edges c0 + lane: row ids (split in 32-bit
+// halves for readlane), dt, dropout multipliers and (backward) scores.
+template <int H, bool SCORES>
+struct EdgeMeta {
+  int nlo, nhi, elo, ehi;
+  float t;
+  float dr[H];
+  float sc[H];
+};
+
+template <int H, bool SCORES>
+__device__ __forceinline__ void stage_meta(const TgatParams& P, int64_t c0, int cnt,
+                                           EdgeMeta<H, SCORES>& M) {
+  const int lane = lane_id();
+  const int64_t e = c0 + (lane < cnt ? lane : 0);
+  const int64_t nr = P.node_idx ? P.node_idx[e] : e;
+  const int64_t er = P.edge_idx ? P.edge_idx[e] : e;
+  M.nlo = static_cast<int>(nr & 0xffffffff);
+  M.nhi = static_cast<int>(nr >> 32);
+  M.elo = static_cast<int>(er & 0xffffffff);
+  M.ehi = static_cast<int>(er >> 32);
+  M.t = P.dt_dim > 0 ? P.dt[e] : 0.f;
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    M.dr[h] = P.drop ? P.drop[e * H + h] : 1.f;
+    M.sc[h] = SCORES ? P.scores[e * H + h] : 0.f;
   }
 }
 
-template <int NS>
-__device__ __forceinline__ void setup_slots(const TgatParams& P, Slot (&sl)[NS], float4 (&tw)[NS],
-                                            float4 (&tb)[NS]) {
+template <int H, bool SCORES>
+__device__ __forceinline__ int64_t meta_node(const EdgeMeta<H, SCORES>& M, int j) {
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_int(M.nhi, j))) << 32) |
+                              static_cast<uint32_t>(lane_int(M.nlo, j)));
+}
+
+template <int H, bool SCORES>
+__device__ __forceinline__ int64_t meta_edge(const EdgeMeta<H, SCORES>& M, int j) {
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_int(M.ehi, j))) << 32) |
+                              static_cast<uint32_t>(lane_int(M.elo, j)));
+}
+
+// Issues the node / edge chunk loads of batch entries [jb, jb+nb) (time and bias chunks
+// are filled in later by fill_x).
+template <int NS, int H, bool SCORES>
+__device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS>& L,
+                                           const EdgeMeta<H, SCORES>& M, int jb, int nb,
+                                           float4 (&x)[kBatch][NS]) {
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    if (b < nb) {
+      const int64_t nrow = meta_node(M, jb + b);
+      const int64_t erow = meta_edge(M, jb + b);
+      const bool nok = nrow >= 0 && nrow < P.n_node;
+      const bool eok = erow >= 0 && erow < P.n_erow;
+      const float* nptr = P.node_tab + (nok ? nrow : 0) * P.ld_node;
+      const float* eptr = P.edge_tab + (eok ? erow : 0) * P.ld_edge;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        const Slot s = L.sl[k];
+        if (s.kind <= kEdge) {
+          const bool is_node = s.kind == kNode;
+          const float* row = is_node ? nptr : eptr;
+          const bool ok = is_node ? nok : eok;
+          const int vec = is_node ? P.node_vec : P.edge_vec;
+          x[b][k] = ok ? load_row_chunk(row, s.off, s.valid, vec) : f4_zero();
+        }
+      }
+    }
+  }
+}
+
+template <bool SIN>
+__device__ __forceinline__ void encode_one(float a, float* rc, float* rs, int j) {
+  if (SIN) {
+    float sv, cv;
+    sincosf(a, &sv, &cv);
+    rc[j] = cv;
+    rs[j] = -sv;
+  } else {
+    rc[j] = cosf(a);
+  }
+}
+
+// cos (and, with SIN, -sin) of the time arguments of batch entries [jb, jb+nb) into the
+// LDS tiles tc[b][j] / ts[b][j]; every lane evaluates dims lane, lane+64, ...
+template <int NS, int H, bool SCORES, bool SIN>
+__device__ __forceinline__ void encode_times(const TgatParams& P, const LaneCtx<NS>& L,
+                                             const EdgeMeta<H, SCORES>& M, int jb, int nb,
+                                             float* tc, float* ts) {
   const int lane = lane_id();
 #pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    const int c = lane + k * kWave;
-    sl[k] = classify(P, c);  // chunks past the bias chunk are kNone
-    tw[k] = f4_zero();
-    tb[k] = f4_zero();
-    if (sl[k].kind == kTime) {
-      const int o = sl[k].off, v = sl[k].valid;
-      if (v > 0) { tw[k].x = P.time_w[o];     tb[k].x = P.time_b[o]; }
-      if (v > 1) { tw[k].y = P.time_w[o + 1]; tb[k].y = P.time_b[o + 1]; }
-      if (v > 2) { tw[k].z = P.time_w[o + 2]; tb[k].z = P.time_b[o + 2]; }
-      if (v > 3) { tw[k].w = P.time_w[o + 3]; tb[k].w = P.time_b[o + 3]; }
+  for (int b = 0; b < kBatch; ++b) {
+    if (b >= nb) break;
+    const float t = lane_flt(M.t, jb + b);
+    float* rc = tc + b * P.tvs;
+    float* rs = SIN ? ts + b * P.tvs : nullptr;
+    if (lane < P.dt_dim) encode_one<SIN>(time_arg(t, L.w0, L.b0), rc, rs, lane);
+    if (lane + kWave < P.dt_dim) encode_one<SIN>(time_arg(t, L.w1, L.b1), rc, rs, lane + kWave);
+    for (int j = lane + 2 * kWave; j < P.dt_dim; j += kWave)
+      encode_one<SIN>(time_arg(t, P.time_w[j], P.time_b[j]), rc, rs, j);
+  }
+}
+
+// Fills the time (from the LDS tile) and bias chunks of the batch, zeroes unused entries.
+template <int NS>
+__device__ __forceinline__ void fill_x(const TgatParams& P, const LaneCtx<NS>& L, int nb,
+                                       const float* tc, float4 (&x)[kBatch][NS]) {
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const Slot s = L.sl[k];
+      if (b >= nb || s.kind == kNone) x[b][k] = f4_zero();
+      else if (s.kind == kTime) x[b][k] = *reinterpret_cast<const float4*>(tc + b * P.tvs + s.off);
+      else if (s.kind == kBias) x[b][k] = make_float4(1.f, 0.f, 0.f, 0.f);
     }
   }
 }
@@ -161,33 +289,98 @@ __device__ __forceinline__ void store_rows(float* base, int64_t hs, int64_t v, i
     }
 }
 
-template <int H, int NS>
-__device__ __forceinline__ float head_dot(const float4 (&q)[H][NS], const float4 (&x)[NS], int h) {
+template <int NS>
+__device__ __forceinline__ float row_dot(const float4 (&a)[NS], const float4 (&b)[NS]) {
   float p = 0.f;
 #pragma unroll
-  for (int k = 0; k < NS; ++k) p += dot4(q[h][k], x[k]);
+  for (int k = 0; k < NS; ++k) p += dot4(a[k], b[k]);
   return p;
 }
 
 // ---------------------------------------------------------------------------------
 // Forward: one wave per destination, online softmax over batches of kBatch edges.
+// Dynamic LDS: per wave one [kBatch][tvs] cosine tile.
 // ---------------------------------------------------------------------------------
 template <int H, int NS>
-__global__ __launch_bounds__(kBlock) void tgat_fwd(TgatParams P) {
-  const int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+struct FwdState {
+  float4 q[H][NS];
+  float4 acc[H][NS];
+  float m[H], l[H];
+};
+
+template <int H, int NS>
+__device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
+                                          const EdgeMeta<H, false>& M, int64_t c0, int jb, int nb,
+                                          float* tc, float4 (&x)[kBatch][NS], FwdState<H, NS>& S) {
+  const int lane = lane_id();
+  if (P.dt_dim > 0) {
+    lds_sync();
+    encode_times<NS, H, false, false>(P, L, M, jb, nb, tc, nullptr);
+    lds_sync();
+  }
+  fill_x<NS>(P, L, nb, tc, x);
+  float sc[kBatch][H];
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+    for (int h = 0; h < H; ++h) sc[b][h] = leaky(wave_sum(row_dot<NS>(S.q[h], x[b])), P.slope);
+  {
+    // scores of the batch: lane b*H+h stores s[c0+jb+b, h] (contiguous)
+    float mine = 0.f;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+        if (lane == b * H + h) mine = sc[b][h];
+    if (lane < nb * H) P.scores[(c0 + jb) * H + lane] = mine;
+  }
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    if (b >= nb) break;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float s = sc[b][h];
+      const float dr = lane_flt(M.dr[h], jb + b);
+      if (s > S.m[h]) {
+        const float r = expf(S.m[h] - s);  // 0 on the first edge
+        S.l[h] = fmaf(S.l[h], r, 1.f);
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+          scale4(S.acc[h][k], r);
+          fma4(S.acc[h][k], dr, x[b][k]);
+        }
+        S.m[h] = s;
+      } else {
+        const float pe = expf(s - S.m[h]);
+        S.l[h] += pe;
+        const float w = pe * dr;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) fma4(S.acc[h][k], w, x[b][k]);
+      }
+    }
+  }
+}
+
+template <int H, int NS>
+__global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams P) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x / kWave;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
   if (v >= P.n_dst) return;
   const int lane = lane_id();
   const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
   const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
 
-  float4 acc[H][NS];
+  FwdState<H, NS> S;
 #pragma unroll
-  for (int h = 0; h < H; ++h)
+  for (int h = 0; h < H; ++h) {
+    S.m[h] = -INFINITY;
+    S.l[h] = 0.f;
 #pragma unroll
-    for (int k = 0; k < NS; ++k) acc[h][k] = f4_zero();
-
+    for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
+  }
   if (e1 <= e0) {  // zero-degree destination: xbar = 0
-    store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, acc, P.cp);
+    store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc, P.cp);
     if (lane < H) {
       P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
       P.stats[(v * H + lane) * 2 + 1] = 0.f;
@@ -195,249 +388,218 @@ __global__ __launch_bounds__(kBlock) void tgat_fwd(TgatParams P) {
     return;
   }
 
-  Slot sl[NS];
-  float4 tw[NS], tb[NS];
-  setup_slots<NS>(P, sl, tw, tb);
-  float4 q[H][NS];
-  load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, q, P.cp);
+  float* tc = lds + wave * (kBatch * P.tvs);
+  LaneCtx<NS> L;
+  setup_lane<NS>(P, L);
+  zero_time_pad(P, tc, kBatch);
+  load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q, P.cp);
 
-  float m[H], l[H];
-#pragma unroll
-  for (int h = 0; h < H; ++h) { m[h] = -INFINITY; l[h] = 0.f; }
-
-  for (int64_t eb = e0; eb < e1; eb += kBatch) {
-    const int nb = static_cast<int>(e1 - eb < kBatch ? e1 - eb : kBatch);
-    float4 x[kBatch][NS];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      if (b < nb) gather_x<NS>(P, sl, tw, tb, eb + b, x[b]);
-      else
-#pragma unroll
-        for (int k = 0; k < NS; ++k) x[b][k] = f4_zero();
-    }
-    float sc[kBatch][H];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b)
-#pragma unroll
-      for (int h = 0; h < H; ++h) sc[b][h] = leaky(wave_sum(head_dot<H, NS>(q, x[b], h)), P.slope);
-
-    // Scores of this batch: lane b*H+h stores s[eb+b, h] (contiguous).
-    {
-      float mine = 0.f;
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b)
-#pragma unroll
-        for (int h = 0; h < H; ++h)
-          if (lane == b * H + h) mine = sc[b][h];
-      if (lane < nb * H) P.scores[eb * H + lane] = mine;
-    }
-
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      if (b >= nb) break;
-      const int64_t e = eb + b;
-#pragma unroll
-      for (int h = 0; h < H; ++h) {
-        const float s = sc[b][h];
-        const float dr = P.drop ? P.drop[e * H + h] : 1.f;
-        if (s > m[h]) {
-          const float r = expf(m[h] - s);  // 0 on the first edge
-          l[h] = fmaf(l[h], r, 1.f);
-#pragma unroll
-          for (int k = 0; k < NS; ++k) {
-            scale4(acc[h][k], r);
-            fma4(acc[h][k], dr, x[b][k]);
-          }
-          m[h] = s;
-        } else {
-          const float pe = expf(s - m[h]);
-          l[h] += pe;
-          const float w = pe * dr;
-#pragma unroll
-          for (int k = 0; k < NS; ++k) fma4(acc[h][k], w, x[b][k]);
-        }
+  for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
+    const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+    EdgeMeta<H, false> M;
+    stage_meta<H, false>(P, c0, cnt, M);
+    float4 xa[kBatch][NS], xb[kBatch][NS];
+    issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
+      const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
+      const int nb2 = cnt - jb - kBatch;
+      const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
+      if (nb > 0) issue_rows<NS, H, false>(P, L, M, jb + kBatch, nb, xb);
+      fwd_batch<H, NS>(P, L, M, c0, jb, na, tc, xa, S);
+      if (nb > 0) {
+        const int nn2 = cnt - jb - 2 * kBatch;
+        const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
+        if (nn > 0) issue_rows<NS, H, false>(P, L, M, jb + 2 * kBatch, nn, xa);
+        fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, S);
       }
     }
   }
 
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const float lsum = l[h];
+    const float lsum = S.l[h];
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-      acc[h][k].x /= lsum;
-      acc[h][k].y /= lsum;
-      acc[h][k].z /= lsum;
-      acc[h][k].w /= lsum;
+      S.acc[h][k].x /= lsum;
+      S.acc[h][k].y /= lsum;
+      S.acc[h][k].z /= lsum;
+      S.acc[h][k].w /= lsum;
     }
   }
-  store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, acc, P.cp);
+  store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc, P.cp);
   if (lane < H) {
     float mm = 0.f, ll = 0.f;
 #pragma unroll
     for (int h = 0; h < H; ++h)
-      if (lane == h) { mm = m[h]; ll = l[h]; }
+      if (lane == h) { mm = S.m[h]; ll = S.l[h]; }
     P.stats[(v * H + lane) * 2 + 0] = mm;
     P.stats[(v * H + lane) * 2 + 1] = ll;
   }
 }
 
 // ---------------------------------------------------------------------------------
-// Backward: one wave per destination (grid-stride), two passes over the edges.
-//   pass 1: da'[e,h] = dxbar[h,v] . x_e,  T_h = sum_e a*drop*da'
-//   pass 2: dz = a*(drop*da' - T)*leaky'(s);  dqt += dz*x_e;
-//           dx_e = sum_h a*drop*dxbar[h] + dz*qt[h]  -> node rows / time-grad partials
+// Backward: one wave per destination (grid-stride), one pass over the edges.
+// Dynamic LDS: per wave [kBatch][tvs] cos and -sin tiles, then the workgroup's time-grad
+// reduction buffer [kWavesPerBlock][2][tvs].
 // ---------------------------------------------------------------------------------
 template <int H, int NS>
-__global__ __launch_bounds__(kBlock) void tgat_bwd(TgatParams P) {
-  __shared__ float red[kWavesPerBlock][2][kWave * NS * 4];
-  const int lane = lane_id();
-  const int wave_in_block = threadIdx.x / kWave;
+struct BwdState {
+  float4 q[H][NS], g[H][NS], dq[H][NS];
+  float4 gw[NS], gb[NS];  // time-grad accumulators of this lane's time chunks (whole wave)
+  float mh[H], lh[H], T[H];
+};
 
-  Slot sl[NS];
-  float4 tw[NS], tb[NS];
-  setup_slots<NS>(P, sl, tw, tb);
-  float4 gw[NS], gb[NS];  // time-grad accumulators for this lane's time chunks
+template <int H, int NS>
+__device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
+                                          const EdgeMeta<H, true>& M, int64_t c0, int jb, int nb,
+                                          float* tc, float* ts, float4 (&x)[kBatch][NS],
+                                          BwdState<H, NS>& S) {
+  if (P.dt_dim > 0) {
+    lds_sync();
+    encode_times<NS, H, true, true>(P, L, M, jb, nb, tc, ts);
+    lds_sync();
+  }
+  fill_x<NS>(P, L, nb, tc, x);
+  float dap[kBatch][H];
 #pragma unroll
-  for (int k = 0; k < NS; ++k) { gw[k] = f4_zero(); gb[k] = f4_zero(); }
+  for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+    for (int h = 0; h < H; ++h) dap[b][h] = wave_sum(row_dot<NS>(S.g[h], x[b]));
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    if (b >= nb) break;
+    const int j = jb + b;
+    const int64_t e = c0 + j;
+    float ad[H], dz[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float s = lane_flt(M.sc[h], j);
+      const float dr = lane_flt(M.dr[h], j);
+      const float a = expf(s - S.mh[h]) / S.lh[h];
+      ad[h] = a * dr;
+      dz[h] = a * (dr * dap[b][h] - S.T[h]) * (s > 0.f ? 1.f : P.slope);
+#pragma unroll
+      for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[b][k]);
+    }
+    const float t = lane_flt(M.t, j);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const Slot s = L.sl[k];
+      if (s.kind != kNode && s.kind != kTime) continue;
+      if (s.kind == kNode && P.d_node == nullptr) continue;
+      float4 dx = f4_zero();
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        fma4(dx, ad[h], S.g[h][k]);
+        fma4(dx, dz[h], S.q[h][k]);
+      }
+      if (s.kind == kNode) {
+        float* drow = P.d_node + e * P.ld_dnode + s.off;
+        if (P.dnode_vec && s.valid == 4) {
+          *reinterpret_cast<float4*>(drow) = dx;
+        } else {
+          if (s.valid > 0) drow[0] = dx.x;
+          if (s.valid > 1) drow[1] = dx.y;
+          if (s.valid > 2) drow[2] = dx.z;
+          if (s.valid > 3) drow[3] = dx.w;
+        }
+      } else {
+        // d cos(w t + b) = -sin(w t + b) * (t dw + db); the pad dims carry dx = 0.
+        const float4 sn = *reinterpret_cast<const float4*>(ts + b * P.tvs + s.off);
+        const float4 pr = make_float4(sn.x * dx.x, sn.y * dx.y, sn.z * dx.z, sn.w * dx.w);
+        S.gb[k].x += pr.x;
+        S.gb[k].y += pr.y;
+        S.gb[k].z += pr.z;
+        S.gb[k].w += pr.w;
+        fma4(S.gw[k], t, pr);
+      }
+    }
+  }
+}
+
+template <int H, int NS>
+__global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams P) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x / kWave;
+  float* tc = lds + wave * (2 * kBatch * P.tvs);
+  float* ts = tc + kBatch * P.tvs;
+  float* red = lds + kWavesPerBlock * 2 * kBatch * P.tvs;
+
+  LaneCtx<NS> L;
+  setup_lane<NS>(P, L);
+  zero_time_pad(P, tc, 2 * kBatch);
+  BwdState<H, NS> S;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) { S.gw[k] = f4_zero(); S.gb[k] = f4_zero(); }
 
   const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
-  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block; v < P.n_dst;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; v < P.n_dst;
        v += total_waves) {
     const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
     const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
-    float4 dq[H][NS];
 #pragma unroll
     for (int h = 0; h < H; ++h)
 #pragma unroll
-      for (int k = 0; k < NS; ++k) dq[h][k] = f4_zero();
+      for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
     if (e1 <= e0) {
-      store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, dq, P.cp);
+      store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq, P.cp);
       continue;
     }
-    float4 q[H][NS], g[H][NS];
-    load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, q, P.cp);
-    load_rows<H, NS>(P.dxbar, P.dxbar_hs, v, P.kp, g, P.cp);
-    float mh[H], lh[H], T[H];
+    load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q, P.cp);
+    load_rows<H, NS>(P.dxbar, P.dxbar_hs, v, P.kp, S.g, P.cp);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      mh[h] = P.stats[(v * H + h) * 2 + 0];
-      lh[h] = P.stats[(v * H + h) * 2 + 1];
-      T[h] = 0.f;
+      S.mh[h] = P.stats[(v * H + h) * 2 + 0];
+      S.lh[h] = P.stats[(v * H + h) * 2 + 1];
+    }
+    {
+      float4 xb[H][NS];
+      load_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, xb, P.cp);
+#pragma unroll
+      for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xb[h]));
     }
 
-    // Pass 1: T_h.
-    for (int64_t eb = e0; eb < e1; eb += kBatch) {
-      const int nb = static_cast<int>(e1 - eb < kBatch ? e1 - eb : kBatch);
-      float4 x[kBatch][NS];
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        if (b < nb) gather_x<NS>(P, sl, tw, tb, eb + b, x[b]);
-        else
-#pragma unroll
-          for (int k = 0; k < NS; ++k) x[b][k] = f4_zero();
-      }
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        float dap[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) dap[h] = wave_sum(head_dot<H, NS>(g, x[b], h));
-        if (b < nb) {
-          const int64_t e = eb + b;
-#pragma unroll
-          for (int h = 0; h < H; ++h) {
-            const float a = expf(P.scores[e * H + h] - mh[h]) / lh[h];
-            const float dr = P.drop ? P.drop[e * H + h] : 1.f;
-            T[h] = fmaf(a * dr, dap[h], T[h]);
-          }
+    for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
+      const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      EdgeMeta<H, true> M;
+      stage_meta<H, true>(P, c0, cnt, M);
+      float4 xa[kBatch][NS], xb[kBatch][NS];
+      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+      for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
+        const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
+        const int nb2 = cnt - jb - kBatch;
+        const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
+        if (nb > 0) issue_rows<NS, H, true>(P, L, M, jb + kBatch, nb, xb);
+        bwd_batch<H, NS>(P, L, M, c0, jb, na, tc, ts, xa, S);
+        if (nb > 0) {
+          const int nn2 = cnt - jb - 2 * kBatch;
+          const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
+          if (nn > 0) issue_rows<NS, H, true>(P, L, M, jb + 2 * kBatch, nn, xa);
+          bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, S);
         }
       }
     }
-
-    // Pass 2: dqt and dx_e.
-    for (int64_t eb = e0; eb < e1; eb += kBatch) {
-      const int nb = static_cast<int>(e1 - eb < kBatch ? e1 - eb : kBatch);
-      float4 x[kBatch][NS];
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        if (b < nb) gather_x<NS>(P, sl, tw, tb, eb + b, x[b]);
-        else
-#pragma unroll
-          for (int k = 0; k < NS; ++k) x[b][k] = f4_zero();
-      }
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        float dap[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) dap[h] = wave_sum(head_dot<H, NS>(g, x[b], h));
-        if (b >= nb) continue;
-        const int64_t e = eb + b;
-        float ad[H], dz[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-          const float s = P.scores[e * H + h];
-          const float a = expf(s - mh[h]) / lh[h];
-          const float dr = P.drop ? P.drop[e * H + h] : 1.f;
-          ad[h] = a * dr;
-          dz[h] = a * (dr * dap[h] - T[h]) * (s > 0.f ? 1.f : P.slope);
-#pragma unroll
-          for (int k = 0; k < NS; ++k) fma4(dq[h][k], dz[h], x[b][k]);
-        }
-        const float t = P.dt_dim > 0 ? P.dt[e] : 0.f;
-#pragma unroll
-        for (int k = 0; k < NS; ++k) {
-          const Slot s = sl[k];
-          if (s.kind != kNode && s.kind != kTime) continue;
-          if (s.kind == kNode && P.d_node == nullptr) continue;
-          float4 dx = f4_zero();
-#pragma unroll
-          for (int h = 0; h < H; ++h) {
-            fma4(dx, ad[h], g[h][k]);
-            fma4(dx, dz[h], q[h][k]);
-          }
-          if (s.kind == kNode) {
-            float* drow = P.d_node + e * P.ld_dnode + s.off;
-            if (P.dnode_vec && s.valid == 4) {
-              *reinterpret_cast<float4*>(drow) = dx;
-            } else {
-              if (s.valid > 0) drow[0] = dx.x;
-              if (s.valid > 1) drow[1] = dx.y;
-              if (s.valid > 2) drow[2] = dx.z;
-              if (s.valid > 3) drow[3] = dx.w;
-            }
-          } else {
-            // d cos(w t + b) = -sin(w t + b) * (t dw + db)
-            float sn;
-            if (s.valid > 0) { sn = -sinf(time_arg(t, tw[k].x, tb[k].x)) * dx.x; gb[k].x += sn; gw[k].x = fmaf(sn, t, gw[k].x); }
-            if (s.valid > 1) { sn = -sinf(time_arg(t, tw[k].y, tb[k].y)) * dx.y; gb[k].y += sn; gw[k].y = fmaf(sn, t, gw[k].y); }
-            if (s.valid > 2) { sn = -sinf(time_arg(t, tw[k].z, tb[k].z)) * dx.z; gb[k].z += sn; gw[k].z = fmaf(sn, t, gw[k].z); }
-            if (s.valid > 3) { sn = -sinf(time_arg(t, tw[k].w, tb[k].w)) * dx.w; gb[k].w += sn; gw[k].w = fmaf(sn, t, gw[k].w); }
-          }
-        }
-      }
-    }
-    store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, dq, P.cp);
+    store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq, P.cp);
   }
 
   // Time-grad partials of this workgroup: waves combined in a fixed order.
   if (P.dt_dim <= 0) return;
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
-    const int base = (lane + k * kWave) * 4;
-    red[wave_in_block][0][base + 0] = gw[k].x; red[wave_in_block][1][base + 0] = gb[k].x;
-    red[wave_in_block][0][base + 1] = gw[k].y; red[wave_in_block][1][base + 1] = gb[k].y;
-    red[wave_in_block][0][base + 2] = gw[k].z; red[wave_in_block][1][base + 2] = gb[k].z;
-    red[wave_in_block][0][base + 3] = gw[k].w; red[wave_in_block][1][base + 3] = gb[k].w;
+    if (L.sl[k].kind != kTime) continue;
+    const int o = L.sl[k].off;
+    float* rw = red + (wave * 2 + 0) * P.tvs + o;
+    float* rb = red + (wave * 2 + 1) * P.tvs + o;
+    rw[0] = S.gw[k].x; rw[1] = S.gw[k].y; rw[2] = S.gw[k].z; rw[3] = S.gw[k].w;
+    rb[0] = S.gb[k].x; rb[1] = S.gb[k].y; rb[2] = S.gb[k].z; rb[3] = S.gb[k].w;
   }
   __syncthreads();
-  // K-space column of time dim j: 4*(cn+ce) + j.
-  const int tbase = 4 * (P.cn + P.ce);
   for (int idx = threadIdx.x; idx < 2 * P.dt_dim; idx += kBlock) {
     const int which = idx / P.dt_dim;
     const int j = idx - which * P.dt_dim;
     float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) sum += red[w][which][tbase + j];
+    for (int w = 0; w < kWavesPerBlock; ++w) sum += red[(w * 2 + which) * P.tvs + j];
     P.partial[(static_cast<int64_t>(blockIdx.x) * 2 + which) * P.dt_dim + j] = sum;
   }
 }
@@ -512,6 +674,7 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_h
   P.ce = static_cast<int>(ceil_div(g->de, 4));
   P.ct = static_cast<int>(ceil_div(g->dt_dim, 4));
   P.cp = P.cn + P.ce + P.ct + 1;
+  P.tvs = 4 * P.ct;
   P.kp = 4 * static_cast<int64_t>(P.cp);
   P.qt = qt; P.qt_hs = qt_hs; P.slope = slope; P.drop = drop;
   if (!aligned16(qt)) return FA_EALIGN;
@@ -519,19 +682,30 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_h
   return FA_OK;
 }
 
+size_t fwd_lds_bytes(const TgatParams& P) {
+  return sizeof(float) * static_cast<size_t>(kWavesPerBlock) * kBatch * P.tvs;
+}
+
+size_t bwd_lds_bytes(const TgatParams& P) {
+  return sizeof(float) * static_cast<size_t>(kWavesPerBlock) * (2 * kBatch + 2) * P.tvs;
+}
+
 template <int H>
 int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
   const dim3 grid(static_cast<unsigned>(ceil_div(P.n_dst, kWavesPerBlock)));
+  const size_t lds = fwd_lds_bytes(P);
   switch (ns) {
-    case 1: hipLaunchKernelGGL((tgat_fwd<H, 1>), grid, dim3(kBlock), 0, stream, P); break;
-    case 2: hipLaunchKernelGGL((tgat_fwd<H, 2>), grid, dim3(kBlock), 0, stream, P); break;
-    case 3: hipLaunchKernelGGL((tgat_fwd<H, 3>), grid, dim3(kBlock), 0, stream, P); break;
-    case 4: hipLaunchKernelGGL((tgat_fwd<H, 4>), grid, dim3(kBlock), 0, stream, P); break;
+    case 1: hipLaunchKernelGGL((tgat_fwd<H, 1>), grid, dim3(kBlock), lds, stream, P); break;
+    case 2: hipLaunchKernelGGL((tgat_fwd<H, 2>), grid, dim3(kBlock), lds, stream, P); break;
+    case 3: hipLaunchKernelGGL((tgat_fwd<H, 3>), grid, dim3(kBlock), lds, stream, P); break;
+    case 4: hipLaunchKernelGGL((tgat_fwd<H, 4>), grid, dim3(kBlock), lds, stream, P); break;
     default: return FA_EUNSUPPORTED;
   }
   return launch_status();
 }
+
+constexpr size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup used by the fused kernels
 
 int bwd_grid(int64_t n_dst) {
   const int64_t want = ceil_div(n_dst, kWavesPerBlock);
@@ -541,11 +715,12 @@ int bwd_grid(int64_t n_dst) {
 template <int H>
 int launch_bwd_h(const TgatParams& P, int grid, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
+  const size_t lds = bwd_lds_bytes(P);
   switch (ns) {
-    case 1: hipLaunchKernelGGL((tgat_bwd<H, 1>), dim3(grid), dim3(kBlock), 0, stream, P); break;
-    case 2: hipLaunchKernelGGL((tgat_bwd<H, 2>), dim3(grid), dim3(kBlock), 0, stream, P); break;
-    case 3: hipLaunchKernelGGL((tgat_bwd<H, 3>), dim3(grid), dim3(kBlock), 0, stream, P); break;
-    case 4: hipLaunchKernelGGL((tgat_bwd<H, 4>), dim3(grid), dim3(kBlock), 0, stream, P); break;
+    case 1: hipLaunchKernelGGL((tgat_bwd<H, 1>), dim3(grid), dim3(kBlock), lds, stream, P); break;
+    case 2: hipLaunchKernelGGL((tgat_bwd<H, 2>), dim3(grid), dim3(kBlock), lds, stream, P); break;
+    case 3: hipLaunchKernelGGL((tgat_bwd<H, 3>), dim3(grid), dim3(kBlock), lds, stream, P); break;
+    case 4: hipLaunchKernelGGL((tgat_bwd<H, 4>), dim3(grid), dim3(kBlock), lds, stream, P); break;
     default: return FA_EUNSUPPORTED;
   }
   return launch_status();
@@ -569,6 +744,7 @@ extern "C" int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const
   int st = fill_params(g, heads, qt, qt_hs, slope, drop, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) return FA_OK;
+  if (fwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
   if (!xbar || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
   if (!aligned16(xbar) || (xbar_hs & 3) || (heads > 1 && xbar_hs < P.kp * P.n_dst)) return FA_EALIGN;
   P.xbar = xbar; P.xbar_hs = xbar_hs; P.scores = scores; P.stats = stats;
@@ -600,10 +776,11 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
 
 extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                                     int64_t qt_hs, float slope, const float* drop,
-                                    const float* scores, const float* stats, const float* dxbar,
-                                    int64_t dxbar_hs, float* dqt, int64_t dqt_hs, float* d_node,
-                                    int64_t ld_dnode, float* d_time_w, float* d_time_b,
-                                    void* scratch, size_t scratch_bytes, hipStream_t stream) {
+                                    const float* xbar, int64_t xbar_hs, const float* scores,
+                                    const float* stats, const float* dxbar, int64_t dxbar_hs,
+                                    float* dqt, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
+                                    float* d_time_w, float* d_time_b, void* scratch,
+                                    size_t scratch_bytes, hipStream_t stream) {
   TgatParams P;
   int st = fill_params(g, heads, qt, qt_hs, slope, drop, P);
   if (st != FA_OK) return st;
@@ -614,15 +791,21 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
     }
     return launch_status();
   }
-  if (!dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if (!aligned16(dxbar) || !aligned16(dqt) || (dxbar_hs & 3) || (dqt_hs & 3)) return FA_EALIGN;
-  if (heads > 1 && (dxbar_hs < P.kp * P.n_dst || dqt_hs < P.kp * P.n_dst)) return FA_EALIGN;
+  if (bwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
+  if (!xbar || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
+  if (!aligned16(xbar) || !aligned16(dxbar) || !aligned16(dqt) || (xbar_hs & 3) || (dxbar_hs & 3) ||
+      (dqt_hs & 3))
+    return FA_EALIGN;
+  if (heads > 1 &&
+      (xbar_hs < P.kp * P.n_dst || dxbar_hs < P.kp * P.n_dst || dqt_hs < P.kp * P.n_dst))
+    return FA_EINVAL;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
   P.dnode_vec = d_node && aligned16(d_node) && (ld_dnode & 3) == 0;
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   const int grid = bwd_grid(P.n_dst);
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
+  P.xbar = const_cast<float*>(xbar); P.xbar_hs = xbar_hs;
   P.dxbar = dxbar; P.dxbar_hs = dxbar_hs; P.dqt = dqt; P.dqt_hs = dqt_hs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
   P.stats = const_cast<float*>(stats); P.partial = static_cast<float*>(scratch);

@@ -186,14 +186,14 @@ def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, head
                + node row (4*dn) + edge row (4*de) + score (4*heads, written / read)
                [+ d_node row (4*dn) written in backward when requested]
     per dst  : forward  qt read + xbar written (2 * 4*heads*Kp) + stats written (8*heads)
-               backward qt, dxbar read + dqt written (3 * 4*heads*Kp) + stats read (8*heads)
+               backward qt, xbar, dxbar read + dqt written (4 * 4*heads*Kp) + stats read (8*heads)
     plus the row offsets 4*(n_dst+1) and the time parameters 8*dt."""
     kp = kspace_width(dn, de, dt)
     edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + 4 * dn + 4 * de
     common = 4 * (n_dst + 1) + 8 * dt
     fwd = common + n_edges * (edge_in + 4 * heads) + n_dst * (2 * 4 * heads * kp + 8 * heads)
     bwd = (common + n_edges * (edge_in + 4 * heads + (4 * dn if d_node else 0))
-           + n_dst * (3 * 4 * heads * kp + 8 * heads))
+           + n_dst * (4 * 4 * heads * kp + 8 * heads))
     return {"fwd": fwd, "bwd": bwd}
 
 
@@ -274,7 +274,7 @@ class TgatAttention(torch.autograd.Function):
         ctx.g = g
         ctx.slope = float(slope)
         ctx.has_drop = drop is not None
-        saved = [qt, time_w, time_b, node_src, scores, stats]
+        saved = [qt, time_w, time_b, node_src, xbar, scores, stats]
         if drop is not None:
             saved.append(drop)
         ctx.save_for_backward(*saved)
@@ -283,16 +283,16 @@ class TgatAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dxbar):
         saved = ctx.saved_tensors
-        qt, time_w, time_b, node_src, scores, stats = saved[:6]
-        drop = saved[6] if ctx.has_drop else None
+        qt, time_w, time_b, node_src, xbar, scores, stats = saved[:7]
+        drop = saved[7] if ctx.has_drop else None
         g = ctx.g
         need_node = ctx.needs_input_grad[3] and node_src.shape[1] > 0
         dxbar = dxbar.contiguous()
         t0 = timer.begin() if timer is not None else None
         dqt, d_node, d_tw, d_tb = fastAgg.tgat_attn_bwd(g.rowptr, node_src, g.node_idx,
                                                         g.edge_tab, g.edge_idx, g.dt, time_w,
-                                                        time_b, qt, ctx.slope, drop, scores,
-                                                        stats, dxbar, need_node)
+                                                        time_b, qt, ctx.slope, drop, xbar,
+                                                        scores, stats, dxbar, need_node)
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[0],

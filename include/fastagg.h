@@ -212,17 +212,18 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
                              const float* scores, const float* stats, float* att,
                              hipStream_t stream);
 
-/* Backward. dxbar: gradient of xbar (same layout, head stride dxbar_hs).
+/* Backward, one pass over the edges. xbar: the forward output (its dot product with dxbar
+ * gives each destination's softmax correction); dxbar: gradient of xbar (same layout).
  * Outputs: dqt (layout of qt, head stride dqt_hs); d_node [n_edges][ld_dnode] gradient of
  * the node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be
  * NULL when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_hs, float slope, const float* drop, const float* scores,
-                         const float* stats, const float* dxbar, int64_t dxbar_hs, float* dqt,
-                         int64_t dqt_hs, float* d_node, int64_t ld_dnode, float* d_time_w,
-                         float* d_time_b, void* scratch, size_t scratch_bytes,
-                         hipStream_t stream);
+                         int64_t qt_hs, float slope, const float* drop, const float* xbar,
+                         int64_t xbar_hs, const float* scores, const float* stats,
+                         const float* dxbar, int64_t dxbar_hs, float* dqt, int64_t dqt_hs,
+                         float* d_node, int64_t ld_dnode, float* d_time_w, float* d_time_b,
+                         void* scratch, size_t scratch_bytes, hipStream_t stream);
 
 /* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
 int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,

@@ -97,6 +97,28 @@ __device__ __forceinline__ float time_arg(float t, float w, float b) {
   return t * w + b;
 }
 
+// Counter-based dropout: keep entry i with probability 1-p, decided by a 32-bit hash of
+// (seed, i) (two rounds of the murmur3 finaliser). u = top 24 bits / 2^24 in [0, 1);
+// kept when u >= p. The same function runs on the host side of the tests.
+__host__ __device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x;
+}
+
+__host__ __device__ inline uint32_t drop_hash(uint64_t seed, uint64_t i) {
+  uint32_t x = mix32(static_cast<uint32_t>(i) ^ static_cast<uint32_t>(seed));
+  return mix32(x + static_cast<uint32_t>(seed >> 32) + static_cast<uint32_t>(i >> 32) * 0x9e3779b9u);
+}
+
+__host__ __device__ inline float drop_mult(uint64_t seed, uint64_t i, float p, float scale) {
+  const float u = static_cast<float>(drop_hash(seed, i) >> 8) * (1.0f / 16777216.0f);
+  return u >= p ? scale : 0.f;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int launch_status() {

@@ -560,7 +560,8 @@ std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> node_idx, at::Tensor edge_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
                                       at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
-                                      double slope, std::optional<at::Tensor> drop) {
+                                      double slope, std::optional<at::Tensor> drop,
+                                      uint64_t drop_seed, double drop_p) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
   const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
@@ -577,8 +578,9 @@ std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
   auto scores = at::empty({g.n_edges, H}, qt.options());
   auto stats = at::empty({g.n_dst, H, 2}, qt.options());
   const int st = fa_tgat_attn_fwd_f32(&g, static_cast<int32_t>(H), qt.data_ptr<float>(),
-                                      qt.stride(0), static_cast<float>(slope), dptr,
-                                      xbar.data_ptr<float>(), xbar.stride(0),
+                                      qt.stride(0), static_cast<float>(slope), dptr, drop_seed,
+                                      static_cast<float>(drop_p), xbar.data_ptr<float>(),
+                                      xbar.stride(0),
                                       scores.data_ptr<float>(), stats.data_ptr<float>(),
                                       stream_of(qt));
   check_status(st, "tgat_attn_fwd");
@@ -591,8 +593,9 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
                                       at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
                                       double slope, std::optional<at::Tensor> drop,
-                                      at::Tensor xbar, at::Tensor scores, at::Tensor stats,
-                                      at::Tensor dxbar, bool need_d_node) {
+                                      uint64_t drop_seed, double drop_p, at::Tensor xbar,
+                                      at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
+                                      bool need_d_node) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
   const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
@@ -619,7 +622,8 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
   auto scratch = at::empty({static_cast<int64_t>(sb)}, qt.options().dtype(at::kByte));
   const int st = fa_tgat_attn_bwd_f32(
       &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(0), static_cast<float>(slope),
-      dptr, xbar.data_ptr<float>(), xbar.stride(0), scores.data_ptr<float>(),
+      dptr, drop_seed, static_cast<float>(drop_p), xbar.data_ptr<float>(), xbar.stride(0),
+      scores.data_ptr<float>(),
       stats.data_ptr<float>(), dxbar.data_ptr<float>(),
       dxbar.stride(0), dqt.data_ptr<float>(), dqt.stride(0),
       need_d_node && g.n_edges > 0 && g.dn > 0 ? d_node.data_ptr<float>() : nullptr,
@@ -627,6 +631,19 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
       sb, stream_of(qt));
   check_status(st, "tgat_attn_bwd");
   return {dqt, need_d_node ? d_node : at::Tensor(), d_tw, d_tb};
+}
+
+// [n_edges, heads] multipliers of the hashed attention dropout (keep/(1-p) or 0).
+at::Tensor dropout_mask(int64_t n_edges, int64_t heads, uint64_t seed, double p, at::Device device) {
+  TORCH_CHECK(n_edges >= 0 && heads > 0, "n_edges must be >= 0 and heads > 0");
+  TORCH_CHECK(p >= 0.0 && p < 1.0, "p must lie in [0, 1)");
+  TORCH_CHECK(device.is_cuda(), "device must be a GPU");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+  auto out = at::empty({n_edges, heads}, at::TensorOptions().dtype(at::kFloat).device(device));
+  const int st = fa_dropout_mask_f32(seed, static_cast<float>(p), n_edges * heads,
+                                     out.data_ptr<float>(), stream_of(out));
+  check_status(st, "dropout_mask");
+  return out;
 }
 
 at::Tensor tgat_attn_weights(at::Tensor dst, at::Tensor scores, at::Tensor stats) {
@@ -728,12 +745,14 @@ PYBIND11_MODULE(fastAgg, m) {
         "fused gather + time encoding + score + segment softmax + aggregation (forward)",
         py::arg("rowptr"), py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"),
         py::arg("edge_idx"), py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"),
-        py::arg("slope"), py::arg("drop"));
+        py::arg("slope"), py::arg("drop"), py::arg("drop_seed") = 0, py::arg("drop_p") = 0.0);
   m.def("tgat_attn_bwd", &tgat_attn_bwd, "backward of tgat_attn_fwd", py::arg("rowptr"),
         py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"), py::arg("edge_idx"),
         py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"), py::arg("slope"),
-        py::arg("drop"), py::arg("xbar"), py::arg("scores"), py::arg("stats"), py::arg("dxbar"),
-        py::arg("need_d_node"));
+        py::arg("drop"), py::arg("drop_seed"), py::arg("drop_p"), py::arg("xbar"),
+        py::arg("scores"), py::arg("stats"), py::arg("dxbar"), py::arg("need_d_node"));
+  m.def("dropout_mask", &dropout_mask, "multipliers of the hashed attention dropout",
+        py::arg("n_edges"), py::arg("heads"), py::arg("seed"), py::arg("p"), py::arg("device"));
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
         py::arg("dst"), py::arg("scores"), py::arg("stats"));
   m.def("gather_rows", &gather_rows, "row gather tab[idx]", py::arg("tab"), py::arg("idx"),

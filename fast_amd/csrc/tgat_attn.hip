@@ -12,6 +12,11 @@
 // [cn+ce, cn+ce+ct), then one bias chunk (1,0,0,0). One wavefront per destination;
 // lane l owns chunks l, l+64, ... (NS slots).
 //
+// Every lane runs the same instruction stream in the edge loops: gathers are buffer loads
+// through a per-row descriptor (lanes whose chunk lies in the other table, or a row out of
+// range, read zeros), per-destination rows are buffer loads / stores bounded by the row
+// length, and the per-lane chunk kinds are applied with selects.
+//
 // Latency structure: the per-edge ids, dt, dropout multipliers (and scores in backward) of
 // up to 64 edges are loaded with one coalesced vector load per array and broadcast with
 // readlane; row gathers run two batches deep (the next batch's loads are in flight while
@@ -46,20 +51,22 @@ enum ChunkKind : int { kNode = 0, kEdge = 1, kTime = 2, kBias = 3, kNone = 4 };
 #endif
 constexpr int kBatch = FA_TGAT_BATCH;
 constexpr int kBwdMaxBlocks = 2048;   // backward grid cap (time-grad partial rows)
+constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every descriptor's range
 
 struct TgatParams {
   int64_t n_dst, n_edges;
   const int32_t* rowptr;
   const float* node_tab; int64_t ld_node; int64_t n_node; int dn; const int64_t* node_idx;
   const float* edge_tab; int64_t ld_edge; int64_t n_erow; int de; const int64_t* edge_idx;
-  int node_vec, edge_vec, dnode_vec;  // rows 16-byte aligned: float4 access allowed
+  int node_tail, edge_tail;           // row width not a multiple of 4: per-dword access
   const float* dt; const float* time_w; const float* time_b; int dt_dim;
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
-  int tvs;                            // LDS row stride of the time tiles (4*ct)
+  int tvs;                            // LDS row stride of the tiles: 4*ct + bias chunk + zero chunk
   int64_t kp;                         // row stride of qt / xbar = 4*cp
   const float* qt; int64_t qt_hs;
   float slope;
-  const float* drop;
+  const float* drop;                  // explicit [E][H] multipliers, or
+  uint64_t drop_seed; float drop_p, drop_scale; int drop_hash;  // hashed dropout
   // forward outputs / backward input
   float* xbar; int64_t xbar_hs;
   float* scores; float* stats;
@@ -70,39 +77,52 @@ struct TgatParams {
   float* partial;                     // [gridDim.x][2][dt_dim]
 };
 
-// What a lane holds in slot k: kind, element offset inside its part, valid count.
-struct Slot {
-  int kind, off, valid;
-};
+// ----- buffer access -------------------------------------------------------------------
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (unformatted) 32-bit buffer
 
-__device__ __forceinline__ Slot classify(const TgatParams& P, int c) {
-  Slot s;
-  if (c < P.cn) {
-    s.kind = kNode; s.off = 4 * c; s.valid = min(4, P.dn - s.off);
-  } else if (c < P.cn + P.ce) {
-    s.kind = kEdge; s.off = 4 * (c - P.cn); s.valid = min(4, P.de - s.off);
-  } else if (c < P.cn + P.ce + P.ct) {
-    s.kind = kTime; s.off = 4 * (c - P.cn - P.ce); s.valid = min(4, P.dt_dim - s.off);
-  } else if (c == P.cn + P.ce + P.ct) {
-    s.kind = kBias; s.off = 0; s.valid = 1;
-  } else {
-    s.kind = kNone; s.off = 0; s.valid = 0;
-  }
-  return s;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kRsrcWord3);
+}
+
+__device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                     __uint_as_float(v[3]));
+}
+
+// Four dword stores: each dword is range-checked on its own, so a chunk that crosses the end
+// of the row writes only its in-range part.
+__device__ __forceinline__ void bstore4_dwords(rsrc_t r, uint32_t off, const float4& x) {
+  const int o = static_cast<int>(off);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
+}
+
+__device__ __forceinline__ void bstore4(rsrc_t r, uint32_t off, const float4& x) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  u4 v;
+  v[0] = __float_as_uint(x.x);
+  v[1] = __float_as_uint(x.y);
+  v[2] = __float_as_uint(x.z);
+  v[3] = __float_as_uint(x.w);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
+}
+
+__device__ __forceinline__ float4 sel4(bool c, const float4& a, const float4& b) {
+  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
+// Keeps the first `valid` components (a chunk that crosses the end of a feature row).
+__device__ __forceinline__ float4 keep_first(const float4& v, int valid) {
+  return make_float4(v.x, valid > 1 ? v.y : 0.f, valid > 2 ? v.z : 0.f, valid > 3 ? v.w : 0.f);
 }
 
 __device__ __forceinline__ int64_t clamp_edge(int64_t e, int64_t n_edges) {
   return e < 0 ? 0 : (e > n_edges ? n_edges : e);
-}
-
-__device__ __forceinline__ float4 load_row_chunk(const float* row, int off, int valid, int vec) {
-  if (vec && valid == 4) return *reinterpret_cast<const float4*>(row + off);
-  float4 v = f4_zero();
-  if (valid > 0) v.x = row[off];
-  if (valid > 1) v.y = row[off + 1];
-  if (valid > 2) v.z = row[off + 2];
-  if (valid > 3) v.w = row[off + 3];
-  return v;
 }
 
 // Orders this wave's LDS accesses across lanes of the same wave.
@@ -117,10 +137,18 @@ __device__ __forceinline__ float lane_flt(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-// Per-lane constants: slot kinds and the time parameters of the dims this lane encodes.
+// ----- per-lane chunk bookkeeping ------------------------------------------------------
+// Each lane owns the K-space chunks lane + 64k (slot k). Row chunks (node / edge feature
+// rows) come from global memory; every other chunk is read from the wave's LDS tile row of
+// the edge, laid out as [time chunks (ct) | bias chunk (1,0,0,0) | zero chunk], so a lane
+// picks between two values with one select and no branch.
 template <int NS>
 struct LaneCtx {
-  Slot sl[NS];
+  uint32_t noff[NS];      // byte offset in the node row (kOob elsewhere; gradient stores)
+  int roff[NS];           // element offset of a row chunk inside its row (0 elsewhere)
+  uint32_t toff[NS];      // element offset of the chunk in the LDS tile row (zero chunk for rows)
+  int valid[NS];          // valid components of a row chunk (4 elsewhere)
+  bool is_node[NS], is_edge[NS];
   float w0, b0, w1, b1;   // time dims j = lane and lane + 64
 };
 
@@ -128,21 +156,51 @@ template <int NS>
 __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) {
   const int lane = lane_id();
 #pragma unroll
-  for (int k = 0; k < NS; ++k) L.sl[k] = classify(P, lane + k * kWave);
+  for (int k = 0; k < NS; ++k) {
+    const int c = lane + k * kWave;
+    L.noff[k] = kOob;
+    L.roff[k] = 0;
+    L.toff[k] = 4u * static_cast<uint32_t>(P.ct + 1);
+    L.valid[k] = 4;
+    L.is_node[k] = false;
+    L.is_edge[k] = false;
+    if (c < P.cn) {
+      L.noff[k] = 16u * static_cast<uint32_t>(c);
+      L.roff[k] = 4 * c;
+      L.valid[k] = min(4, P.dn - 4 * c);
+      L.is_node[k] = true;
+    } else if (c < P.cn + P.ce) {
+      L.roff[k] = 4 * (c - P.cn);
+      L.valid[k] = min(4, P.de - 4 * (c - P.cn));
+      L.is_edge[k] = true;
+    } else if (c < P.cn + P.ce + P.ct) {
+      L.toff[k] = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
+    } else if (c == P.cn + P.ce + P.ct) {
+      L.toff[k] = 4u * static_cast<uint32_t>(P.ct);
+    }
+  }
   L.w0 = lane < P.dt_dim ? P.time_w[lane] : 0.f;
   L.b0 = lane < P.dt_dim ? P.time_b[lane] : 0.f;
   L.w1 = lane + kWave < P.dt_dim ? P.time_w[lane + kWave] : 0.f;
   L.b1 = lane + kWave < P.dt_dim ? P.time_b[lane + kWave] : 0.f;
 }
 
-// Zeroes the padding dims [dt_dim, tvs) of `rows` rows of this wave's time tiles.
-__device__ __forceinline__ void zero_time_pad(const TgatParams& P, float* tile, int rows) {
+// Writes the constant part [dt_dim, tvs) of `rows` rows of this wave's tiles: time padding
+// and the zero chunk get 0; the bias chunk gets (1,0,0,0) in the first `cos_rows` rows
+// (cosine tiles) and zeros in the others (-sin tiles, whose non-time chunks must be 0).
+__device__ __forceinline__ void init_tiles(const TgatParams& P, float* tile, int rows,
+                                           int cos_rows) {
   const int lane = lane_id();
   const int pad = P.tvs - P.dt_dim;
-  if (pad <= 0) return;
-  for (int i = lane; i < rows * pad; i += kWave) tile[(i / pad) * P.tvs + P.dt_dim + i % pad] = 0.f;
+  for (int i = lane; i < rows * pad; i += kWave) {
+    const int r = i / pad;
+    const int j = P.dt_dim + (i - r * pad);
+    tile[r * P.tvs + j] = (j == 4 * P.ct && r < cos_rows) ? 1.f : 0.f;
+  }
+  lds_sync();
 }
 
+// ----- per-edge metadata ---------------------------------------------------------------
 // Per-lane metadata of up to 64 consecutive edges c0 + lane: row ids (split in 32-bit
 // halves for readlane), dt, dropout multipliers and (backward) scores.
 template <int H, bool SCORES>
@@ -167,7 +225,10 @@ __device__ __forceinline__ void stage_meta(const TgatParams& P, int64_t c0, int 
   M.t = P.dt_dim > 0 ? P.dt[e] : 0.f;
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    M.dr[h] = P.drop ? P.drop[e * H + h] : 1.f;
+    float dr = 1.f;
+    if (P.drop) dr = P.drop[e * H + h];
+    else if (P.drop_hash) dr = drop_mult(P.drop_seed, static_cast<uint64_t>(e * H + h), P.drop_p, P.drop_scale);
+    M.dr[h] = dr;
     M.sc[h] = SCORES ? P.scores[e * H + h] : 0.f;
   }
 }
@@ -184,12 +245,21 @@ __device__ __forceinline__ int64_t meta_edge(const EdgeMeta<H, SCORES>& M, int j
                               static_cast<uint32_t>(lane_int(M.elo, j)));
 }
 
-// Issues the node / edge chunk loads of batch entries [jb, jb+nb) (time and bias chunks
-// are filled in later by fill_x).
+// Four dword loads of row[o..o+3] with the indices clamped into the row (the components past
+// its end are zeroed later), for rows whose width is not a multiple of 4.
+__device__ __forceinline__ float4 load4_clamped(const float* row, int o, int last) {
+  return make_float4(row[min(o, last)], row[min(o + 1, last)], row[min(o + 2, last)],
+                     row[min(o + 3, last)]);
+}
+
+// Issues the row-chunk loads of batch entries [jb, jb+nb): one load per slot from a per-lane
+// address (node row or edge row).
+// ok[b] bit 0 / 1: the node / edge row of entry b is in range (rows out of range are read
+// as row 0 and zeroed when the batch is assembled).
 template <int NS, int H, bool SCORES>
 __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS>& L,
                                            const EdgeMeta<H, SCORES>& M, int jb, int nb,
-                                           float4 (&x)[kBatch][NS]) {
+                                           float4 (&x)[kBatch][NS], int (&ok)[kBatch]) {
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b < nb) {
@@ -197,17 +267,21 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
       const int64_t erow = meta_edge(M, jb + b);
       const bool nok = nrow >= 0 && nrow < P.n_node;
       const bool eok = erow >= 0 && erow < P.n_erow;
+      ok[b] = (nok ? 1 : 0) | (eok ? 2 : 0);
+      if (P.dn + P.de == 0) continue;
       const float* nptr = P.node_tab + (nok ? nrow : 0) * P.ld_node;
       const float* eptr = P.edge_tab + (eok ? erow : 0) * P.ld_edge;
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
-        const Slot s = L.sl[k];
-        if (s.kind <= kEdge) {
-          const bool is_node = s.kind == kNode;
-          const float* row = is_node ? nptr : eptr;
-          const bool ok = is_node ? nok : eok;
-          const int vec = is_node ? P.node_vec : P.edge_vec;
-          x[b][k] = ok ? load_row_chunk(row, s.off, s.valid, vec) : f4_zero();
+        // only the lanes of row chunks load (the others take their chunk from LDS)
+        if (L.is_node[k] || L.is_edge[k]) {
+          const float* row = L.is_node[k] ? nptr : eptr;
+          if (P.node_tail || P.edge_tail) {
+            const int last = (L.is_node[k] ? P.dn : P.de) - 1;
+            x[b][k] = load4_clamped(row, L.roff[k], last);
+          } else {
+            x[b][k] = *reinterpret_cast<const float4*>(row + L.roff[k]);
+          }
         }
       }
     }
@@ -215,14 +289,17 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
 }
 
 template <bool SIN>
-__device__ __forceinline__ void encode_one(float a, float* rc, float* rs, int j) {
+__device__ __forceinline__ void encode_one(float a, float* rc, float* rs, int j, bool ok) {
   if (SIN) {
     float sv, cv;
     sincosf(a, &sv, &cv);
-    rc[j] = cv;
-    rs[j] = -sv;
+    if (ok) {
+      rc[j] = cv;
+      rs[j] = -sv;
+    }
   } else {
-    rc[j] = cosf(a);
+    const float cv = cosf(a);
+    if (ok) rc[j] = cv;
   }
 }
 
@@ -239,54 +316,65 @@ __device__ __forceinline__ void encode_times(const TgatParams& P, const LaneCtx<
     const float t = lane_flt(M.t, jb + b);
     float* rc = tc + b * P.tvs;
     float* rs = SIN ? ts + b * P.tvs : nullptr;
-    if (lane < P.dt_dim) encode_one<SIN>(time_arg(t, L.w0, L.b0), rc, rs, lane);
-    if (lane + kWave < P.dt_dim) encode_one<SIN>(time_arg(t, L.w1, L.b1), rc, rs, lane + kWave);
-    for (int j = lane + 2 * kWave; j < P.dt_dim; j += kWave)
-      encode_one<SIN>(time_arg(t, P.time_w[j], P.time_b[j]), rc, rs, j);
+    encode_one<SIN>(time_arg(t, L.w0, L.b0), rc, rs, lane, lane < P.dt_dim);
+    if (P.dt_dim > kWave)
+      encode_one<SIN>(time_arg(t, L.w1, L.b1), rc, rs, lane + kWave, lane + kWave < P.dt_dim);
+    for (int j0 = 2 * kWave; j0 < P.dt_dim; j0 += kWave) {
+      const int j = j0 + lane;
+      const int jc = j < P.dt_dim ? j : P.dt_dim - 1;
+      encode_one<SIN>(time_arg(t, P.time_w[jc], P.time_b[jc]), rc, rs, j, j < P.dt_dim);
+    }
   }
 }
 
-// Fills the time (from the LDS tile) and bias chunks of the batch, zeroes unused entries.
+// Assembles the batch's chunks: row chunks from the loads (zeroed past the row end and for
+// rows out of range), every other chunk from the LDS tile row. Entries past nb are left as
+// they are (their results are not used).
 template <int NS>
-__device__ __forceinline__ void fill_x(const TgatParams& P, const LaneCtx<NS>& L, int nb,
-                                       const float* tc, float4 (&x)[kBatch][NS]) {
+__device__ __forceinline__ void assemble_x(const TgatParams& P, const LaneCtx<NS>& L, int nb,
+                                           const float* tc, const int (&ok)[kBatch],
+                                           float4 (&x)[kBatch][NS]) {
+  const bool tails = P.node_tail || P.edge_tail;
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
+    if (b >= nb) break;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-      const Slot s = L.sl[k];
-      if (b >= nb || s.kind == kNone) x[b][k] = f4_zero();
-      else if (s.kind == kTime) x[b][k] = *reinterpret_cast<const float4*>(tc + b * P.tvs + s.off);
-      else if (s.kind == kBias) x[b][k] = make_float4(1.f, 0.f, 0.f, 0.f);
+      const float4 tv = *reinterpret_cast<const float4*>(tc + b * P.tvs + L.toff[k]);
+      float4 rv = x[b][k];
+      if (tails) rv = keep_first(rv, L.valid[k]);
+      bool row = L.is_node[k] || L.is_edge[k];
+      if (ok[b] != 3) {  // wave-uniform: an out-of-range row reads as zeros
+        const bool bad = (L.is_node[k] && !(ok[b] & 1)) || (L.is_edge[k] && !(ok[b] & 2));
+        rv = sel4(bad, f4_zero(), rv);
+      }
+      x[b][k] = sel4(row, rv, tv);
     }
   }
 }
 
 template <int H, int NS>
 __device__ __forceinline__ void load_rows(const float* base, int64_t hs, int64_t v, int64_t kp,
-                                          float4 (&r)[H][NS], int cp) {
+                                          float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
-  for (int h = 0; h < H; ++h)
+  for (int h = 0; h < H; ++h) {
+    const rsrc_t rr = make_rsrc(base + h * hs + v * kp, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
-      const int c = lane + k * kWave;
-      r[h][k] = c < cp ? *reinterpret_cast<const float4*>(base + h * hs + v * kp + 4 * c)
-                       : f4_zero();
-    }
+    for (int k = 0; k < NS; ++k) r[h][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+  }
 }
 
 template <int H, int NS>
 __device__ __forceinline__ void store_rows(float* base, int64_t hs, int64_t v, int64_t kp,
-                                           const float4 (&r)[H][NS], int cp) {
+                                           const float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
-  for (int h = 0; h < H; ++h)
+  for (int h = 0; h < H; ++h) {
+    const rsrc_t rr = make_rsrc(base + h * hs + v * kp, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
-      const int c = lane + k * kWave;
-      if (c < cp) *reinterpret_cast<float4*>(base + h * hs + v * kp + 4 * c) = r[h][k];
-    }
+    for (int k = 0; k < NS; ++k) bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), r[h][k]);
+  }
 }
 
 template <int NS>
@@ -311,14 +399,15 @@ struct FwdState {
 template <int H, int NS>
 __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
                                           const EdgeMeta<H, false>& M, int64_t c0, int jb, int nb,
-                                          float* tc, float4 (&x)[kBatch][NS], FwdState<H, NS>& S) {
+                                          float* tc, float4 (&x)[kBatch][NS],
+                                          const int (&ok)[kBatch], FwdState<H, NS>& S) {
   const int lane = lane_id();
   if (P.dt_dim > 0) {
     lds_sync();
     encode_times<NS, H, false, false>(P, L, M, jb, nb, tc, nullptr);
     lds_sync();
   }
-  fill_x<NS>(P, L, nb, tc, x);
+  assemble_x<NS>(P, L, nb, tc, ok, x);
   float sc[kBatch][H];
 #pragma unroll
   for (int b = 0; b < kBatch; ++b)
@@ -330,8 +419,7 @@ __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>
 #pragma unroll
     for (int b = 0; b < kBatch; ++b)
 #pragma unroll
-      for (int h = 0; h < H; ++h)
-        if (lane == b * H + h) mine = sc[b][h];
+      for (int h = 0; h < H; ++h) mine = (lane == b * H + h) ? sc[b][h] : mine;
     if (lane < nb * H) P.scores[(c0 + jb) * H + lane] = mine;
   }
 #pragma unroll
@@ -341,22 +429,20 @@ __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>
     for (int h = 0; h < H; ++h) {
       const float s = sc[b][h];
       const float dr = lane_flt(M.dr[h], jb + b);
+      // online softmax; s and m are wave-uniform, so this branch does not diverge. The
+      // first edge has m = -inf and r = 0.
       if (s > S.m[h]) {
-        const float r = expf(S.m[h] - s);  // 0 on the first edge
-        S.l[h] = fmaf(S.l[h], r, 1.f);
+        const float r = expf(S.m[h] - s);
+        S.l[h] *= r;
 #pragma unroll
-        for (int k = 0; k < NS; ++k) {
-          scale4(S.acc[h][k], r);
-          fma4(S.acc[h][k], dr, x[b][k]);
-        }
+        for (int k = 0; k < NS; ++k) scale4(S.acc[h][k], r);
         S.m[h] = s;
-      } else {
-        const float pe = expf(s - S.m[h]);
-        S.l[h] += pe;
-        const float w = pe * dr;
-#pragma unroll
-        for (int k = 0; k < NS; ++k) fma4(S.acc[h][k], w, x[b][k]);
       }
+      const float pe = expf(s - S.m[h]);
+      S.l[h] += pe;
+      const float w = pe * dr;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) fma4(S.acc[h][k], w, x[b][k]);
     }
   }
 }
@@ -380,7 +466,7 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams
     for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
   }
   if (e1 <= e0) {  // zero-degree destination: xbar = 0
-    store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc, P.cp);
+    store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc);
     if (lane < H) {
       P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
       P.stats[(v * H + lane) * 2 + 1] = 0.f;
@@ -391,26 +477,27 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams
   float* tc = lds + wave * (kBatch * P.tvs);
   LaneCtx<NS> L;
   setup_lane<NS>(P, L);
-  zero_time_pad(P, tc, kBatch);
-  load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q, P.cp);
+  init_tiles(P, tc, kBatch, kBatch);
+  load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q);
 
   for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
     const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
     EdgeMeta<H, false> M;
     stage_meta<H, false>(P, c0, cnt, M);
     float4 xa[kBatch][NS], xb[kBatch][NS];
-    issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    int oka[kBatch], okb[kBatch];
+    issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa, oka);
     for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
       const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
       const int nb2 = cnt - jb - kBatch;
       const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
-      if (nb > 0) issue_rows<NS, H, false>(P, L, M, jb + kBatch, nb, xb);
-      fwd_batch<H, NS>(P, L, M, c0, jb, na, tc, xa, S);
+      if (nb > 0) issue_rows<NS, H, false>(P, L, M, jb + kBatch, nb, xb, okb);
+      fwd_batch<H, NS>(P, L, M, c0, jb, na, tc, xa, oka, S);
       if (nb > 0) {
         const int nn2 = cnt - jb - 2 * kBatch;
         const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
-        if (nn > 0) issue_rows<NS, H, false>(P, L, M, jb + 2 * kBatch, nn, xa);
-        fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, S);
+        if (nn > 0) issue_rows<NS, H, false>(P, L, M, jb + 2 * kBatch, nn, xa, oka);
+        fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, okb, S);
       }
     }
   }
@@ -426,12 +513,14 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams
       S.acc[h][k].w /= lsum;
     }
   }
-  store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc, P.cp);
+  store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc);
   if (lane < H) {
     float mm = 0.f, ll = 0.f;
 #pragma unroll
-    for (int h = 0; h < H; ++h)
-      if (lane == h) { mm = S.m[h]; ll = S.l[h]; }
+    for (int h = 0; h < H; ++h) {
+      mm = lane == h ? S.m[h] : mm;
+      ll = lane == h ? S.l[h] : ll;
+    }
     P.stats[(v * H + lane) * 2 + 0] = mm;
     P.stats[(v * H + lane) * 2 + 1] = ll;
   }
@@ -446,25 +535,26 @@ template <int H, int NS>
 struct BwdState {
   float4 q[H][NS], g[H][NS], dq[H][NS];
   float4 gw[NS], gb[NS];  // time-grad accumulators of this lane's time chunks (whole wave)
-  float mh[H], lh[H], T[H];
+  float mh[H], il[H], T[H];  // row max, 1 / softmax denominator, dxbar . xbar
 };
 
 template <int H, int NS>
 __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
                                           const EdgeMeta<H, true>& M, int64_t c0, int jb, int nb,
                                           float* tc, float* ts, float4 (&x)[kBatch][NS],
-                                          BwdState<H, NS>& S) {
+                                          const int (&ok)[kBatch], BwdState<H, NS>& S) {
   if (P.dt_dim > 0) {
     lds_sync();
     encode_times<NS, H, true, true>(P, L, M, jb, nb, tc, ts);
     lds_sync();
   }
-  fill_x<NS>(P, L, nb, tc, x);
+  assemble_x<NS>(P, L, nb, tc, ok, x);
   float dap[kBatch][H];
 #pragma unroll
   for (int b = 0; b < kBatch; ++b)
 #pragma unroll
     for (int h = 0; h < H; ++h) dap[b][h] = wave_sum(row_dot<NS>(S.g[h], x[b]));
+  const int lane = lane_id();
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b >= nb) break;
@@ -475,37 +565,32 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
     for (int h = 0; h < H; ++h) {
       const float s = lane_flt(M.sc[h], j);
       const float dr = lane_flt(M.dr[h], j);
-      const float a = expf(s - S.mh[h]) / S.lh[h];
+      const float a = expf(s - S.mh[h]) * S.il[h];
       ad[h] = a * dr;
       dz[h] = a * (dr * dap[b][h] - S.T[h]) * (s > 0.f ? 1.f : P.slope);
 #pragma unroll
       for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[b][k]);
     }
     const float t = lane_flt(M.t, j);
+    const rsrc_t rd = make_rsrc(P.d_node ? P.d_node + e * P.ld_dnode : P.dxbar,
+                                P.d_node ? 4u * static_cast<uint32_t>(P.dn) : 0u);
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-      const Slot s = L.sl[k];
-      if (s.kind != kNode && s.kind != kTime) continue;
-      if (s.kind == kNode && P.d_node == nullptr) continue;
       float4 dx = f4_zero();
 #pragma unroll
       for (int h = 0; h < H; ++h) {
         fma4(dx, ad[h], S.g[h][k]);
         fma4(dx, dz[h], S.q[h][k]);
       }
-      if (s.kind == kNode) {
-        float* drow = P.d_node + e * P.ld_dnode + s.off;
-        if (P.dnode_vec && s.valid == 4) {
-          *reinterpret_cast<float4*>(drow) = dx;
-        } else {
-          if (s.valid > 0) drow[0] = dx.x;
-          if (s.valid > 1) drow[1] = dx.y;
-          if (s.valid > 2) drow[2] = dx.z;
-          if (s.valid > 3) drow[3] = dx.w;
-        }
-      } else {
-        // d cos(w t + b) = -sin(w t + b) * (t dw + db); the pad dims carry dx = 0.
-        const float4 sn = *reinterpret_cast<const float4*>(ts + b * P.tvs + s.off);
+      // node-row gradient (the descriptor drops the lanes outside the node part)
+      if (P.d_node) {
+        if (P.node_tail) bstore4_dwords(rd, L.noff[k], dx);
+        else bstore4(rd, L.noff[k], dx);
+      }
+      // d cos(w t + b) = -sin(w t + b) * (t dw + db); the pad dims carry dx = 0
+      if (P.dt_dim > 0) {
+        // the -sin tile is zero outside the time dims, so only time chunks contribute
+        const float4 sn = *reinterpret_cast<const float4*>(ts + b * P.tvs + L.toff[k]);
         const float4 pr = make_float4(sn.x * dx.x, sn.y * dx.y, sn.z * dx.z, sn.w * dx.w);
         S.gb[k].x += pr.x;
         S.gb[k].y += pr.y;
@@ -514,6 +599,7 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
         fma4(S.gw[k], t, pr);
       }
     }
+    (void)lane;
   }
 }
 
@@ -527,7 +613,7 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
 
   LaneCtx<NS> L;
   setup_lane<NS>(P, L);
-  zero_time_pad(P, tc, 2 * kBatch);
+  init_tiles(P, tc, 2 * kBatch, kBatch);
   BwdState<H, NS> S;
 #pragma unroll
   for (int k = 0; k < NS; ++k) { S.gw[k] = f4_zero(); S.gb[k] = f4_zero(); }
@@ -542,21 +628,21 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
     if (e1 <= e0) {
-      store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq, P.cp);
+      store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq);
       continue;
     }
-    load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q, P.cp);
-    load_rows<H, NS>(P.dxbar, P.dxbar_hs, v, P.kp, S.g, P.cp);
+    load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q);
+    load_rows<H, NS>(P.dxbar, P.dxbar_hs, v, P.kp, S.g);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
-      S.lh[h] = P.stats[(v * H + h) * 2 + 1];
+      S.il[h] = 1.f / P.stats[(v * H + h) * 2 + 1];
     }
     {
-      float4 xb[H][NS];
-      load_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, xb, P.cp);
+      float4 xr[H][NS];
+      load_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, xr);
 #pragma unroll
-      for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xb[h]));
+      for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xr[h]));
     }
 
     for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
@@ -564,30 +650,32 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
       EdgeMeta<H, true> M;
       stage_meta<H, true>(P, c0, cnt, M);
       float4 xa[kBatch][NS], xb[kBatch][NS];
-      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+      int oka[kBatch], okb[kBatch];
+      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa, oka);
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
         const int nb2 = cnt - jb - kBatch;
         const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
-        if (nb > 0) issue_rows<NS, H, true>(P, L, M, jb + kBatch, nb, xb);
-        bwd_batch<H, NS>(P, L, M, c0, jb, na, tc, ts, xa, S);
+        if (nb > 0) issue_rows<NS, H, true>(P, L, M, jb + kBatch, nb, xb, okb);
+        bwd_batch<H, NS>(P, L, M, c0, jb, na, tc, ts, xa, oka, S);
         if (nb > 0) {
           const int nn2 = cnt - jb - 2 * kBatch;
           const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
-          if (nn > 0) issue_rows<NS, H, true>(P, L, M, jb + 2 * kBatch, nn, xa);
-          bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, S);
+          if (nn > 0) issue_rows<NS, H, true>(P, L, M, jb + 2 * kBatch, nn, xa, oka);
+          bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, okb, S);
         }
       }
     }
-    store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq, P.cp);
+    store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq);
   }
 
-  // Time-grad partials of this workgroup: waves combined in a fixed order.
+  // Time-grad partials of this workgroup: waves combined in a fixed order. Every time dim
+  // is owned by exactly one (lane, slot); the other lanes hold zeros and write them to the
+  // bias or zero chunk, which the sum below does not read.
   if (P.dt_dim <= 0) return;
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
-    if (L.sl[k].kind != kTime) continue;
-    const int o = L.sl[k].off;
+    const uint32_t o = L.toff[k];
     float* rw = red + (wave * 2 + 0) * P.tvs + o;
     float* rb = red + (wave * 2 + 1) * P.tvs + o;
     rw[0] = S.gw[k].x; rw[1] = S.gw[k].y; rw[2] = S.gw[k].z; rw[3] = S.gw[k].w;
@@ -651,7 +739,7 @@ __global__ __launch_bounds__(kBlock) void gather_rows(const float* tab, int64_t 
 // Host side
 // ---------------------------------------------------------------------------------
 int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_hs, float slope,
-                const float* drop, TgatParams& P) {
+                const float* drop, uint64_t drop_seed, float drop_p, TgatParams& P) {
   if (!g || heads <= 0) return FA_EINVAL;
   if (g->n_dst < 0 || g->n_edges < 0 || g->dn < 0 || g->de < 0 || g->dt_dim < 0) return FA_EINVAL;
   if (g->n_edges > INT32_MAX) return FA_EUNSUPPORTED;
@@ -667,16 +755,24 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_h
   P.dn = g->dn; P.node_idx = g->node_idx;
   P.edge_tab = g->edge_tab; P.ld_edge = g->ld_edge; P.n_erow = g->de > 0 ? g->n_edge_rows : 0;
   P.de = g->de; P.edge_idx = g->edge_idx;
-  P.node_vec = aligned16(g->node_tab) && (g->ld_node & 3) == 0;
-  P.edge_vec = aligned16(g->edge_tab) && (g->ld_edge & 3) == 0;
+  // Row chunks are read as float4 when every row start is 16-byte aligned, else dword-wise.
+  P.node_tail = g->dn > 0 && ((g->dn & 3) || (g->ld_node & 3) || !aligned16(g->node_tab));
+  P.edge_tail = g->de > 0 && ((g->de & 3) || (g->ld_edge & 3) || !aligned16(g->edge_tab));
+  if (g->n_edges > 0 && ((g->dn > 0 && g->n_node <= 0) || (g->de > 0 && g->n_edge_rows <= 0)))
+    return FA_EINVAL;
   P.dt = g->dt; P.time_w = g->time_w; P.time_b = g->time_b; P.dt_dim = g->dt_dim;
   P.cn = static_cast<int>(ceil_div(g->dn, 4));
   P.ce = static_cast<int>(ceil_div(g->de, 4));
   P.ct = static_cast<int>(ceil_div(g->dt_dim, 4));
   P.cp = P.cn + P.ce + P.ct + 1;
-  P.tvs = 4 * P.ct;
+  P.tvs = 4 * (P.ct + 2);
   P.kp = 4 * static_cast<int64_t>(P.cp);
   P.qt = qt; P.qt_hs = qt_hs; P.slope = slope; P.drop = drop;
+  if (!(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
+  P.drop_seed = drop_seed;
+  P.drop_p = drop_p;
+  P.drop_scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
+  P.drop_hash = (drop == nullptr && drop_p > 0.f) ? 1 : 0;
   if (!aligned16(qt)) return FA_EALIGN;
   if (heads > 1 && ((qt_hs & 3) || qt_hs < P.kp * g->n_dst)) return FA_EINVAL;
   return FA_OK;
@@ -737,11 +833,12 @@ extern "C" int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim) {
 }
 
 extern "C" int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_hs, float slope, const float* drop, float* xbar,
+                                    int64_t qt_hs, float slope, const float* drop,
+                                    uint64_t drop_seed, float drop_p, float* xbar,
                                     int64_t xbar_hs, float* scores, float* stats,
                                     hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_hs, slope, drop, P);
+  int st = fill_params(g, heads, qt, qt_hs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) return FA_OK;
   if (fwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
@@ -776,13 +873,14 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
 
 extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                                     int64_t qt_hs, float slope, const float* drop,
+                                    uint64_t drop_seed, float drop_p,
                                     const float* xbar, int64_t xbar_hs, const float* scores,
                                     const float* stats, const float* dxbar, int64_t dxbar_hs,
                                     float* dqt, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
                                     float* d_time_w, float* d_time_b, void* scratch,
                                     size_t scratch_bytes, hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_hs, slope, drop, P);
+  int st = fill_params(g, heads, qt, qt_hs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) {
     if (P.dt_dim > 0 && d_time_w && d_time_b) {
@@ -800,7 +898,6 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
       (xbar_hs < P.kp * P.n_dst || dxbar_hs < P.kp * P.n_dst || dqt_hs < P.kp * P.n_dst))
     return FA_EINVAL;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
-  P.dnode_vec = d_node && aligned16(d_node) && (ld_dnode & 3) == 0;
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   const int grid = bwd_grid(P.n_dst);
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
@@ -808,6 +905,8 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   P.xbar = const_cast<float*>(xbar); P.xbar_hs = xbar_hs;
   P.dxbar = dxbar; P.dxbar_hs = dxbar_hs; P.dqt = dqt; P.dqt_hs = dqt_hs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
+  // 16-byte node-gradient stores need 16-byte aligned gradient rows as well
+  if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.node_tail = true;
   P.stats = const_cast<float*>(stats); P.partial = static_cast<float*>(scratch);
   if (static_cast<int64_t>(kBatch) * heads > kWave) return FA_EUNSUPPORTED;
   switch (heads) {
@@ -820,6 +919,23 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   if (st != FA_OK || P.dt_dim <= 0) return st;
   hipLaunchKernelGGL(time_grad_reduce, dim3(static_cast<unsigned>(ceil_div(2 * P.dt_dim, kWavesPerBlock))),
                      dim3(kBlock), 0, stream, P.partial, grid, P.dt_dim, d_time_w, d_time_b);
+  return launch_status();
+}
+
+__global__ __launch_bounds__(kBlock) void dropout_mask(uint64_t seed, float p, float scale,
+                                                      int64_t n, float* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < n) out[i] = drop_mult(seed, static_cast<uint64_t>(i), p, scale);
+}
+
+extern "C" int fa_dropout_mask_f32(uint64_t seed, float p, int64_t n, float* out,
+                                   hipStream_t stream) {
+  if (n < 0 || !(p >= 0.f && p < 1.f)) return FA_EINVAL;
+  if (n == 0) return FA_OK;
+  if (!out) return FA_EINVAL;
+  const float scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(p)));
+  hipLaunchKernelGGL(dropout_mask, dim3(static_cast<unsigned>(ceil_div(n, kBlock))), dim3(kBlock), 0,
+                     stream, seed, p, scale, n, out);
   return launch_status();
 }
 

@@ -261,11 +261,13 @@ class TgatAttention(torch.autograd.Function):
     None, else a table gathered by ``node_idx``)."""
 
     @staticmethod
-    def forward(ctx, qt, time_w, time_b, node_src, g: _Graph, slope: float, drop):
+    def forward(ctx, qt, time_w, time_b, node_src, g: _Graph, slope: float, drop,
+                drop_seed: int = 0, drop_p: float = 0.0):
         t0 = timer.begin() if timer is not None else None
         xbar, scores, stats = fastAgg.tgat_attn_fwd(g.rowptr, node_src, g.node_idx, g.edge_tab,
                                                     g.edge_idx, g.dt, time_w, time_b, qt,
-                                                    float(slope), drop)
+                                                    float(slope), drop, int(drop_seed),
+                                                    float(drop_p))
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
@@ -274,6 +276,8 @@ class TgatAttention(torch.autograd.Function):
         ctx.g = g
         ctx.slope = float(slope)
         ctx.has_drop = drop is not None
+        ctx.drop_seed = int(drop_seed)
+        ctx.drop_p = float(drop_p)
         saved = [qt, time_w, time_b, node_src, xbar, scores, stats]
         if drop is not None:
             saved.append(drop)
@@ -291,7 +295,8 @@ class TgatAttention(torch.autograd.Function):
         t0 = timer.begin() if timer is not None else None
         dqt, d_node, d_tw, d_tb = fastAgg.tgat_attn_bwd(g.rowptr, node_src, g.node_idx,
                                                         g.edge_tab, g.edge_idx, g.dt, time_w,
-                                                        time_b, qt, ctx.slope, drop, xbar,
+                                                        time_b, qt, ctx.slope, drop,
+                                                        ctx.drop_seed, ctx.drop_p, xbar,
                                                         scores, stats, dxbar, need_node)
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
@@ -305,7 +310,41 @@ class TgatAttention(torch.autograd.Function):
                 d_src = d_node
             else:
                 d_src = torch.zeros_like(node_src).index_add_(0, g.node_idx, d_node)
-        return dqt, d_tw, d_tb, d_src, None, None, None
+        return dqt, d_tw, d_tb, d_src, None, None, None, None, None
+
+
+def _rows_t_mm(a: torch.Tensor, b: torch.Tensor, chunk: int = 8192) -> torch.Tensor:
+    """a^T b for tall a [n, p], b [n, q], split over row chunks (one batched product
+    plus a sum) so that the reduction over n spreads over many workgroups."""
+    n = a.shape[0]
+    s = n // chunk
+    if s < 2:
+        return a.t() @ b
+    m = s * chunk
+    out = torch.bmm(a[:m].reshape(s, chunk, a.shape[1]).transpose(1, 2),
+                    b[:m].reshape(s, chunk, b.shape[1])).sum(0)
+    if m < n:
+        out = out + a[m:].t() @ b[m:]
+    return out
+
+
+class RowLinear(torch.autograd.Function):
+    """y = x W^T + b for x with many rows; the weight gradient is a split-row reduction."""
+
+    @staticmethod
+    def forward(ctx, x, W, b):
+        ctx.save_for_backward(x, W)
+        ctx.has_b = b is not None
+        return F.linear(x, W, b)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, W = ctx.saved_tensors
+        dy = dy.contiguous()
+        dx = dy @ W if ctx.needs_input_grad[0] else None
+        dW = _rows_t_mm(dy, x) if ctx.needs_input_grad[1] else None
+        db = dy.sum(0) if ctx.has_b and ctx.needs_input_grad[2] else None
+        return dx, dW, db
 
 
 # ---------------------------------------------------------------------------------------
@@ -354,20 +393,22 @@ class TransfomerAttentionLayer(torch.nn.Module):
             zt = torch.cos(self.time_enc.w.bias)
             bias = bq + torch.mv(Wq[:, Dn:], zt)
         if Dn > 0:
-            return F.linear(hdst, Wq[:, :Dn], bias)
+            return RowLinear.apply(hdst, Wq[:, :Dn], bias)
         return bias.expand(N, D)
 
     def forward(self, b: Block, _layers: int = 0, _hist: int = 0) -> torch.Tensor:
-        drop = None
         p = self.att_dropout.p
-        if self.training and p > 0 and b.num_edges() > 0:
-            drop = torch.empty(b.num_edges(), self.num_head, device=b.device)
-            drop.bernoulli_(1 - p).div_(1 - p)
-        return self.attend(b, drop)
+        if self.training and p > 0:
+            # seed of the kernels' counter-based dropout, drawn from torch's CPU generator
+            seed = int(torch.randint(0, 2**62, (1,)).item())
+            return self.attend(b, drop_seed=seed, drop_p=p)
+        return self.attend(b)
 
-    def attend(self, b: Block, drop: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """The layer with an explicit attention-dropout multiplier ``drop`` [E, heads]
-        (0 or 1/(1-p) per entry; None = no attention dropout)."""
+    def attend(self, b: Block, drop: Optional[torch.Tensor] = None, drop_seed: int = 0,
+               drop_p: float = 0.0) -> torch.Tensor:
+        """The layer with an explicit attention dropout: ``drop`` [E, heads] multipliers
+        (0 or 1/(1-p) per entry), or, when ``drop`` is None and ``drop_p`` > 0, the kernels'
+        hashed dropout of seed ``drop_seed`` (fastAgg.dropout_mask gives its multipliers)."""
         Dn, De, Dt = self.dim_node_feat, self.dim_edge_feat, self.dim_time
         H, D = self.num_head, self.dim_out
         dh = D // H
@@ -397,16 +438,18 @@ class TransfomerAttentionLayer(torch.nn.Module):
             tw = tb = torch.empty(0, device=dev)
             dt = torch.zeros(E, device=dev)
         g = _Graph(b.rowptr(), node_idx, edge_tab, edge_idx, dt)
-        xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop)
+        xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop, drop_seed,
+                                   drop_p)
 
         wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt)
         out = torch.bmm(xbar, wv.view(H, dh, kp).transpose(1, 2).contiguous())  # [H, N, dh]
         agg = out.transpose(0, 1).reshape(N, D)
         Wo = self.w_out.weight
         if Dn > 0:
-            rst = torch.addmm(F.linear(hdst, Wo[:, D:], self.w_out.bias), agg, Wo[:, :D].t())
+            rst = (RowLinear.apply(agg, Wo[:, :D], None)
+                   + RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias))
         else:
-            rst = F.linear(agg, Wo, self.w_out.bias)
+            rst = RowLinear.apply(agg, Wo, self.w_out.bias)
         rst = F.relu(self.dropout(rst))
         return self.layer_norm(rst)
 

@@ -198,13 +198,20 @@ typedef struct fa_tgat_graph {
 /* K-space width Kp for the given dims (all > = 0). */
 int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim);
 
-/* Forward. qt: [heads][n_dst][Kp] (head stride qt_hs, row stride Kp);
- * drop: optional [n_edges][heads] multipliers (dropout keep/(1-p)), may be NULL.
+/* Forward. qt: [heads][n_dst][Kp] (head stride qt_hs, row stride Kp).
+ * Attention dropout: drop = optional explicit [n_edges][heads] multipliers (keep/(1-p) or
+ * 0); when drop is NULL and drop_p > 0, entry (e,h) is kept iff the counter-based hash of
+ * (drop_seed, e*heads+h) clears drop_p (see fa_dropout_mask_f32); drop_p = 0: no dropout.
  * Outputs: xbar [heads][n_dst][Kp] (head stride xbar_hs), scores [n_edges][heads]
  * (post-LeakyReLU), stats [n_dst][heads][2] = (max, sum of exp). */
 int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_hs, float slope, const float* drop, float* xbar,
-                         int64_t xbar_hs, float* scores, float* stats, hipStream_t stream);
+                         int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
+                         float drop_p, float* xbar, int64_t xbar_hs, float* scores,
+                         float* stats, hipStream_t stream);
+
+/* The multipliers of the hashed attention dropout: out[i] = 1/(1-p) if
+ * (hash(seed, i) >> 8) / 2^24 >= p else 0, for i < n (i = e*heads + h). */
+int fa_dropout_mask_f32(uint64_t seed, float p, int64_t n, float* out, hipStream_t stream);
 
 /* Normalised attention att[e,h] = exp(score - max[dst]) / sum[dst] (pre-dropout), for
  * callers that want the weights themselves. dst: [n_edges] int64 in [0, n_dst). */
@@ -219,7 +226,8 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
  * NULL when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_hs, float slope, const float* drop, const float* xbar,
+                         int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
+                         float drop_p, const float* xbar,
                          int64_t xbar_hs, const float* scores, const float* stats,
                          const float* dxbar, int64_t dxbar_hs, float* dqt, int64_t dqt_hs,
                          float* d_node, int64_t ld_dnode, float* d_time_w, float* d_time_b,

@@ -252,3 +252,24 @@ void ref_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t*
     }
   }
 }
+
+/* Counter-based dropout multipliers of the fused TGAT kernels: entry i kept iff
+ * (hash(seed, i) >> 8) / 2^24 >= p, hash = two rounds of the murmur3 32-bit finaliser. */
+static uint32_t ref_mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x;
+}
+
+void ref_dropout_mask_f32(uint64_t seed, float p, int64_t n, float* out) {
+  const float scale = (float)(1.0 / (1.0 - (double)p));
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t x = ref_mix32((uint32_t)i ^ (uint32_t)seed);
+    x = ref_mix32(x + (uint32_t)(seed >> 32) + (uint32_t)((uint64_t)i >> 32) * 0x9e3779b9u);
+    const float u = (float)(x >> 8) * (1.0f / 16777216.0f);
+    out[i] = u >= p ? scale : 0.f;
+  }
+}

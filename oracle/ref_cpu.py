@@ -134,6 +134,12 @@ class _C:
                                            self._p(dx), ctypes.c_int64(dx.shape[1]))
         return dx
 
+    def dropout_mask(self, n_edges, heads, seed, p):
+        out = np.empty((n_edges, heads), np.float32)
+        self.lib.ref_dropout_mask_f32(ctypes.c_uint64(seed), ctypes.c_float(p),
+                                      ctypes.c_int64(n_edges * heads), self._p(out))
+        return out
+
     # --- aggregation -------------------------------------------------------------------
     def edge_scatter_sum(self, dst, src, x, n_out, indptr=None):
         dst = np.ascontiguousarray(dst, dtype=np.int64)

@@ -148,3 +148,55 @@ def test_zero_edge_block(dev):
     blk.edata["dt"] = torch.zeros(0, device=dev)
     out = layer(blk)
     assert out.shape == (5, 4) and torch.count_nonzero(out) == 0
+
+
+def test_dropout_mask_matches_restatement(dev):
+    import fast_amd
+    from oracle.ref_cpu import C
+
+    for seed, p, E, H in ((0, 0.1, 1000, 2), (2**40 + 12345, 0.5, 777, 8), (7, 0.0, 10, 1)):
+        got = fast_amd.fastAgg.dropout_mask(E, H, seed, p, dev).cpu().numpy()
+        ref = C.dropout_mask(E, H, seed, p)
+        assert (got == ref).all(), (seed, p)
+    m = fast_amd.fastAgg.dropout_mask(500_000, 2, 123, 0.1, dev)
+    keep = float((m > 0).float().mean())
+    assert abs(keep - 0.9) < 0.003, keep
+
+
+def test_hashed_dropout_equals_explicit_mask(dev):
+    """The kernels' in-kernel dropout (seed, p) gives exactly the layer computed with the
+    explicit multipliers fastAgg.dropout_mask(seed, p), forward and backward, and both match
+    the restatement with that mask."""
+    import fast_amd
+    from fast_amd.tgat import TransfomerAttentionLayer
+    from fast_amd.workloads import single_layer
+
+    torch.manual_seed(0)
+    layer = TransfomerAttentionLayer(100, 172, 100, 2, 0.0, 0.3, 100).to(dev)
+    degrees = np.array([10] * 100 + [0, 1, 25])
+    inp = single_layer(len(degrees), degrees=degrees, seed=3)
+    seed, p = 99, 0.3
+    outs, grads = [], []
+    for explicit in (False, True):
+        blk = inp.block.to(dev)
+        blk.srcdata["h"].requires_grad_(True)
+        layer.zero_grad()
+        if explicit:
+            mask = fast_amd.fastAgg.dropout_mask(blk.num_edges(), 2, seed, p, dev)
+            out = layer.attend(blk, drop=mask)
+        else:
+            out = layer.attend(blk, drop_seed=seed, drop_p=p)
+        out.backward(inp.dout.to(dev))
+        outs.append(out.detach())
+        grads.append([blk.srcdata["h"].grad.clone()] + [q.grad.clone() for q in layer.parameters()])
+    assert torch.equal(outs[0], outs[1])
+    for a, b in zip(grads[0], grads[1]):
+        assert torch.equal(a, b)
+    cpu = inp.block
+    mask = torch.from_numpy(__import__("oracle.ref_cpu", fromlist=["C"]).C.dropout_mask(
+        cpu.num_edges(), 2, seed, p))
+    P = layer_params(layer)
+    src, dst = cpu.edges()
+    ref = tgat_layer(P, cpu.srcdata["h"].double(), cpu.edata["f"], cpu.edata["dt"], src, dst,
+                     len(degrees), att_drop=mask)
+    assert_rel(outs[0], ref, FP32_TOL, "hashed dropout vs restatement")

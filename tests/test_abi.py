@@ -1,0 +1,138 @@
+"""The C ABI library (fast_amd/lib/libfastagg_hip.so) on the CPU: it loads, exports exactly
+the entry points include/fastagg.h declares, and its host-side logic (status text, K-space
+width, scratch sizes, argument validation that rejects a call before any launch) behaves
+as documented. No kernel is launched here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fastagg.h")
+FA_OK, FA_EINVAL, FA_EUNSUPPORTED, FA_EALIGN, FA_ESCRATCH = 0, -1, -2, -3, -4
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from fast_amd import build as fb
+
+    path = fb.lib_path()
+    if not os.path.exists(path):
+        fb.build_hip_library()
+    return ctypes.CDLL(path)
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for must in ("fa_tgat_attn_fwd_f32", "fa_tgat_attn_bwd_f32", "fa_edge_softmax_fwd_f32",
+                 "fa_edge_softmax_bwd_f32", "fa_edge_scatter_sum_f32", "fa_segment_sum_f32",
+                 "fa_exclusive_sum_i32", "fa_degree_count_i32", "fa_balance_mask_i32",
+                 "fa_fused_attn_fwd_f32", "fa_fused_attn_bwd_f32", "fa_group_softmax_fwd_f32"):
+        assert must in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared in fastagg.h but not exported: {missing}"
+
+
+def test_no_undeclared_exports():
+    from fast_amd import build as fb
+
+    out = subprocess.run(["nm", "-D", "--defined-only", fb.lib_path()], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    extra = sorted(n for n in exported if n.startswith("fa_") and n not in declared_functions())
+    assert not extra, f"exported but not declared: {extra}"
+
+
+def test_status_strings_and_version(lib):
+    lib.fa_status_string.restype = ctypes.c_char_p
+    for st in (FA_OK, FA_EINVAL, FA_EUNSUPPORTED, FA_EALIGN, FA_ESCRATCH):
+        assert lib.fa_status_string(st)
+    assert lib.fa_status_string(FA_OK) == b"success"
+    assert lib.fa_status_string(-99) == b"unknown status"
+    assert lib.fa_abi_version() // 100 == 1
+
+
+def test_kspace_width(lib):
+    lib.fa_tgat_kspace.restype = ctypes.c_int64
+    k = lambda dn, de, dt: lib.fa_tgat_kspace(ctypes.c_int32(dn), ctypes.c_int32(de),
+                                              ctypes.c_int32(dt))
+    # node | edge | time blocks padded to 4, then the bias column padded to a float4 chunk
+    assert k(100, 172, 100) == 100 + 172 + 100 + 4
+    assert k(7, 5, 3) == 8 + 8 + 4 + 4
+    assert k(0, 0, 0) == 4
+    assert k(413, 186, 100) == 416 + 188 + 100 + 4
+    assert k(-1, 0, 0) < 0
+
+
+def test_scratch_sizes(lib):
+    lib.fa_tgat_attn_bwd_scratch_bytes.restype = ctypes.c_size_t
+    lib.fa_exclusive_sum_scratch_bytes.restype = ctypes.c_size_t
+    assert lib.fa_tgat_attn_bwd_scratch_bytes(ctypes.c_int64(1000), ctypes.c_int32(0)) == 0
+    small = lib.fa_tgat_attn_bwd_scratch_bytes(ctypes.c_int64(1000), ctypes.c_int32(100))
+    big = lib.fa_tgat_attn_bwd_scratch_bytes(ctypes.c_int64(10 ** 7), ctypes.c_int32(100))
+    assert 0 < small <= big
+    assert big <= 64 << 20  # per-workgroup partials of the time gradients: bounded
+    assert lib.fa_exclusive_sum_scratch_bytes(ctypes.c_int64(10 ** 6)) >= 0
+
+
+class TgatGraph(ctypes.Structure):
+    _fields_ = [("n_dst", ctypes.c_int64), ("n_edges", ctypes.c_int64),
+                ("rowptr", ctypes.c_void_p),
+                ("node_tab", ctypes.c_void_p), ("ld_node", ctypes.c_int64),
+                ("n_node", ctypes.c_int64), ("dn", ctypes.c_int32), ("node_idx", ctypes.c_void_p),
+                ("edge_tab", ctypes.c_void_p), ("ld_edge", ctypes.c_int64),
+                ("n_edge_rows", ctypes.c_int64), ("de", ctypes.c_int32),
+                ("edge_idx", ctypes.c_void_p),
+                ("dt", ctypes.c_void_p), ("time_w", ctypes.c_void_p), ("time_b", ctypes.c_void_p),
+                ("dt_dim", ctypes.c_int32)]
+
+
+def _fwd(lib, g, heads=2, qt=None, qt_hs=0):
+    return lib.fa_tgat_attn_fwd_f32(ctypes.byref(g), ctypes.c_int32(heads), ctypes.c_void_p(qt),
+                                    ctypes.c_int64(qt_hs), ctypes.c_float(0.2), None,
+                                    ctypes.c_uint64(0), ctypes.c_float(0.0), None,
+                                    ctypes.c_int64(0), None, None, None)
+
+
+def test_tgat_fwd_rejects_bad_arguments(lib):
+    """Argument errors come back as FA_E* codes before anything touches a device."""
+    assert lib.fa_tgat_attn_fwd_f32(None, 2, None, 0, ctypes.c_float(0.2), None, 0,
+                                    ctypes.c_float(0.0), None, 0, None, None, None) == FA_EINVAL
+    g = TgatGraph(n_dst=-1)
+    assert _fwd(lib, g) == FA_EINVAL
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=None, dn=4, ld_node=4)
+    assert _fwd(lib, g) == FA_EINVAL  # missing rowptr / tables
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=16, node_tab=64, ld_node=2, n_node=10, dn=4)
+    assert _fwd(lib, g, qt=64) == FA_EINVAL  # leading dimension below the row width
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=16, dt_dim=4)
+    assert _fwd(lib, g, qt=64) == FA_EINVAL  # time encoding without dt / w / b
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=16)
+    assert _fwd(lib, g, heads=0, qt=64) == FA_EINVAL
+
+
+def test_softmax_rejects_bad_arguments(lib):
+    f = lib.fa_edge_softmax_fwd_f32
+    # (indptr, n_seg, n_edges, x, ldx, heads, y, ldy, mode, stream)
+    assert f(None, ctypes.c_int64(4), ctypes.c_int64(8), None, ctypes.c_int64(2),
+             ctypes.c_int32(2), None, ctypes.c_int64(2), ctypes.c_int32(0), None) == FA_EINVAL
+    P = ctypes.c_void_p(16)
+    call = lambda n_seg, heads, ldx, mode: f(P, ctypes.c_int64(n_seg), ctypes.c_int64(8), P,
+                                             ctypes.c_int64(ldx), ctypes.c_int32(heads), P,
+                                             ctypes.c_int64(2), ctypes.c_int32(mode), None)
+    assert call(4, 2, 2, 2) == FA_EINVAL    # unknown mode
+    assert call(4, 2, 1, 0) == FA_EINVAL    # leading dimension below the head count
+    assert call(-1, 2, 2, 0) == FA_EINVAL
+    assert call(0, 2, 2, 0) == FA_OK        # nothing to do: returns before any launch
+    assert call(4, 0, 2, 0) == FA_OK

@@ -1,0 +1,189 @@
+"""Host-side logic of fast_amd on the CPU (no kernel launches): the binding's error
+behaviour, the operator-flag manager, the block layout, the K-space algebra the fused
+kernels rely on, module construction order, the workload generators and bench.py's
+single-GPU guard."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import fast_amd
+from fast_amd import efficientGOP, tgat, workloads
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+fa = fast_amd.fastAgg
+
+
+def test_binding_is_the_top_level_fastAgg():
+    import fastAgg
+
+    assert fastAgg is fa
+    for name in ("forward_edge_softmax", "backward_edge_softmax", "forward_csr_edge_softmax",
+                 "backward_csr_edge_softmax", "forward_balanced_edge_softmax",
+                 "backward_balanced_edge_softmax", "forward_tgat", "backward_tgat",
+                 "forward_tgat_shd", "backward_tgat_shd", "forward_fused_attn",
+                 "backward_fused_attn", "exclusive_sum", "cal_deg", "getBalancedPtr"):
+        assert callable(getattr(fa, name)), name
+
+
+@pytest.mark.parametrize("call", [
+    lambda: fa.forward_edge_softmax(torch.zeros(3, dtype=torch.int32),
+                                    torch.zeros(3, dtype=torch.int32), torch.zeros(4, 2), 512, 2),
+    lambda: fa.exclusive_sum(torch.zeros(5, dtype=torch.int32)),
+    lambda: fa.cal_deg(torch.zeros(5, dtype=torch.int32), 3),
+    lambda: fa.forward_tgat(torch.zeros(4, dtype=torch.int64), torch.zeros(4, dtype=torch.int64),
+                            torch.zeros(8, 3), 4, 8, 128),
+])
+def test_cpu_tensors_are_rejected(call):
+    """Same contract as the reference binding (TORCH_CHECK is_cuda, operators.cpp:3-5)."""
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        call()
+
+
+def test_init_gop_launch_constants():
+    """efficientGOP.py:6-38: per-method launch parameters (accepted, not used by gfx950)."""
+    fm = efficientGOP.forwardManager()
+    fm.init_gop(fast_agg=1, fast_esm=1)
+    assert (fm.fastAggFlag, fm.fastESMFlag, fm.aggNodePB, fm.aggFeat) == (1, 1, 8, 128)
+    assert (fm.node_num_per_block, fm.reduceSize) == (512, 16)
+    fm.init_gop(fast_agg=2, fast_esm=2, csr_out=1)
+    assert (fm.aggNodePB, fm.aggFeat, fm.reduceSize, fm.node_num_per_block, fm.CSR_OUT) == (
+        8, 32, 16, 32, 1)
+
+
+def test_block_layout():
+    degs = torch.tensor([2, 0, 3, 1])
+    b = tgat.Block.from_fanout(4, degs)
+    src, dst = b.edges()
+    assert b.num_dst_nodes() == 4 and b.num_edges() == 6 and b.num_src_nodes() == 10
+    assert src.tolist() == [4, 5, 6, 7, 8, 9]          # edge e comes from source node N + e
+    assert dst.tolist() == [0, 0, 2, 2, 2, 3]          # grouped by ascending destination
+    assert b.indptr.tolist() == [0, 2, 5, 6]           # CSR over the non-empty destinations
+    assert b.indptr.dtype == torch.int32
+
+
+def test_kspace_absorbs_the_projection():
+    """W [x_n | x_e | x_t] + b == to_kspace(W, b) . x_aug, where x_aug pads every part to a
+    multiple of 4 and appends the constant 1 of the bias (then 3 zeros)."""
+    g = torch.Generator().manual_seed(0)
+    for dn, de, dt in ((7, 5, 3), (100, 172, 100), (0, 12, 9), (13, 6, 0), (8, 0, 4)):
+        D, E = 6, 11
+        W = torch.randn(D, dn + de + dt, generator=g, dtype=torch.float64)
+        b = torch.randn(D, generator=g, dtype=torch.float64)
+        x = torch.randn(E, dn + de + dt, generator=g, dtype=torch.float64)
+        Wk = tgat.to_kspace(W, b, dn, de, dt)
+        assert Wk.shape == (D, tgat.kspace_width(dn, de, dt))
+        parts, off = [], 0
+        for d in (dn, de, dt):
+            parts.append(torch.nn.functional.pad(x[:, off:off + d], (0, (-d) % 4)))
+            off += d
+        one = torch.zeros(E, 4, dtype=torch.float64)
+        one[:, 0] = 1.0
+        x_aug = torch.cat(parts + [one], 1)
+        torch.testing.assert_close(x_aug @ Wk.T, x @ W.T + b, rtol=1e-12, atol=1e-12)
+
+
+def test_absorbed_attention_equals_per_edge_attention():
+    """The fused kernels score q_h . (W_k x + b_k)_h as (Q_h W_k,h) . x_aug and aggregate
+    V through xbar = sum_e a_e x_aug,e, out_h = W_v,h xbar_h; with a softmax over one
+    destination both orders give the same result (float64, on the CPU)."""
+    g = torch.Generator().manual_seed(1)
+    dn, de, dt, H, dh, E = 5, 6, 3, 2, 4, 9
+    D = H * dh
+    Wk, Wv = (torch.randn(D, dn + de + dt, generator=g, dtype=torch.float64) for _ in range(2))
+    bk, bv = (torch.randn(D, generator=g, dtype=torch.float64) for _ in range(2))
+    x = torch.randn(E, dn + de + dt, generator=g, dtype=torch.float64)
+    q = torch.randn(H, dh, generator=g, dtype=torch.float64)
+    K = (x @ Wk.T + bk).view(E, H, dh)
+    V = (x @ Wv.T + bv).view(E, H, dh)
+    s = torch.nn.functional.leaky_relu((K * q[None]).sum(-1), 0.2)
+    a = torch.softmax(s, 0)
+    out_ref = (a[:, :, None] * V).sum(0)
+    # absorbed form
+    wk = tgat.to_kspace(Wk, bk, dn, de, dt).view(H, dh, -1)
+    wv = tgat.to_kspace(Wv, bv, dn, de, dt).view(H, dh, -1)
+    parts, off = [], 0
+    for d in (dn, de, dt):
+        parts.append(torch.nn.functional.pad(x[:, off:off + d], (0, (-d) % 4)))
+        off += d
+    bias = torch.zeros(E, 4, dtype=torch.float64)
+    bias[:, 0] = 1
+    x_aug = torch.cat(parts + [bias], 1)
+    qt = torch.einsum("hd,hdk->hk", q, wk)
+    s2 = torch.nn.functional.leaky_relu(x_aug @ qt.T, 0.2)
+    a2 = torch.softmax(s2, 0)
+    xbar = a2.T @ x_aug                      # [H, Kp]
+    out = torch.einsum("hdk,hk->hd", wv, xbar)
+    torch.testing.assert_close(out, out_ref, rtol=1e-12, atol=1e-12)
+
+
+def test_fused_kernel_bytes_accounting():
+    n, e, dn, de, dt, H = 120_000, 1_200_000, 100, 172, 100, 2
+    kp = tgat.kspace_width(dn, de, dt)
+    b = tgat.fused_kernel_bytes(n, e, dn, de, dt, H, True, True)
+    per_edge = 8 + 8 + 4 + 4 * (dn + de) + 4 * H
+    assert b["fwd"] == 4 * (n + 1) + 8 * dt + e * per_edge + n * (8 * H * kp + 8 * H)
+    assert b["bwd"] == 4 * (n + 1) + 8 * dt + e * per_edge + n * (16 * H * kp + 8 * H)
+    assert tgat.fused_kernel_bytes(n, e, dn, de, dt, H, True, True, d_node=True)["bwd"] == \
+        b["bwd"] + e * 4 * dn
+
+
+def test_layer_construction_order_matches_reference():
+    """Same modules, shapes and creation order as layers.py:53-97 (non-combined, fastKQV
+    off), so a given torch seed gives the same initial parameters."""
+    dn, de, dt, H, D = 100, 172, 100, 2, 100
+    torch.manual_seed(42)
+    layer = tgat.TransfomerAttentionLayer(dn, de, dt, H, 0.1, 0.1, D)
+    torch.manual_seed(42)
+    te = torch.nn.Linear(1, dt)
+    te.weight = torch.nn.Parameter(torch.from_numpy(
+        1 / 10 ** np.linspace(0, 9, dt, dtype=np.float32)).reshape(dt, -1))
+    te.bias = torch.nn.Parameter(torch.zeros(dt))
+    ref = [("time_enc.w.weight", te.weight), ("time_enc.w.bias", te.bias)]
+    for name, fin in (("w_q", dn + dt), ("w_k", dn + de + dt), ("w_v", dn + de + dt),
+                      ("w_out", dn + D)):
+        lin = torch.nn.Linear(fin, D)
+        ref += [(name + ".weight", lin.weight), (name + ".bias", lin.bias)]
+    ln = torch.nn.LayerNorm(D)
+    ref += [("layer_norm.weight", ln.weight), ("layer_norm.bias", ln.bias)]
+    got = list(layer.named_parameters())
+    assert [n for n, _ in got] == [n for n, _ in ref]
+    for (n, p), (_, r) in zip(got, ref):
+        assert torch.equal(p.detach(), r.detach()), n
+    assert layer.negative_slope == 0.2
+
+
+def test_time_encode_module():
+    te = tgat.TimeEncode(5)
+    t = torch.tensor([0.0, 1.0, 250.0])
+    y = te(t)
+    assert torch.equal(y[0], torch.ones(5))
+    ref = torch.cos(t[:, None].double() * te.w.weight.detach().view(1, -1).double())
+    torch.testing.assert_close(y.double(), ref, rtol=0, atol=1e-6)
+
+
+def test_workloads_are_seeded():
+    a = workloads.single_layer(50, seed=3)
+    b = workloads.single_layer(50, seed=3)
+    assert torch.equal(a.block.edata["dt"], b.block.edata["dt"])
+    assert torch.equal(a.block.srcdata["h"], b.block.srcdata["h"])
+    c = workloads.single_layer(50, seed=4)
+    assert not torch.equal(a.block.edata["dt"], c.block.edata["dt"])
+    assert a.block.num_edges() == 500 and bool((a.block.edata["dt"] >= 0).all())
+
+
+def test_ragged_degrees():
+    d = workloads.ragged_degrees(20_000, seed=0)
+    assert d.min() >= 0 and d.max() <= 20
+    zero = float((d == 0).mean())
+    assert 0.03 < zero < 0.08  # about 5 % of the destinations carry no edges
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)

@@ -1,0 +1,329 @@
+"""The CPU restatement (oracle/) pinned on the CPU, no GPU needed.
+
+Three kinds of checks, chosen so that an index, sign, operand-order or concatenation-order
+mistake in the oracle fails at least one of them:
+  * the golden fixtures under tests/golden/ (plain-Python loops over the definitions,
+    written by tests/golden/make_golden.py without touching oracle/);
+  * closed forms and invariants of the operations (softmax sums to 1 and is shift
+    invariant, degree-1 segments give exactly 1, scatter-sum is the adjoint of the gather,
+    a one-key batched softmax is the segment softmax, ...);
+  * finite differences of the layer (fixture) against the oracle's autograd gradients.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref_cpu
+from oracle.ref_cpu import C
+from tests._util import FP32_TOL, assert_rel, rel_err
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    with open(os.path.join(GOLD, name)) as fh:
+        return json.load(fh)
+
+
+def _csr_from_degrees(degs):
+    """indptr over the non-empty segments and the dst id of every edge."""
+    dst = np.repeat(np.arange(len(degs)), degs).astype(np.int64)
+    nz = np.asarray([d for d in degs if d > 0], dtype=np.int64)
+    indptr = np.concatenate([[0], np.cumsum(nz)]).astype(np.int32)
+    return indptr, dst
+
+
+# ---------------------------------------------------------------------------------------
+# bookkeeping: bit-exact integers
+# ---------------------------------------------------------------------------------------
+def test_bookkeeping_golden():
+    g = _load("bookkeeping.json")
+    for c in g["exclusive_sum"]:
+        np.testing.assert_array_equal(C.exclusive_sum(np.asarray(c["in"], np.int64)), c["out"])
+    for c in g["cal_deg"]:
+        np.testing.assert_array_equal(C.cal_deg(np.asarray(c["ids"], np.int64), c["n_nodes"]),
+                                      c["out"])
+    for c in g["balance_mask"]:
+        np.testing.assert_array_equal(C.balance_mask(np.asarray(c["ptr"]), c["threshold"]),
+                                      c["out"])
+    for c in g["rowptr"]:
+        np.testing.assert_array_equal(C.rowptr(np.asarray(c["dst"], np.int64), c["n_dst"]),
+                                      c["out"])
+
+
+def test_cnte_golden():
+    """The sampler's cntE (run lengths of the sorted row array, cumulated) is the exclusive
+    sum of the per-destination counts of the non-empty destinations (unique2indptr)."""
+    for c in _load("bookkeeping.json")["cnte"]:
+        dst = np.asarray(c["dst"], np.int64)
+        _, counts = np.unique(dst, return_counts=True)
+        np.testing.assert_array_equal(C.exclusive_sum(counts), c["out"])
+
+
+def test_bookkeeping_closed_forms():
+    rng = np.random.default_rng(3)
+    x = rng.integers(0, 50, 10_000)
+    np.testing.assert_array_equal(C.exclusive_sum(x), np.concatenate([[0], np.cumsum(x)]))
+    ids = rng.integers(-3, 700, 20_000)
+    ref = np.bincount(ids[(ids >= 0) & (ids < 650)], minlength=650)
+    np.testing.assert_array_equal(C.cal_deg(ids, 650), ref)
+    degs = rng.integers(0, 6, 500)
+    dst = np.repeat(np.arange(500), degs)
+    np.testing.assert_array_equal(C.rowptr(dst, 500), np.concatenate([[0], np.cumsum(degs)]))
+    # threshold 1 on a strictly increasing pointer marks every non-empty entry
+    ptr = np.concatenate([[0], np.cumsum(rng.integers(1, 4, 300))])
+    np.testing.assert_array_equal(C.balance_mask(ptr, 1), np.ones(300, np.int32))
+
+
+# ---------------------------------------------------------------------------------------
+# segment softmax (edge_softmax.cu:255-329 formula; dgl.ops.edge_softmax semantics)
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", [0, 1])
+def test_edge_softmax_golden(mode):
+    for c in _load("softmax.json"):
+        x = np.asarray(c["x"], np.float32)
+        y = C.edge_softmax_fwd(c["indptr"], x, c["heads"], mode)
+        assert_rel(y, c["y"], FP32_TOL, f"softmax mode {mode}")
+        dx = C.edge_softmax_bwd(c["indptr"], np.asarray(c["dy"], np.float32), y, c["heads"])
+        assert_rel(dx, c["dx"], FP32_TOL, "softmax backward")
+
+
+def test_torch_edge_softmax_golden():
+    """The float64 torch restatement used inside the layer oracle, forward and autograd."""
+    for c in _load("softmax.json"):
+        ip = np.asarray(c["indptr"])
+        dst = torch.from_numpy(np.repeat(np.arange(ip.size - 1), np.diff(ip)))
+        x = torch.tensor(c["x"], dtype=torch.float64, requires_grad=True)
+        y = ref_cpu.edge_softmax(x, dst, ip.size - 1)
+        assert rel_err(y, c["y"]) < 1e-12
+        y.backward(torch.tensor(c["dy"], dtype=torch.float64))
+        assert rel_err(x.grad, c["dx"]) < 1e-12
+
+
+def test_edge_softmax_invariants():
+    rng = np.random.default_rng(11)
+    degs = [1, 2, 7, 64, 65, 300, 1, 3]
+    indptr, dst = _csr_from_degrees(degs)
+    E, H = dst.size, 3
+    x = (rng.standard_normal((E, H)) * 4).astype(np.float32)
+    y = C.edge_softmax_fwd(indptr, x, H, 0)
+    seg_sum = np.add.reduceat(y.astype(np.float64), indptr[:-1], axis=0)
+    np.testing.assert_allclose(seg_sum, 1.0, rtol=0, atol=1e-5)
+    # degree-1 segments give exactly 1
+    for s, d in enumerate([d for d in degs if d]):
+        if d == 1:
+            assert np.all(y[indptr[s]] == 1.0)
+    # shift invariance within a segment (shift by a per-segment constant)
+    shift = np.repeat(rng.uniform(-20, 20, len(degs)), degs).astype(np.float32)[:, None]
+    y2 = C.edge_softmax_fwd(indptr, (x.astype(np.float64) + shift).astype(np.float32), H, 0)
+    assert rel_err(y2, y) < 1e-4  # the shifted inputs are re-rounded to float32
+    # equal scores in a segment give 1/deg
+    yeq = C.edge_softmax_fwd(indptr, np.ones_like(x), H, 1)
+    ref = np.repeat(1.0 / np.asarray(degs, np.float64), degs)[:, None] * np.ones((1, H))
+    assert rel_err(yeq, ref) < 1e-6
+    # the backward is orthogonal to the constants: its per-segment sum vanishes
+    dy = rng.standard_normal((E, H)).astype(np.float32)
+    dx = C.edge_softmax_bwd(indptr, dy, y, H)
+    np.testing.assert_allclose(np.add.reduceat(dx.astype(np.float64), indptr[:-1], axis=0), 0.0,
+                               atol=1e-5)
+
+
+def test_group_softmax_reduces_to_segment_softmax():
+    """One key per batch: the batched softmax is the segment softmax of the batches. With two
+    interleaved keys it is the segment softmax of the edges sorted by (batch, key)."""
+    rng = np.random.default_rng(5)
+    degs = [3, 9, 1, 12]
+    bptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int64)
+    E, L = int(bptr[-1]), max(degs)
+    x = rng.standard_normal((E, 2)).astype(np.float32)
+    dy = rng.standard_normal((E, 2)).astype(np.float32)
+    key0 = np.zeros((len(degs), L), np.int64)
+    y = C.group_softmax_fwd(bptr, key0, x)
+    y_ref = C.edge_softmax_fwd(bptr.astype(np.int32), x, 2, 1)
+    assert rel_err(y, y_ref) < 1e-6
+    assert rel_err(C.group_softmax_bwd(bptr, key0, dy, y),
+                   C.edge_softmax_bwd(bptr.astype(np.int32), dy, y_ref, 2)) < 1e-6
+    # interleaved keys 0/1 inside every batch
+    key = np.zeros((len(degs), L), np.int64)
+    for b, d in enumerate(degs):
+        key[b, :d] = np.arange(d) % 2
+    y = C.group_softmax_fwd(bptr, key, x)
+    order, seg = [], [0]
+    for b, d in enumerate(degs):
+        for k in (0, 1):
+            idx = [bptr[b] + j for j in range(d) if key[b, j] == k]
+            if idx:
+                order += idx
+                seg.append(seg[-1] + len(idx))
+    order = np.asarray(order)
+    ys = C.edge_softmax_fwd(np.asarray(seg, np.int32), x[order], 2, 1)
+    assert rel_err(y[order], ys) < 1e-6
+
+
+# ---------------------------------------------------------------------------------------
+# aggregation (update_all(copy_u, sum) semantics; aggregate_*.cu)
+# ---------------------------------------------------------------------------------------
+def test_aggregation_golden():
+    for c in _load("aggregation.json"):
+        dst, src = np.asarray(c["dst"], np.int64), np.asarray(c["src"], np.int64)
+        x = np.asarray(c["x"], np.float32)
+        N = c["n_dst"]
+        assert_rel(C.edge_scatter_sum(dst, src, x, N), c["agg"], FP32_TOL, "scatter sum")
+        assert_rel(C.segment_sum(c["indptr"], dst, src, x, N), c["agg"], FP32_TOL, "segment sum")
+        # backward = scatter of dout[dst] into the source rows
+        dx = C.edge_scatter_sum(src, dst, np.asarray(c["dout"], np.float32), x.shape[0])
+        assert_rel(dx, c["dx"], FP32_TOL, "scatter-sum backward")
+        got = ref_cpu.copy_u_sum(torch.from_numpy(x).double(), torch.from_numpy(src),
+                                 torch.from_numpy(dst), N)
+        assert rel_err(got, c["agg"]) < 1e-12
+
+
+def test_aggregation_adjoint():
+    """<A x, y> == <x, A^T y> for the gather-sum A and its transpose; empty dst rows are 0."""
+    rng = np.random.default_rng(8)
+    degs = [0, 4, 1, 0, 9, 2]
+    indptr, dst = _csr_from_degrees(degs)
+    N, E, dim = len(degs), dst.size, 5
+    src = rng.permutation(np.arange(N, N + E)).astype(np.int64)
+    x = rng.standard_normal((N + E, dim)).astype(np.float32)
+    yv = rng.standard_normal((N, dim)).astype(np.float32)
+    ax = C.edge_scatter_sum(dst, src, x, N)
+    aty = C.edge_scatter_sum(src, dst, yv, N + E)
+    assert math.isclose(float((ax.astype(np.float64) * yv).sum()),
+                        float((x.astype(np.float64) * aty).sum()), rel_tol=1e-5)
+    assert np.all(ax[[0, 3]] == 0.0)
+    assert_rel(C.segment_sum(indptr, dst, src, x, N), ax, FP32_TOL, "segment vs scatter")
+
+
+# ---------------------------------------------------------------------------------------
+# fused LeakyReLU + softmax + dropout + aggregation (fused_attention.cu intended semantics)
+# ---------------------------------------------------------------------------------------
+def test_fused_attn_golden():
+    c = _load("fused_attn.json")
+    dst, src = np.asarray(c["dst"], np.int64), np.asarray(c["src"], np.int64)
+    score, V = np.asarray(c["score"], np.float32), np.asarray(c["V"], np.float32)
+    mask = np.asarray(c["mask"], np.float32)
+    N = c["n_dst"]
+    out, attn = C.fused_attn_fwd(c["indptr"], dst, src, N, score, V, c["slope"], c["p"], mask)
+    assert_rel(attn, c["attn"], FP32_TOL, "fused attn")
+    assert_rel(out, c["out"], FP32_TOL, "fused out")
+    d_act, gV = C.fused_attn_bwd(c["indptr"], dst, src, N, N + dst.size,
+                                 np.asarray(c["dout"], np.float32), V, attn, mask, c["p"])
+    assert_rel(d_act, c["d_act"], FP32_TOL, "fused d_act")
+    assert_rel(gV, c["grad_V"], FP32_TOL, "fused grad_V")
+
+
+# ---------------------------------------------------------------------------------------
+# time encoding (layers.py:10-29)
+# ---------------------------------------------------------------------------------------
+def test_time_weight_golden():
+    g = _load("time_weight.json")
+    w = ref_cpu.time_encoding_weight(100).numpy()
+    np.testing.assert_array_equal(w, np.asarray(g["w_float32"], np.float32))
+    # float32 exponents up to 9 carry a relative error of up to 9 * ln(10) * 2^-24 ~ 1.2e-6
+    np.testing.assert_allclose(w.astype(np.float64), g["w_exact"], rtol=1.5e-6)
+
+
+def test_time_encode_closed_form():
+    w = ref_cpu.time_encoding_weight(7).double().requires_grad_(True)
+    b = torch.linspace(-1.0, 2.0, 7, dtype=torch.float64).requires_grad_(True)
+    # dt = 0 gives cos(b); with b = 0 exactly 1
+    assert torch.equal(ref_cpu.time_encode(torch.zeros(3), w.detach(), torch.zeros(7)),
+                       torch.ones(3, 7, dtype=torch.float64))
+    z = ref_cpu.time_encode(torch.zeros(2), w, b)
+    assert rel_err(z, torch.cos(b.detach()).expand(2, 7)) < 1e-7
+    # the argument is the float32 Linear(1, Dt) value: rounded product, then rounded sum
+    t = torch.tensor([0.0, 3.5, 1234.0, 9.0e5])
+    t32, w32, b32 = t.numpy()[:, None], w.detach().float().numpy()[None], b.detach().float().numpy()[None]
+    arg = torch.from_numpy(((t32 * w32).astype(np.float32) + b32).astype(np.float32)).double()
+    y = ref_cpu.time_encode(t, w, b)
+    assert rel_err(y, torch.cos(arg)) < 1e-15
+    # gradients at that point: d/dw = -sin(arg) * t, d/db = -sin(arg)
+    gy = torch.randn(4, 7, dtype=torch.float64, generator=torch.Generator().manual_seed(0))
+    y.backward(gy)
+    sn = torch.sin(arg)
+    assert rel_err(w.grad, (-sn * t.double()[:, None] * gy).sum(0)) < 1e-6
+    assert rel_err(b.grad, (-sn * gy).sum(0)) < 1e-6
+
+
+# ---------------------------------------------------------------------------------------
+# one TGAT layer (layers.py:98-240, TGAT branch) against plain loops + finite differences
+# ---------------------------------------------------------------------------------------
+def _layer_case():
+    c = _load("tgat_layer_tiny.json")
+    Dn, De, Dt, H, D = c["dims"]
+    T = lambda v: torch.tensor(v, dtype=torch.float64)
+    P = {
+        "time_enc.w.weight": T(c["P"]["tw"]).view(-1, 1), "time_enc.w.bias": T(c["P"]["tb"]),
+        "w_q.weight": T(c["P"]["Wq"]), "w_q.bias": T(c["P"]["bq"]),
+        "w_k.weight": T(c["P"]["Wk"]), "w_k.bias": T(c["P"]["bk"]),
+        "w_v.weight": T(c["P"]["Wv"]), "w_v.bias": T(c["P"]["bv"]),
+        "w_out.weight": T(c["P"]["Wo"]), "w_out.bias": T(c["P"]["bo"]),
+        "layer_norm.weight": T(c["P"]["lnw"]), "layer_norm.bias": T(c["P"]["lnb"]),
+    }
+    for v in P.values():
+        v.requires_grad_(True)
+    P.update({"_eps": 1e-5, "_heads": H, "_dims": (Dn, De, Dt, D)})
+    N = len(c["degs"])
+    dst = torch.tensor(c["dst"], dtype=torch.int64)
+    src = torch.arange(N, N + dst.numel())
+    h = T(c["h"]).requires_grad_(True)
+    return c, P, h, src, dst, N
+
+
+def test_tgat_layer_golden_forward():
+    c, P, h, src, dst, N = _layer_case()
+    out = ref_cpu.tgat_layer(P, h, torch.tensor(c["f"]), torch.tensor(c["dt"], dtype=torch.float32),
+                             src, dst, N)
+    assert rel_err(out, c["out"]) < 1e-10
+
+
+def test_tgat_layer_golden_gradients():
+    c, P, h, src, dst, N = _layer_case()
+    out = ref_cpu.tgat_layer(P, h, torch.tensor(c["f"]), torch.tensor(c["dt"], dtype=torch.float32),
+                             src, dst, N)
+    (out * torch.tensor(c["wsum"], dtype=torch.float64)).sum().backward()
+    names = {"Wk": "w_k.weight", "Wv": "w_v.weight", "Wq": "w_q.weight", "tb": "time_enc.w.bias",
+             "tw": "time_enc.w.weight", "Wo": "w_out.weight", "bk": "w_k.bias"}
+    for key, fd in c["fd_grads"].items():
+        name, idx = key.split("[")
+        idx = [int(i) for i in idx.rstrip("]").split(",")]
+        grad = h.grad if name == "h" else P[names[name]].grad
+        got = float(grad[tuple(idx)] if len(idx) > 1 or name != "tw" else grad[idx[0], 0])
+        # The differences were taken with the exact time argument, the oracle rounds it to
+        # float32 like the reference (|arg| ~ 1e4, so cos moves by up to ~5e-4 relative).
+        assert math.isclose(got, fd, rel_tol=5e-4, abs_tol=1e-6), (key, got, fd)
+
+
+def test_tgat_layer_zero_edges():
+    """layers.py:101-102: a block without edges returns zeros [N, D] (no w_out, no norm)."""
+    c, P, h, src, dst, N = _layer_case()
+    e = torch.zeros(0, dtype=torch.int64)
+    out = ref_cpu.tgat_layer(P, h[:N], torch.zeros(0, 3), torch.zeros(0), e, e, N)
+    assert torch.equal(out, torch.zeros(N, P["_dims"][3], dtype=torch.float64))
+
+
+# ---------------------------------------------------------------------------------------
+# counter-based attention dropout (the fused kernels' mask)
+# ---------------------------------------------------------------------------------------
+def test_dropout_mask_properties():
+    n, H = 100_000, 2
+    for p in (0.1, 0.5):
+        m = C.dropout_mask(n, H, 1234, p)
+        scale = np.float32(1.0 / (1.0 - p))
+        assert set(np.unique(m).tolist()) <= {0.0, float(scale)}
+        keep = (m > 0).mean()
+        sd = math.sqrt(p * (1 - p) / m.size)
+        assert abs(keep - (1 - p)) < 5 * sd, (p, keep)
+        # counter-based: a prefix of a longer mask is the shorter mask
+        np.testing.assert_array_equal(C.dropout_mask(1000, H, 1234, p).ravel(), m.ravel()[:2000])
+    assert np.all(C.dropout_mask(1000, 2, 7, 0.0) == 1.0)
+    a, b = C.dropout_mask(4000, 2, 1, 0.5), C.dropout_mask(4000, 2, 2, 0.5)
+    assert 0.4 < (a != b).mean() < 0.6  # independent seeds disagree on about half the entries
+    # the high seed word matters as well
+    c = C.dropout_mask(4000, 2, 1 + (1 << 32), 0.5)
+    assert 0.4 < (a != c).mean() < 0.6

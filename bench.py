@@ -19,6 +19,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -28,6 +29,9 @@ if ROOT not in sys.path:
 
 METRIC = "temporal-attn aggregated edges/s fwd+bwd (fanout 10); HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
+# rocprofv3 --pmc summary of this workload (FETCH_SIZE / WRITE_SIZE per dispatch, scaled by
+# the same counters on the copy probe below); gives roofline.traffic when present
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "tgat_C3_pmc_traffic.md")
 
 
 def parse():
@@ -38,10 +42,44 @@ def parse():
     ap.add_argument("--roots", type=int, default=4000)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-roots", type=int, default=200,
+    ap.add_argument("--cpu-roots", type=int, default=4000,
                     help="roots of the bounded CPU sample (same MFG shape, fewer roots)")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--copy-probe-mb", type=int, default=256,
+                    help="after the timed steps, one plain row copy of this many MiB "
+                         "(fastAgg.gather_rows over rows of 1024 floats): the known-size kernel "
+                         "that scales the PMC byte counters; 0 disables it")
     return ap.parse_args()
+
+
+def progress(msg: str) -> None:
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` (read + written) from the committed rocprofv3
+    --pmc summary, or None when there is none for it."""
+    try:
+        with open(PMC_SUMMARY) as fh:
+            text = fh.read()
+    except OSError:
+        return None
+    m = re.search(rf"^traffic_per_launch\s+{re.escape(kernel)}\s+(\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_probe(mb: int) -> None:
+    """One row copy of ``mb`` MiB: reads mb MiB of rows + 8 B of index per row, writes mb MiB."""
+    import torch
+
+    import fast_amd
+
+    rows = mb * 256  # 1024 floats = 4 KiB per row
+    src = torch.randn(rows, 1024, device="cuda:0")
+    idx = torch.arange(rows, device="cuda:0")
+    torch.cuda.synchronize()
+    fast_amd.fastAgg.gather_rows(src, idx, rows)
+    torch.cuda.synchronize()
 
 
 def cpu_model() -> str:
@@ -132,9 +170,11 @@ def main():
         out.backward(inp.dout)
         opt.step()
 
+    progress(f"inputs resident: {len(blocks)} blocks, {edges} edges per step")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    progress(f"{args.warmup} warm-up steps done")
     timer = tgat.KernelTimer()
     tgat.timer = timer
     torch.cuda.synchronize()
@@ -144,6 +184,9 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     tgat.timer = None
+    progress(f"{args.steps} timed steps done: {(t1 - t0) * 1e3 / args.steps:.3f} ms/step")
+    if args.copy_probe_mb > 0:
+        copy_probe(args.copy_probe_mb)
     ms = (t1 - t0) * 1e3 / args.steps
     kern = timer.summary()
     dom_name = max(kern, key=lambda k: kern[k]["ms"])
@@ -181,11 +224,13 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": dom["GB/s"] / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(dom_name),
+            "algorithmic_bytes_per_launch": dom["bytes"] // max(1, dom["launches"]),
         },
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_roots, args.cpu_reps, args.seed)
+        progress("cpu baseline done")
     print(json.dumps(line), flush=True)
 
 

@@ -50,9 +50,22 @@ __device__ __forceinline__ float lane_read(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Cross-row step of a wave reduction: rows 1 and 3 receive lane 15 of the row below
+// (row_bcast:15), then rows 2 and 3 receive lane 31 (row_bcast:31); lane 63 then holds
+// (S3 + S2) + (S1 + S0) for row results S0..S3.
+constexpr int kRowBcast15 = 0x142;
+constexpr int kRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);
-  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+  v += dpp_bcast<kRowBcast15, 0xA>(v);
+  v += dpp_bcast<kRowBcast31, 0xC>(v);
+  return lane_read(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -95,6 +108,33 @@ __device__ __forceinline__ float leaky(float z, float slope) { return z > 0.f ? 
 __device__ __forceinline__ float time_arg(float t, float w, float b) {
 #pragma clang fp contract(off)
   return t * w + b;
+}
+
+// exp(x) as 2^(x log2 e) on the hardware exp2 (a couple of ulp; used for softmax weights,
+// whose arguments are <= 0).
+__device__ __forceinline__ float exp_fast(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
+// sin and cos of x (radians) for |x| <= 2^22 on the hardware sin/cos, whose argument is in
+// revolutions: f = x/(2 pi) - k with k = rint(x c_hi), evaluated as
+// fma(x, c_lo, fma(x, c_hi, -k)) where c_hi + c_lo = 1/(2 pi) (float32 split); the inner
+// FMA forms x c_hi - k exactly before its one rounding, so |f| <= 1/2 carries an error of
+// about 3e-8 revolutions. The hardware functions are accurate to about 1.3e-7 absolute on
+// [-1/2, 1/2]. Contraction is off: fusing x*c_hi into a later step would change the
+// algorithm.
+namespace trig {
+constexpr float kInvTwoPiHi = 0.15915493667125701904296875f;   // float32(1/(2 pi))
+constexpr float kInvTwoPiLo = 6.4206383e-09f;                   // 1/(2 pi) - kInvTwoPiHi
+constexpr float kMaxArg = 4194304.0f;                           // 2^22
+}  // namespace trig
+
+__device__ __forceinline__ void sincos_hw(float x, float& s, float& c) {
+#pragma clang fp contract(off)
+  const float k = rintf(x * trig::kInvTwoPiHi);
+  const float f = fmaf(x, trig::kInvTwoPiLo, fmaf(x, trig::kInvTwoPiHi, -k));
+  s = __builtin_amdgcn_sinf(f);
+  c = __builtin_amdgcn_cosf(f);
 }
 
 // Counter-based dropout: keep entry i with probability 1-p, decided by a 32-bit hash of

@@ -551,11 +551,11 @@ void check_kspace(const at::Tensor& t, const fa_tgat_graph& g, int64_t heads, co
   CHECK_INPUT(t);
   CHECK_DTYPE(t, at::kFloat);
   const int64_t kp = fa_tgat_kspace(g.dn, g.de, g.dt_dim);
-  TORCH_CHECK(t.dim() == 3 && t.size(0) == heads && t.size(1) == g.n_dst && t.size(2) == kp, name,
-              " must be [heads, n_dst, ", kp, "]");
+  TORCH_CHECK(t.dim() == 3 && t.size(0) == g.n_dst && t.size(1) == heads && t.size(2) == kp, name,
+              " must be [n_dst, heads, ", kp, "]");
 }
 
-// -> [xbar [H, N, Kp], scores [E, H], stats [N, H, 2]]
+// -> [xbar [N, H, Kp], scores [E, H], stats [N, H, 2]]
 std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> node_idx, at::Tensor edge_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
@@ -563,7 +563,8 @@ std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
                                       double slope, std::optional<at::Tensor> drop,
                                       uint64_t drop_seed, double drop_p) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
-  const int64_t H = qt.size(0);
+  TORCH_CHECK(qt.dim() == 3, "qt must be [n_dst, heads, Kp]");
+  const int64_t H = qt.size(1);
   check_kspace(qt, g, H, "qt");
   const float* dptr = nullptr;
   if (drop.has_value()) {
@@ -597,7 +598,8 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
                                       bool need_d_node) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
-  const int64_t H = qt.size(0);
+  TORCH_CHECK(qt.dim() == 3, "qt must be [n_dst, heads, Kp]");
+  const int64_t H = qt.size(1);
   check_kspace(qt, g, H, "qt");
   check_kspace(xbar, g, H, "xbar");
   check_kspace(dxbar, g, H, "dxbar");

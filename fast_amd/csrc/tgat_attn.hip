@@ -2,26 +2,28 @@
 //
 // For destination v with edges e in rowptr[v]..rowptr[v+1] and heads h:
 //   x_e        = [node_tab[node_row(e)] | edge_tab[edge_row(e)] | cos(w*dt_e + b) | 1]
-//   z[e,h]     = qt[h,v,:] . x_e                     (qt = Q_h W_k,aug[h], bias in col Kb)
+//   z[e,h]     = qt[v,h,:] . x_e                     (qt = Q_h W_k,aug[h], bias in col Kb)
 //   s[e,h]     = leaky_relu(z, slope)
 //   a[e,h]     = exp(s - max_v,h) / sum_v,h          (softmax over the destination's edges)
-//   xbar[h,v]  = sum_e a[e,h] * drop[e,h] * x_e      (column Kb = sum_e a*drop)
+//   xbar[v,h]  = sum_e a[e,h] * drop[e,h] * x_e      (column Kb = sum_e a*drop)
 //
 // x_e is gathered and time-encoded on the fly and never stored. Layout of one row in
 // "K-space" (float4 chunks): node chunks [0,cn), edge chunks [cn,cn+ce), time chunks
-// [cn+ce, cn+ce+ct), then one bias chunk (1,0,0,0). One wavefront per destination;
-// lane l owns chunks l, l+64, ... (NS slots).
+// [cn+ce, cn+ce+ct), then one bias chunk (1,0,0,0). One wavefront per destination
+// (grid-stride); lane l owns chunks l, l+64, ... (NS slots). Per-destination rows (qt,
+// xbar, dxbar, dqt) are [heads][Kp] blocks at a row stride per destination.
 //
-// Every lane runs the same instruction stream in the edge loops: gathers are buffer loads
-// through a per-row descriptor (lanes whose chunk lies in the other table, or a row out of
-// range, read zeros), per-destination rows are buffer loads / stores bounded by the row
-// length, and the per-lane chunk kinds are applied with selects.
+// Gathers are buffer loads through a per-row descriptor sized to the row (reads past the
+// row end or of a row id out of range return 0), issued only by the lanes whose chunk lies
+// in that table; the other lanes take their chunk (time, bias or zero) from a per-wave LDS
+// tile row. Wave-level control flow depends only on wave-uniform values, except for those
+// exec-masked loads and LDS reads.
 //
 // Latency structure: the per-edge ids, dt, dropout multipliers (and scores in backward) of
 // up to 64 edges are loaded with one coalesced vector load per array and broadcast with
 // readlane; row gathers run two batches deep (the next batch's loads are in flight while
 // the current one is scored); time encodings are evaluated by all 64 lanes (dims lane,
-// lane+64, ...) into a per-wave LDS tile.
+// lane+64, ...) into the LDS tile.
 //
 // Backward, per destination, in one pass over the edges:
 //   T_h     = dxbar[h] . xbar[h]                      (= sum_e a*drop*(dxbar[h] . x_e))
@@ -36,7 +38,6 @@
 namespace fa {
 namespace {
 
-enum ChunkKind : int { kNode = 0, kEdge = 1, kTime = 2, kBias = 3, kNone = 4 };
 
 // Tunables (build-time): edges per batch (two batches are in flight), and the minimum
 // waves per SIMD the compiler must allow for the forward / backward kernels.
@@ -50,7 +51,7 @@ enum ChunkKind : int { kNode = 0, kEdge = 1, kTime = 2, kBias = 3, kNone = 4 };
 #define FA_TGAT_BWD_WAVES 1
 #endif
 constexpr int kBatch = FA_TGAT_BATCH;
-constexpr int kBwdMaxBlocks = 2048;   // backward grid cap (time-grad partial rows)
+constexpr int kMaxBlocks = 2048;      // grid cap of the grid-stride kernels (time-grad partial rows)
 constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every descriptor's range
 
 struct TgatParams {
@@ -63,16 +64,16 @@ struct TgatParams {
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
   int tvs;                            // LDS row stride of the tiles: 4*ct + bias chunk + zero chunk
   int64_t kp;                         // row stride of qt / xbar = 4*cp
-  const float* qt; int64_t qt_hs;
+  const float* qt; int64_t qt_rs;
   float slope;
   const float* drop;                  // explicit [E][H] multipliers, or
   uint64_t drop_seed; float drop_p, drop_scale; int drop_hash;  // hashed dropout
   // forward outputs / backward input
-  float* xbar; int64_t xbar_hs;
+  float* xbar; int64_t xbar_rs;
   float* scores; float* stats;
   // backward
-  const float* dxbar; int64_t dxbar_hs;
-  float* dqt; int64_t dqt_hs;
+  const float* dxbar; int64_t dxbar_rs;
+  float* dqt; int64_t dqt_rs;
   float* d_node; int64_t ld_dnode;
   float* partial;                     // [gridDim.x][2][dt_dim]
 };
@@ -90,6 +91,16 @@ __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
   return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                      __uint_as_float(v[3]));
+}
+
+// Four dword loads: each dword is range-checked on its own, so a chunk that crosses the end
+// of the row keeps its in-range part and reads 0 past it.
+__device__ __forceinline__ float4 bload4_dwords(rsrc_t r, uint32_t off) {
+  const int o = static_cast<int>(off);
+  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
 }
 
 // Four dword stores: each dword is range-checked on its own, so a chunk that crosses the end
@@ -110,15 +121,6 @@ __device__ __forceinline__ void bstore4(rsrc_t r, uint32_t off, const float4& x)
   v[2] = __float_as_uint(x.z);
   v[3] = __float_as_uint(x.w);
   __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
-}
-
-__device__ __forceinline__ float4 sel4(bool c, const float4& a, const float4& b) {
-  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
-}
-
-// Keeps the first `valid` components (a chunk that crosses the end of a feature row).
-__device__ __forceinline__ float4 keep_first(const float4& v, int valid) {
-  return make_float4(v.x, valid > 1 ? v.y : 0.f, valid > 2 ? v.z : 0.f, valid > 3 ? v.w : 0.f);
 }
 
 __device__ __forceinline__ int64_t clamp_edge(int64_t e, int64_t n_edges) {
@@ -144,11 +146,11 @@ __device__ __forceinline__ float lane_flt(float v, int j) {
 // picks between two values with one select and no branch.
 template <int NS>
 struct LaneCtx {
-  uint32_t noff[NS];      // byte offset in the node row (kOob elsewhere; gradient stores)
-  int roff[NS];           // element offset of a row chunk inside its row (0 elsewhere)
+  uint32_t noff[NS];      // byte offset of a node chunk in the node row (kOob elsewhere)
+  uint32_t eoff[NS];      // byte offset of an edge chunk in the edge row (kOob elsewhere)
   uint32_t toff[NS];      // element offset of the chunk in the LDS tile row (zero chunk for rows)
-  int valid[NS];          // valid components of a row chunk (4 elsewhere)
   bool is_node[NS], is_edge[NS];
+  bool slot_node[NS], slot_time[NS];  // wave-uniform: slot k holds some node / time chunk
   float w0, b0, w1, b1;   // time dims j = lane and lane + 64
 };
 
@@ -158,20 +160,18 @@ __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) 
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
     const int c = lane + k * kWave;
+    L.slot_node[k] = k * kWave < P.cn;
+    L.slot_time[k] = P.ct > 0 && k * kWave < P.cn + P.ce + P.ct && (k + 1) * kWave > P.cn + P.ce;
     L.noff[k] = kOob;
-    L.roff[k] = 0;
+    L.eoff[k] = kOob;
     L.toff[k] = 4u * static_cast<uint32_t>(P.ct + 1);
-    L.valid[k] = 4;
     L.is_node[k] = false;
     L.is_edge[k] = false;
     if (c < P.cn) {
       L.noff[k] = 16u * static_cast<uint32_t>(c);
-      L.roff[k] = 4 * c;
-      L.valid[k] = min(4, P.dn - 4 * c);
       L.is_node[k] = true;
     } else if (c < P.cn + P.ce) {
-      L.roff[k] = 4 * (c - P.cn);
-      L.valid[k] = min(4, P.de - 4 * (c - P.cn));
+      L.eoff[k] = 16u * static_cast<uint32_t>(c - P.cn);
       L.is_edge[k] = true;
     } else if (c < P.cn + P.ce + P.ct) {
       L.toff[k] = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
@@ -245,21 +245,14 @@ __device__ __forceinline__ int64_t meta_edge(const EdgeMeta<H, SCORES>& M, int j
                               static_cast<uint32_t>(lane_int(M.elo, j)));
 }
 
-// Four dword loads of row[o..o+3] with the indices clamped into the row (the components past
-// its end are zeroed later), for rows whose width is not a multiple of 4.
-__device__ __forceinline__ float4 load4_clamped(const float* row, int o, int last) {
-  return make_float4(row[min(o, last)], row[min(o + 1, last)], row[min(o + 2, last)],
-                     row[min(o + 3, last)]);
-}
-
-// Issues the row-chunk loads of batch entries [jb, jb+nb): one load per slot from a per-lane
-// address (node row or edge row).
-// ok[b] bit 0 / 1: the node / edge row of entry b is in range (rows out of range are read
-// as row 0 and zeroed when the batch is assembled).
+// Issues the row-chunk loads of batch entries [jb, jb+nb): the lanes of node chunks load
+// from the node row, the lanes of edge chunks from the edge row, through buffer
+// descriptors whose range is the row itself (zero for a row id out of range), so the
+// hardware returns 0 past the row end and for missing rows; the other lanes load nothing.
 template <int NS, int H, bool SCORES>
 __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS>& L,
                                            const EdgeMeta<H, SCORES>& M, int jb, int nb,
-                                           float4 (&x)[kBatch][NS], int (&ok)[kBatch]) {
+                                           float4 (&x)[kBatch][NS]) {
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b < nb) {
@@ -267,22 +260,14 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
       const int64_t erow = meta_edge(M, jb + b);
       const bool nok = nrow >= 0 && nrow < P.n_node;
       const bool eok = erow >= 0 && erow < P.n_erow;
-      ok[b] = (nok ? 1 : 0) | (eok ? 2 : 0);
-      if (P.dn + P.de == 0) continue;
-      const float* nptr = P.node_tab + (nok ? nrow : 0) * P.ld_node;
-      const float* eptr = P.edge_tab + (eok ? erow : 0) * P.ld_edge;
+      const rsrc_t nr = make_rsrc(P.node_tab + (nok ? nrow : 0) * P.ld_node,
+                                  nok ? 4u * static_cast<uint32_t>(P.dn) : 0u);
+      const rsrc_t er = make_rsrc(P.edge_tab + (eok ? erow : 0) * P.ld_edge,
+                                  eok ? 4u * static_cast<uint32_t>(P.de) : 0u);
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
-        // only the lanes of row chunks load (the others take their chunk from LDS)
-        if (L.is_node[k] || L.is_edge[k]) {
-          const float* row = L.is_node[k] ? nptr : eptr;
-          if (P.node_tail || P.edge_tail) {
-            const int last = (L.is_node[k] ? P.dn : P.de) - 1;
-            x[b][k] = load4_clamped(row, L.roff[k], last);
-          } else {
-            x[b][k] = *reinterpret_cast<const float4*>(row + L.roff[k]);
-          }
-        }
+        if (L.is_node[k]) x[b][k] = P.node_tail ? bload4_dwords(nr, L.noff[k]) : bload4(nr, L.noff[k]);
+        else if (L.is_edge[k]) x[b][k] = P.edge_tail ? bload4_dwords(er, L.eoff[k]) : bload4(er, L.eoff[k]);
       }
     }
   }
@@ -290,16 +275,15 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
 
 template <bool SIN>
 __device__ __forceinline__ void encode_one(float a, float* rc, float* rs, int j, bool ok) {
-  if (SIN) {
-    float sv, cv;
-    sincosf(a, &sv, &cv);
-    if (ok) {
-      rc[j] = cv;
-      rs[j] = -sv;
-    }
-  } else {
-    const float cv = cosf(a);
-    if (ok) rc[j] = cv;
+  float sv, cv;
+  sincos_hw(a, sv, cv);
+  if (fabsf(a) > trig::kMaxArg) {  // outside the reduction's range (not expected for times)
+    if (SIN) sincosf(a, &sv, &cv);
+    else cv = cosf(a);
+  }
+  if (ok) {
+    rc[j] = cv;
+    if (SIN) rs[j] = -sv;
   }
 }
 
@@ -327,51 +311,42 @@ __device__ __forceinline__ void encode_times(const TgatParams& P, const LaneCtx<
   }
 }
 
-// Assembles the batch's chunks: row chunks from the loads (zeroed past the row end and for
-// rows out of range), every other chunk from the LDS tile row. Entries past nb are left as
-// they are (their results are not used).
+// Completes the batch's chunks: lanes of row chunks keep what they loaded, every other lane
+// reads its chunk (time, bias or zero) from the LDS tile row of the entry.
 template <int NS>
 __device__ __forceinline__ void assemble_x(const TgatParams& P, const LaneCtx<NS>& L, int nb,
-                                           const float* tc, const int (&ok)[kBatch],
-                                           float4 (&x)[kBatch][NS]) {
-  const bool tails = P.node_tail || P.edge_tail;
+                                           const float* tc, float4 (&x)[kBatch][NS]) {
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b >= nb) break;
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
-      const float4 tv = *reinterpret_cast<const float4*>(tc + b * P.tvs + L.toff[k]);
-      float4 rv = x[b][k];
-      if (tails) rv = keep_first(rv, L.valid[k]);
-      bool row = L.is_node[k] || L.is_edge[k];
-      if (ok[b] != 3) {  // wave-uniform: an out-of-range row reads as zeros
-        const bool bad = (L.is_node[k] && !(ok[b] & 1)) || (L.is_edge[k] && !(ok[b] & 2));
-        rv = sel4(bad, f4_zero(), rv);
-      }
-      x[b][k] = sel4(row, rv, tv);
-    }
+    for (int k = 0; k < NS; ++k)
+      if (!(L.is_node[k] || L.is_edge[k]))
+        x[b][k] = *reinterpret_cast<const float4*>(tc + b * P.tvs + L.toff[k]);
   }
 }
 
+// Rows of a per-destination [heads][Kp] block: destination v starts at base + v*rs, head h
+// at + h*kp.
 template <int H, int NS>
-__device__ __forceinline__ void load_rows(const float* base, int64_t hs, int64_t v, int64_t kp,
+__device__ __forceinline__ void load_rows(const float* base, int64_t rs, int64_t v, int64_t kp,
                                           float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const rsrc_t rr = make_rsrc(base + h * hs + v * kp, 4u * static_cast<uint32_t>(kp));
+    const rsrc_t rr = make_rsrc(base + v * rs + h * kp, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
     for (int k = 0; k < NS; ++k) r[h][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
   }
 }
 
 template <int H, int NS>
-__device__ __forceinline__ void store_rows(float* base, int64_t hs, int64_t v, int64_t kp,
+__device__ __forceinline__ void store_rows(float* base, int64_t rs, int64_t v, int64_t kp,
                                            const float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const rsrc_t rr = make_rsrc(base + h * hs + v * kp, 4u * static_cast<uint32_t>(kp));
+    const rsrc_t rr = make_rsrc(base + v * rs + h * kp, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
     for (int k = 0; k < NS; ++k) bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), r[h][k]);
   }
@@ -386,7 +361,8 @@ __device__ __forceinline__ float row_dot(const float4 (&a)[NS], const float4 (&b
 }
 
 // ---------------------------------------------------------------------------------
-// Forward: one wave per destination, online softmax over batches of kBatch edges.
+// Forward: one wave per destination (grid-stride over destinations), online softmax over
+// batches of kBatch edges.
 // Dynamic LDS: per wave one [kBatch][tvs] cosine tile.
 // ---------------------------------------------------------------------------------
 template <int H, int NS>
@@ -400,14 +376,14 @@ template <int H, int NS>
 __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
                                           const EdgeMeta<H, false>& M, int64_t c0, int jb, int nb,
                                           float* tc, float4 (&x)[kBatch][NS],
-                                          const int (&ok)[kBatch], FwdState<H, NS>& S) {
+                                          FwdState<H, NS>& S) {
   const int lane = lane_id();
   if (P.dt_dim > 0) {
     lds_sync();
     encode_times<NS, H, false, false>(P, L, M, jb, nb, tc, nullptr);
     lds_sync();
   }
-  assemble_x<NS>(P, L, nb, tc, ok, x);
+  assemble_x<NS>(P, L, nb, tc, x);
   float sc[kBatch][H];
 #pragma unroll
   for (int b = 0; b < kBatch; ++b)
@@ -432,13 +408,13 @@ __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>
       // online softmax; s and m are wave-uniform, so this branch does not diverge. The
       // first edge has m = -inf and r = 0.
       if (s > S.m[h]) {
-        const float r = expf(S.m[h] - s);
+        const float r = exp_fast(S.m[h] - s);
         S.l[h] *= r;
 #pragma unroll
         for (int k = 0; k < NS; ++k) scale4(S.acc[h][k], r);
         S.m[h] = s;
       }
-      const float pe = expf(s - S.m[h]);
+      const float pe = exp_fast(s - S.m[h]);
       S.l[h] += pe;
       const float w = pe * dr;
 #pragma unroll
@@ -450,79 +426,74 @@ __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>
 template <int H, int NS>
 __global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams P) {
   extern __shared__ float lds[];
-  const int wave = threadIdx.x / kWave;
-  const int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave;
-  if (v >= P.n_dst) return;
+  const int wave = uniform(threadIdx.x / kWave);
   const int lane = lane_id();
-  const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
-  const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
-
-  FwdState<H, NS> S;
-#pragma unroll
-  for (int h = 0; h < H; ++h) {
-    S.m[h] = -INFINITY;
-    S.l[h] = 0.f;
-#pragma unroll
-    for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
-  }
-  if (e1 <= e0) {  // zero-degree destination: xbar = 0
-    store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc);
-    if (lane < H) {
-      P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
-      P.stats[(v * H + lane) * 2 + 1] = 0.f;
-    }
-    return;
-  }
-
   float* tc = lds + wave * (kBatch * P.tvs);
   LaneCtx<NS> L;
   setup_lane<NS>(P, L);
   init_tiles(P, tc, kBatch, kBatch);
-  load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q);
 
-  for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
-    const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
-    EdgeMeta<H, false> M;
-    stage_meta<H, false>(P, c0, cnt, M);
-    float4 xa[kBatch][NS], xb[kBatch][NS];
-    int oka[kBatch], okb[kBatch];
-    issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa, oka);
-    for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
-      const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
-      const int nb2 = cnt - jb - kBatch;
-      const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
-      if (nb > 0) issue_rows<NS, H, false>(P, L, M, jb + kBatch, nb, xb, okb);
-      fwd_batch<H, NS>(P, L, M, c0, jb, na, tc, xa, oka, S);
-      if (nb > 0) {
-        const int nn2 = cnt - jb - 2 * kBatch;
-        const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
-        if (nn > 0) issue_rows<NS, H, false>(P, L, M, jb + 2 * kBatch, nn, xa, oka);
-        fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, okb, S);
-      }
-    }
-  }
-
-#pragma unroll
-  for (int h = 0; h < H; ++h) {
-    const float lsum = S.l[h];
-#pragma unroll
-    for (int k = 0; k < NS; ++k) {
-      S.acc[h][k].x /= lsum;
-      S.acc[h][k].y /= lsum;
-      S.acc[h][k].z /= lsum;
-      S.acc[h][k].w /= lsum;
-    }
-  }
-  store_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, S.acc);
-  if (lane < H) {
-    float mm = 0.f, ll = 0.f;
+  const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; v < P.n_dst;
+       v += total_waves) {
+    const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
+    const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
+    FwdState<H, NS> S;
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      mm = lane == h ? S.m[h] : mm;
-      ll = lane == h ? S.l[h] : ll;
+      S.m[h] = -INFINITY;
+      S.l[h] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
     }
-    P.stats[(v * H + lane) * 2 + 0] = mm;
-    P.stats[(v * H + lane) * 2 + 1] = ll;
+    if (e1 <= e0) {  // zero-degree destination: xbar = 0
+      store_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, S.acc);
+      if (lane < H) {
+        P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
+        P.stats[(v * H + lane) * 2 + 1] = 0.f;
+      }
+      continue;
+    }
+    load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
+
+    for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
+      const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      EdgeMeta<H, false> M;
+      stage_meta<H, false>(P, c0, cnt, M);
+      float4 xa[kBatch][NS], xb[kBatch][NS];
+      issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+      for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
+        const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
+        const int nb2 = cnt - jb - kBatch;
+        const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
+        if (nb > 0) issue_rows<NS, H, false>(P, L, M, jb + kBatch, nb, xb);
+        fwd_batch<H, NS>(P, L, M, c0, jb, na, tc, xa, S);
+        if (nb > 0) {
+          const int nn2 = cnt - jb - 2 * kBatch;
+          const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
+          if (nn > 0) issue_rows<NS, H, false>(P, L, M, jb + 2 * kBatch, nn, xa);
+          fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, S);
+        }
+      }
+    }
+
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float inv = 1.f / S.l[h];
+#pragma unroll
+      for (int k = 0; k < NS; ++k) scale4(S.acc[h][k], inv);
+    }
+    store_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, S.acc);
+    if (lane < H) {
+      float mm = 0.f, ll = 0.f;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        mm = lane == h ? S.m[h] : mm;
+        ll = lane == h ? S.l[h] : ll;
+      }
+      P.stats[(v * H + lane) * 2 + 0] = mm;
+      P.stats[(v * H + lane) * 2 + 1] = ll;
+    }
   }
 }
 
@@ -542,13 +513,13 @@ template <int H, int NS>
 __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>& L,
                                           const EdgeMeta<H, true>& M, int64_t c0, int jb, int nb,
                                           float* tc, float* ts, float4 (&x)[kBatch][NS],
-                                          const int (&ok)[kBatch], BwdState<H, NS>& S) {
+                                          BwdState<H, NS>& S) {
   if (P.dt_dim > 0) {
     lds_sync();
     encode_times<NS, H, true, true>(P, L, M, jb, nb, tc, ts);
     lds_sync();
   }
-  assemble_x<NS>(P, L, nb, tc, ok, x);
+  assemble_x<NS>(P, L, nb, tc, x);
   float dap[kBatch][H];
 #pragma unroll
   for (int b = 0; b < kBatch; ++b)
@@ -565,7 +536,7 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
     for (int h = 0; h < H; ++h) {
       const float s = lane_flt(M.sc[h], j);
       const float dr = lane_flt(M.dr[h], j);
-      const float a = expf(s - S.mh[h]) * S.il[h];
+      const float a = exp_fast(s - S.mh[h]) * S.il[h];
       ad[h] = a * dr;
       dz[h] = a * (dr * dap[b][h] - S.T[h]) * (s > 0.f ? 1.f : P.slope);
 #pragma unroll
@@ -576,6 +547,10 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
                                 P.d_node ? 4u * static_cast<uint32_t>(P.dn) : 0u);
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
+      // the input gradient dx_e is used for node chunks (when d_node is wanted) and time
+      // chunks only; slots holding neither are skipped (a wave-uniform test)
+      const bool want_node = P.d_node && L.slot_node[k];
+      if (!(want_node || L.slot_time[k])) continue;
       float4 dx = f4_zero();
 #pragma unroll
       for (int h = 0; h < H; ++h) {
@@ -583,12 +558,12 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
         fma4(dx, dz[h], S.q[h][k]);
       }
       // node-row gradient (the descriptor drops the lanes outside the node part)
-      if (P.d_node) {
+      if (want_node) {
         if (P.node_tail) bstore4_dwords(rd, L.noff[k], dx);
         else bstore4(rd, L.noff[k], dx);
       }
       // d cos(w t + b) = -sin(w t + b) * (t dw + db); the pad dims carry dx = 0
-      if (P.dt_dim > 0) {
+      if (L.slot_time[k]) {
         // the -sin tile is zero outside the time dims, so only time chunks contribute
         const float4 sn = *reinterpret_cast<const float4*>(ts + b * P.tvs + L.toff[k]);
         const float4 pr = make_float4(sn.x * dx.x, sn.y * dx.y, sn.z * dx.z, sn.w * dx.w);
@@ -606,7 +581,7 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
 template <int H, int NS>
 __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams P) {
   extern __shared__ float lds[];
-  const int wave = threadIdx.x / kWave;
+  const int wave = uniform(threadIdx.x / kWave);
   float* tc = lds + wave * (2 * kBatch * P.tvs);
   float* ts = tc + kBatch * P.tvs;
   float* red = lds + kWavesPerBlock * 2 * kBatch * P.tvs;
@@ -628,11 +603,11 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
     if (e1 <= e0) {
-      store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq);
+      store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
       continue;
     }
-    load_rows<H, NS>(P.qt, P.qt_hs, v, P.kp, S.q);
-    load_rows<H, NS>(P.dxbar, P.dxbar_hs, v, P.kp, S.g);
+    load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
+    load_rows<H, NS>(P.dxbar, P.dxbar_rs, v, P.kp, S.g);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
@@ -640,7 +615,7 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
     }
     {
       float4 xr[H][NS];
-      load_rows<H, NS>(P.xbar, P.xbar_hs, v, P.kp, xr);
+      load_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, xr);
 #pragma unroll
       for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xr[h]));
     }
@@ -650,23 +625,22 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
       EdgeMeta<H, true> M;
       stage_meta<H, true>(P, c0, cnt, M);
       float4 xa[kBatch][NS], xb[kBatch][NS];
-      int oka[kBatch], okb[kBatch];
-      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa, oka);
+      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
         const int nb2 = cnt - jb - kBatch;
         const int nb = nb2 < 0 ? 0 : (nb2 < kBatch ? nb2 : kBatch);
-        if (nb > 0) issue_rows<NS, H, true>(P, L, M, jb + kBatch, nb, xb, okb);
-        bwd_batch<H, NS>(P, L, M, c0, jb, na, tc, ts, xa, oka, S);
+        if (nb > 0) issue_rows<NS, H, true>(P, L, M, jb + kBatch, nb, xb);
+        bwd_batch<H, NS>(P, L, M, c0, jb, na, tc, ts, xa, S);
         if (nb > 0) {
           const int nn2 = cnt - jb - 2 * kBatch;
           const int nn = nn2 < 0 ? 0 : (nn2 < kBatch ? nn2 : kBatch);
-          if (nn > 0) issue_rows<NS, H, true>(P, L, M, jb + 2 * kBatch, nn, xa, oka);
-          bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, okb, S);
+          if (nn > 0) issue_rows<NS, H, true>(P, L, M, jb + 2 * kBatch, nn, xa);
+          bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, S);
         }
       }
     }
-    store_rows<H, NS>(P.dqt, P.dqt_hs, v, P.kp, S.dq);
+    store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
   }
 
   // Time-grad partials of this workgroup: waves combined in a fixed order. Every time dim
@@ -738,7 +712,7 @@ __global__ __launch_bounds__(kBlock) void gather_rows(const float* tab, int64_t 
 // ---------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------
-int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_hs, float slope,
+int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_rs, float slope,
                 const float* drop, uint64_t drop_seed, float drop_p, TgatParams& P) {
   if (!g || heads <= 0) return FA_EINVAL;
   if (g->n_dst < 0 || g->n_edges < 0 || g->dn < 0 || g->de < 0 || g->dt_dim < 0) return FA_EINVAL;
@@ -767,14 +741,15 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_h
   P.cp = P.cn + P.ce + P.ct + 1;
   P.tvs = 4 * (P.ct + 2);
   P.kp = 4 * static_cast<int64_t>(P.cp);
-  P.qt = qt; P.qt_hs = qt_hs; P.slope = slope; P.drop = drop;
+  P.qt = qt; P.qt_rs = qt_rs; P.slope = slope; P.drop = drop;
   if (!(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
   P.drop_seed = drop_seed;
   P.drop_p = drop_p;
   P.drop_scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
   P.drop_hash = (drop == nullptr && drop_p > 0.f) ? 1 : 0;
   if (!aligned16(qt)) return FA_EALIGN;
-  if (heads > 1 && ((qt_hs & 3) || qt_hs < P.kp * g->n_dst)) return FA_EINVAL;
+  if (qt_rs & 3) return FA_EALIGN;
+  if (qt_rs < P.kp * heads) return FA_EINVAL;
   return FA_OK;
 }
 
@@ -786,10 +761,16 @@ size_t bwd_lds_bytes(const TgatParams& P) {
   return sizeof(float) * static_cast<size_t>(kWavesPerBlock) * (2 * kBatch + 2) * P.tvs;
 }
 
+// Workgroups of a grid-stride launch over n_dst destinations (4 per workgroup pass).
+int stride_grid(int64_t n_dst) {
+  const int64_t want = ceil_div(n_dst, kWavesPerBlock);
+  return static_cast<int>(want < kMaxBlocks ? (want < 1 ? 1 : want) : kMaxBlocks);
+}
+
 template <int H>
 int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
-  const dim3 grid(static_cast<unsigned>(ceil_div(P.n_dst, kWavesPerBlock)));
+  const dim3 grid(static_cast<unsigned>(stride_grid(P.n_dst)));
   const size_t lds = fwd_lds_bytes(P);
   switch (ns) {
     case 1: hipLaunchKernelGGL((tgat_fwd<H, 1>), grid, dim3(kBlock), lds, stream, P); break;
@@ -803,10 +784,7 @@ int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
 
 constexpr size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup used by the fused kernels
 
-int bwd_grid(int64_t n_dst) {
-  const int64_t want = ceil_div(n_dst, kWavesPerBlock);
-  return static_cast<int>(want < kBwdMaxBlocks ? (want < 1 ? 1 : want) : kBwdMaxBlocks);
-}
+int bwd_grid(int64_t n_dst) { return stride_grid(n_dst); }
 
 template <int H>
 int launch_bwd_h(const TgatParams& P, int grid, hipStream_t stream) {
@@ -833,18 +811,19 @@ extern "C" int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim) {
 }
 
 extern "C" int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_hs, float slope, const float* drop,
+                                    int64_t qt_rs, float slope, const float* drop,
                                     uint64_t drop_seed, float drop_p, float* xbar,
-                                    int64_t xbar_hs, float* scores, float* stats,
+                                    int64_t xbar_rs, float* scores, float* stats,
                                     hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_hs, slope, drop, drop_seed, drop_p, P);
+  int st = fill_params(g, heads, qt, qt_rs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) return FA_OK;
   if (fwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
   if (!xbar || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if (!aligned16(xbar) || (xbar_hs & 3) || (heads > 1 && xbar_hs < P.kp * P.n_dst)) return FA_EALIGN;
-  P.xbar = xbar; P.xbar_hs = xbar_hs; P.scores = scores; P.stats = stats;
+  if (!aligned16(xbar) || (xbar_rs & 3)) return FA_EALIGN;
+  if (xbar_rs < P.kp * heads) return FA_EINVAL;
+  P.xbar = xbar; P.xbar_rs = xbar_rs; P.scores = scores; P.stats = stats;
   if (static_cast<int64_t>(kBatch) * heads > kWave) return FA_EUNSUPPORTED;
   switch (heads) {
     case 1: return launch_fwd_h<1>(P, stream);
@@ -872,15 +851,15 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
 }
 
 extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_hs, float slope, const float* drop,
+                                    int64_t qt_rs, float slope, const float* drop,
                                     uint64_t drop_seed, float drop_p,
-                                    const float* xbar, int64_t xbar_hs, const float* scores,
-                                    const float* stats, const float* dxbar, int64_t dxbar_hs,
-                                    float* dqt, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
+                                    const float* xbar, int64_t xbar_rs, const float* scores,
+                                    const float* stats, const float* dxbar, int64_t dxbar_rs,
+                                    float* dqt, int64_t dqt_rs, float* d_node, int64_t ld_dnode,
                                     float* d_time_w, float* d_time_b, void* scratch,
                                     size_t scratch_bytes, hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_hs, slope, drop, drop_seed, drop_p, P);
+  int st = fill_params(g, heads, qt, qt_rs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) {
     if (P.dt_dim > 0 && d_time_w && d_time_b) {
@@ -891,19 +870,18 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   }
   if (bwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
   if (!xbar || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if (!aligned16(xbar) || !aligned16(dxbar) || !aligned16(dqt) || (xbar_hs & 3) || (dxbar_hs & 3) ||
-      (dqt_hs & 3))
+  if (!aligned16(xbar) || !aligned16(dxbar) || !aligned16(dqt) || (xbar_rs & 3) || (dxbar_rs & 3) ||
+      (dqt_rs & 3))
     return FA_EALIGN;
-  if (heads > 1 &&
-      (xbar_hs < P.kp * P.n_dst || dxbar_hs < P.kp * P.n_dst || dqt_hs < P.kp * P.n_dst))
+  if (xbar_rs < P.kp * heads || dxbar_rs < P.kp * heads || dqt_rs < P.kp * heads)
     return FA_EINVAL;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   const int grid = bwd_grid(P.n_dst);
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
-  P.xbar = const_cast<float*>(xbar); P.xbar_hs = xbar_hs;
-  P.dxbar = dxbar; P.dxbar_hs = dxbar_hs; P.dqt = dqt; P.dqt_hs = dqt_hs;
+  P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs;
+  P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dqt = dqt; P.dqt_rs = dqt_rs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
   // 16-byte node-gradient stores need 16-byte aligned gradient rows as well
   if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.node_tail = true;

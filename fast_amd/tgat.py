@@ -5,14 +5,16 @@ order, initialisation) and ``forward(b, _layers, _hist)`` of the reference layer
 (layers.py:53-240, TGAT/TGN branch) and computes the same function. Its data path differs:
 
   reference                                   this layer
-  K = w_k(cat[h_src, f, cos(w dt+b)])  [E,D]  qt[h,v] = Q[v,h] W_k[h] (+ b_k column)   [H,N,Kp]
-  V = w_v(cat[...])                    [E,D]  xbar[h,v] = sum_e a'[e,h] x_e (one kernel) [H,N,Kp]
-  score = sum(Q[dst]*K), softmax, V*att,      out[v,h] = W_v[h] xbar[h,v] (+ b_v * sum a')
-  update_all(copy_u, sum)
+  K = w_k(cat[h_src, f, cos(w dt+b)])  [E,D]  qt[v,h] = Q[v,h] W_k[h] (+ b_k column)   [N,H,Kp]
+  V = w_v(cat[...])                    [E,D]  xbar[v,h] = sum_e a'[e,h] x_e (one kernel) [N,H,Kp]
+  score = sum(Q[dst]*K), softmax, V*att,      rst = w_out([W_v xbar | h_dst])
+  update_all(copy_u, sum), w_out
 
-so the K/V projections run over the N destinations instead of the E edges, and the
-neighbour gather, time encoding, scoring, segment softmax and weighted reduction happen in
-one pass over the gathered rows x_e (never written to memory).
+so the K/V projections run over the N destinations instead of the E edges (and fold into
+the neighbouring projections: qt comes from h_dst in one product, xbar goes through
+W_o[:, :D] W_v in one product), and the neighbour gather, time encoding, scoring, segment
+softmax and weighted reduction happen in one pass over the gathered rows x_e (never
+written to memory).
 """
 from __future__ import annotations
 
@@ -256,7 +258,7 @@ class _Graph:
 class TgatAttention(torch.autograd.Function):
     """xbar = fused gather/time-encode/score/softmax/reduce (see module docstring).
 
-    Differentiable inputs: ``qt`` [H,N,Kp], ``time_w`` [Dt], ``time_b`` [Dt] and
+    Differentiable inputs: ``qt`` [N,H,Kp], ``time_w`` [Dt], ``time_b`` [Dt] and
     ``node_src`` (the node rows feeding the edges: one row per edge when ``node_idx`` is
     None, else a table gathered by ``node_idx``)."""
 
@@ -269,8 +271,8 @@ class TgatAttention(torch.autograd.Function):
                                                     float(slope), drop, int(drop_seed),
                                                     float(drop_p))
         if t0 is not None:
-            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
-                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
+            nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
                                     g.node_idx is not None, g.edge_idx is not None)["fwd"]
             timer.end("tgat_fwd", t0, nb)
         ctx.g = g
@@ -299,8 +301,8 @@ class TgatAttention(torch.autograd.Function):
                                                         ctx.drop_seed, ctx.drop_p, xbar,
                                                         scores, stats, dxbar, need_node)
         if t0 is not None:
-            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
-                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
+            nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
                                     g.node_idx is not None, g.edge_idx is not None,
                                     need_node)["bwd"]
             timer.end("tgat_bwd", t0, nb)
@@ -313,7 +315,7 @@ class TgatAttention(torch.autograd.Function):
         return dqt, d_tw, d_tb, d_src, None, None, None, None, None
 
 
-def _rows_t_mm(a: torch.Tensor, b: torch.Tensor, chunk: int = 8192) -> torch.Tensor:
+def _rows_t_mm(a: torch.Tensor, b: torch.Tensor, chunk: int = 2048) -> torch.Tensor:
     """a^T b for tall a [n, p], b [n, q], split over row chunks (one batched product
     plus a sum) so that the reduction over n spreads over many workgroups."""
     n = a.shape[0]
@@ -382,19 +384,14 @@ class TransfomerAttentionLayer(torch.nn.Module):
         self.w_out = torch.nn.Linear(dim_node_feat + dim_out, dim_out)
         self.layer_norm = torch.nn.LayerNorm(dim_out)
 
-    def _queries(self, hdst: Optional[torch.Tensor], N: int, device) -> torch.Tensor:
-        Dn, Dt, D = self.dim_node_feat, self.dim_time, self.dim_out
-        if Dn == 0 and Dt == 0:  # layers.py:137-140
-            return torch.ones(N, D, device=device)
-        Wq, bq = self.w_q.weight, self.w_q.bias
-        bias = bq
+    def _query_bias(self) -> Optional[torch.Tensor]:
+        """Bias of the query projection with the time encoding of dt = 0 for every
+        destination folded in (layers.py:109-110): b_q + W_q[:, Dn:] cos(b)."""
+        Dn, Dt = self.dim_node_feat, self.dim_time
+        bias = self.w_q.bias
         if Dt > 0:
-            # time encoding of dt = 0 for every destination (layers.py:109-110): cos(b)
-            zt = torch.cos(self.time_enc.w.bias)
-            bias = bq + torch.mv(Wq[:, Dn:], zt)
-        if Dn > 0:
-            return RowLinear.apply(hdst, Wq[:, :Dn], bias)
-        return bias.expand(N, D)
+            bias = bias + torch.mv(self.w_q.weight[:, Dn:], torch.cos(self.time_enc.w.bias))
+        return bias
 
     def forward(self, b: Block, _layers: int = 0, _hist: int = 0) -> torch.Tensor:
         p = self.att_dropout.p
@@ -417,10 +414,20 @@ class TransfomerAttentionLayer(torch.nn.Module):
         if E == 0:  # layers.py:101-102
             return torch.zeros((N, D), device=dev)
         hdst = b.dst_node_feats() if Dn > 0 else None
-        Q = self._queries(hdst, N, dev)
         kp = kspace_width(Dn, De, Dt)
-        wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt)
-        qt = torch.bmm(Q.view(N, H, dh).transpose(0, 1), wk.view(H, dh, kp))
+        # Absorbed keys: qt[v, h, :] = Q[v, h, :] W_k,aug[h], as one product
+        # hdst (Wk_blk W_q)^T + Wk_blk b_q with Wk_blk = blockdiag_h(W_k,aug[h]^T).
+        wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
+        wk_blk = torch.block_diag(*[wk[h].t() for h in range(H)])          # [H*kp, D]
+        if Dn + Dt == 0:  # layers.py:137-140: Q = 1
+            qt = wk_blk.sum(1).expand(N, H * kp).contiguous()
+        else:
+            qb = wk_blk @ self._query_bias()
+            if Dn > 0:
+                qt = RowLinear.apply(hdst, wk_blk @ self.w_q.weight[:, :Dn], qb)
+            else:
+                qt = qb.expand(N, H * kp).contiguous()
+        qt = qt.view(N, H, kp)
 
         node_src, node_idx = b.src_node_source() if Dn > 0 else (None, None)
         edge_tab, edge_idx = b.edge_source() if De > 0 else (None, None)
@@ -441,15 +448,18 @@ class TransfomerAttentionLayer(torch.nn.Module):
         xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop, drop_seed,
                                    drop_p)
 
-        wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt)
-        out = torch.bmm(xbar, wv.view(H, dh, kp).transpose(1, 2).contiguous())  # [H, N, dh]
-        agg = out.transpose(0, 1).reshape(N, D)
+        # Absorbed values and output projection: agg = xbar Wv_blk^T with
+        # Wv_blk = blockdiag_h(W_v,aug[h]), then rst = w_out([agg | hdst]) as
+        # xbar (W_o[:, :D] Wv_blk)^T + hdst W_o[:, D:]^T + b_o.
+        wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
+        wv_blk = torch.block_diag(*[wv[h] for h in range(H)])              # [D, H*kp]
         Wo = self.w_out.weight
+        xflat = xbar.view(N, H * kp)
         if Dn > 0:
-            rst = (RowLinear.apply(agg, Wo[:, :D], None)
+            rst = (RowLinear.apply(xflat, Wo[:, :D] @ wv_blk, None)
                    + RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias))
         else:
-            rst = RowLinear.apply(agg, Wo, self.w_out.bias)
+            rst = RowLinear.apply(xflat, Wo @ wv_blk, self.w_out.bias)
         rst = F.relu(self.dropout(rst))
         return self.layer_norm(rst)
 

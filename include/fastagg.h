@@ -173,9 +173,9 @@ int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* d
  * in "K-space": node features padded to Pn = roundup(Dn,4), edge features to
  * Pe = roundup(De,4), time encoding to Pt = roundup(Dt,4), then the constant 1 at
  * column Kb = Pn+Pe+Pt, zero-padded to Kp = roundup(Kb+1,4).
- * K and V are never formed per edge: with q~[h,v,:] = Q[v,h,:] W_k,aug[h] (bias in
+ * K and V are never formed per edge: with q~[v,h,:] = Q[v,h,:] W_k,aug[h] (bias in
  * column Kb) the score is q~.x_e, and the aggregation returns
- * xbar[h,v,:] = sum_e a'[e,h] x_e (column Kb = sum_e a'), to which the caller applies
+ * xbar[v,h,:] = sum_e a'[e,h] x_e (column Kb = sum_e a'), to which the caller applies
  * W_v,aug. Destination v owns edges rowptr[v]..rowptr[v+1] (clamped to [0, n_edges]).
  * ------------------------------------------------------------------------------- */
 
@@ -198,15 +198,18 @@ typedef struct fa_tgat_graph {
 /* K-space width Kp for the given dims (all > = 0). */
 int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim);
 
-/* Forward. qt: [heads][n_dst][Kp] (head stride qt_hs, row stride Kp).
+/* Forward. Per-destination blocks are [heads][Kp] rows: qt row of destination v, head h
+ * at qt + v*qt_rs + h*Kp (qt_rs >= heads*Kp, a multiple of 4), i.e. a [n_dst][heads][Kp]
+ * array when qt_rs = heads*Kp; xbar, dxbar and dqt below use the same layout with their own
+ * row strides.
  * Attention dropout: drop = optional explicit [n_edges][heads] multipliers (keep/(1-p) or
  * 0); when drop is NULL and drop_p > 0, entry (e,h) is kept iff the counter-based hash of
  * (drop_seed, e*heads+h) clears drop_p (see fa_dropout_mask_f32); drop_p = 0: no dropout.
- * Outputs: xbar [heads][n_dst][Kp] (head stride xbar_hs), scores [n_edges][heads]
- * (post-LeakyReLU), stats [n_dst][heads][2] = (max, sum of exp). */
+ * Outputs: xbar (row stride xbar_rs), scores [n_edges][heads] (post-LeakyReLU),
+ * stats [n_dst][heads][2] = (max, sum of exp). */
 int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
-                         float drop_p, float* xbar, int64_t xbar_hs, float* scores,
+                         int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,
+                         float drop_p, float* xbar, int64_t xbar_rs, float* scores,
                          float* stats, hipStream_t stream);
 
 /* The multipliers of the hashed attention dropout: out[i] = 1/(1-p) if
@@ -220,16 +223,16 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
                              hipStream_t stream);
 
 /* Backward, one pass over the edges. xbar: the forward output (its dot product with dxbar
- * gives each destination's softmax correction); dxbar: gradient of xbar (same layout).
- * Outputs: dqt (layout of qt, head stride dqt_hs); d_node [n_edges][ld_dnode] gradient of
- * the node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be
- * NULL when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
+ * gives each destination's softmax correction); dxbar: gradient of xbar. Outputs: dqt
+ * (layout of qt, row stride dqt_rs); d_node [n_edges][ld_dnode] gradient of the
+ * node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be NULL
+ * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
+                         int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,
                          float drop_p, const float* xbar,
-                         int64_t xbar_hs, const float* scores, const float* stats,
-                         const float* dxbar, int64_t dxbar_hs, float* dqt, int64_t dqt_hs,
+                         int64_t xbar_rs, const float* scores, const float* stats,
+                         const float* dxbar, int64_t dxbar_rs, float* dqt, int64_t dqt_rs,
                          float* d_node, int64_t ld_dnode, float* d_time_w, float* d_time_b,
                          void* scratch, size_t scratch_bytes, hipStream_t stream);
 

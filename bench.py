@@ -154,6 +154,9 @@ def main():
     from fast_amd.workloads import two_layer
 
     dev = torch.device("cuda:0")
+    # rocBLAS picks faster fp32 kernels than hipBLASLt for the layer's tall-skinny
+    # projections ([N, 100] x [100, 752] and transposes) on this stack
+    torch.backends.cuda.preferred_blas_library("cublas")
     torch.manual_seed(args.seed)
     enc = TGATEncoder(100, 172, 100, 2, 100, num_layers=2, dropout=0.1, att_dropout=0.1).to(dev)
     enc.train()

@@ -1,0 +1,230 @@
+// Fused epilogue of the temporal attention layer (layers.py:224-237):
+//   u   = r1 + r2                       (the two halves of w_out([agg | h_dst]), bias included)
+//   y   = relu(dropout(u))              (counter-hash dropout, multiplier 1/(1-p) or 0)
+//   out = (y - mean(y)) * rstd * gamma + beta,   rstd = 1/sqrt(var(y) + eps)   (LayerNorm)
+// and its backward. One wave per row (grid-stride); lane l holds columns l, l+64, ... of the
+// row (coalesced), so rows up to 64*kMaxPer columns wide are handled in registers. Row sums
+// use the wave reductions of fa_common.hpp. The weight / bias gradients of the LayerNorm
+// are accumulated per wave, combined per workgroup in a fixed order and summed over
+// workgroups by a second kernel (no float atomics).
+#include "fa_common.hpp"
+
+namespace fa {
+namespace {
+
+constexpr int kMaxPer = 4;          // columns per lane: rows up to 256 wide
+constexpr int kEpiMaxBlocks = 1024;  // grid cap (rows of the weight-gradient partials)
+
+struct EpiParams {
+  int64_t n;
+  int d;
+  const float* r1; int64_t ld1;
+  const float* r2; int64_t ld2;     // may be null
+  const float* gamma;
+  const float* beta;
+  float eps;
+  int drop;                         // apply the hashed dropout
+  uint64_t seed;
+  float p, scale;
+  float* out;
+  float* y;                         // [n][d] saved relu(dropout(u))
+  float* stats;                     // [n][2] mean, rstd
+};
+
+template <int PER>
+__global__ __launch_bounds__(kBlock) void epilogue_fwd(EpiParams P) {
+  const int lane = lane_id();
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const float inv_d = 1.f / static_cast<float>(P.d);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       r < P.n; r += total) {
+    float v[PER];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + i * kWave;
+      float u = 0.f;
+      if (c < P.d) {
+        u = P.r1[r * P.ld1 + c];
+        if (P.r2) u += P.r2[r * P.ld2 + c];
+        if (P.drop) u *= drop_mult(P.seed, static_cast<uint64_t>(r * P.d + c), P.p, P.scale);
+        u = u > 0.f ? u : 0.f;
+      }
+      v[i] = u;
+      s += u;
+    }
+    const float mean = wave_sum(s) * inv_d;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + i * kWave;
+      const float dv = c < P.d ? v[i] - mean : 0.f;
+      q += dv * dv;
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(q) * inv_d + P.eps);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + i * kWave;
+      if (c < P.d) {
+        P.y[r * P.d + c] = v[i];
+        P.out[r * P.d + c] = (v[i] - mean) * rstd * P.gamma[c] + P.beta[c];
+      }
+    }
+    if (lane == 0) {
+      P.stats[2 * r] = mean;
+      P.stats[2 * r + 1] = rstd;
+    }
+  }
+}
+
+struct EpiBwdParams {
+  int64_t n;
+  int d;
+  const float* dout;
+  const float* y;
+  const float* stats;
+  const float* gamma;
+  float scale;                      // dropout multiplier of kept entries (1 without dropout)
+  float* du;
+  float* partial;                   // [grid][2][d]: sums of dout*yhat and dout
+};
+
+template <int PER>
+__global__ __launch_bounds__(kBlock) void epilogue_bwd(EpiBwdParams P) {
+  __shared__ float red[kWavesPerBlock][2][kMaxPer * kWave];
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const float inv_d = 1.f / static_cast<float>(P.d);
+  float gg[PER], gb[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) gg[i] = gb[i] = 0.f;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; r < P.n; r += total) {
+    const float mean = P.stats[2 * r], rstd = P.stats[2 * r + 1];
+    float yh[PER], g[PER], yv[PER];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + i * kWave;
+      float dy = 0.f, yy = 0.f, gm = 0.f;
+      if (c < P.d) {
+        dy = P.dout[r * P.d + c];
+        yy = P.y[r * P.d + c];
+        gm = P.gamma[c];
+      }
+      yv[i] = yy;
+      yh[i] = c < P.d ? (yy - mean) * rstd : 0.f;
+      g[i] = dy * gm;
+      gg[i] = fmaf(dy, yh[i], gg[i]);
+      gb[i] += dy;
+      s1 += g[i];
+      s2 = fmaf(g[i], yh[i], s2);
+    }
+    const float m1 = wave_sum(s1) * inv_d;
+    const float m2 = wave_sum(s2) * inv_d;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = lane + i * kWave;
+      if (c < P.d) {
+        const float dyv = rstd * (g[i] - m1 - yh[i] * m2);
+        // y = relu(u * mult): dy/du = mult where y > 0, else 0
+        P.du[r * P.d + c] = yv[i] > 0.f ? dyv * P.scale : 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    red[wave][0][lane + i * kWave] = gg[i];
+    red[wave][1][lane + i * kWave] = gb[i];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 2 * P.d; idx += kBlock) {
+    const int which = idx / P.d;
+    const int c = idx - which * P.d;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) s += red[w][which][c];
+    P.partial[(static_cast<int64_t>(blockIdx.x) * 2 + which) * P.d + c] = s;
+  }
+}
+
+// out[which][c] = sum over rows r of partial[r][which][c]: one wave per output, fixed order.
+__global__ __launch_bounds__(kBlock) void column_sums(const float* partial, int rows, int d,
+                                                     float* out0, float* out1) {
+  const int o = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (o >= 2 * d) return;
+  const int which = o / d;
+  const int c = o - which * d;
+  float s = 0.f;
+  for (int r = lane_id(); r < rows; r += kWave) s += partial[(static_cast<int64_t>(r) * 2 + which) * d + c];
+  s = wave_sum(s);
+  if (lane_id() == 0) (which == 0 ? out0 : out1)[c] = s;
+}
+
+int epi_grid(int64_t n) {
+  const int64_t want = ceil_div(n, kWavesPerBlock);
+  return static_cast<int>(want < kEpiMaxBlocks ? (want < 1 ? 1 : want) : kEpiMaxBlocks);
+}
+
+}  // namespace
+}  // namespace fa
+
+using namespace fa;
+
+extern "C" int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, int64_t ld1,
+                                        const float* r2, int64_t ld2, const float* gamma,
+                                        const float* beta, float eps, uint64_t drop_seed,
+                                        float drop_p, float* out, float* y, float* stats,
+                                        hipStream_t stream) {
+  if (n < 0 || d <= 0 || d > kMaxPer * kWave || !(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
+  if (n == 0) return FA_OK;
+  if (!r1 || ld1 < d || (r2 && ld2 < d) || !gamma || !beta || !out || !y || !stats) return FA_EINVAL;
+  EpiParams P;
+  P.n = n; P.d = d; P.r1 = r1; P.ld1 = ld1; P.r2 = r2; P.ld2 = ld2; P.gamma = gamma; P.beta = beta;
+  P.eps = eps; P.drop = drop_p > 0.f; P.seed = drop_seed; P.p = drop_p;
+  P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
+  P.out = out; P.y = y; P.stats = stats;
+  const dim3 grid(epi_grid(n));
+  switch (static_cast<int>(ceil_div(d, kWave))) {
+    case 1: hipLaunchKernelGGL(epilogue_fwd<1>, grid, dim3(kBlock), 0, stream, P); break;
+    case 2: hipLaunchKernelGGL(epilogue_fwd<2>, grid, dim3(kBlock), 0, stream, P); break;
+    case 3: hipLaunchKernelGGL(epilogue_fwd<3>, grid, dim3(kBlock), 0, stream, P); break;
+    default: hipLaunchKernelGGL(epilogue_fwd<4>, grid, dim3(kBlock), 0, stream, P); break;
+  }
+  return launch_status();
+}
+
+extern "C" size_t fa_tgat_epilogue_bwd_scratch_bytes(int64_t n, int32_t d) {
+  if (n <= 0 || d <= 0) return 0;
+  return static_cast<size_t>(epi_grid(n)) * 2 * static_cast<size_t>(d) * sizeof(float);
+}
+
+extern "C" int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const float* y,
+                                        const float* stats, const float* gamma, float drop_p,
+                                        float* du, float* dgamma, float* dbeta, void* scratch,
+                                        size_t scratch_bytes, hipStream_t stream) {
+  if (n < 0 || d <= 0 || d > kMaxPer * kWave || !(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
+  if (!dgamma || !dbeta || !gamma) return FA_EINVAL;
+  if (n == 0) {
+    hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(2 * d, kWavesPerBlock))),
+                       dim3(kBlock), 0, stream, static_cast<const float*>(nullptr), 0, d, dgamma, dbeta);
+    return launch_status();
+  }
+  if (!dout || !y || !stats || !du) return FA_EINVAL;
+  if (!scratch || scratch_bytes < fa_tgat_epilogue_bwd_scratch_bytes(n, d)) return FA_ESCRATCH;
+  EpiBwdParams P;
+  P.n = n; P.d = d; P.dout = dout; P.y = y; P.stats = stats; P.gamma = gamma;
+  P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
+  P.du = du; P.partial = static_cast<float*>(scratch);
+  const int grid = epi_grid(n);
+  switch (static_cast<int>(ceil_div(d, kWave))) {
+    case 1: hipLaunchKernelGGL(epilogue_bwd<1>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+    case 2: hipLaunchKernelGGL(epilogue_bwd<2>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+    case 3: hipLaunchKernelGGL(epilogue_bwd<3>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+    default: hipLaunchKernelGGL(epilogue_bwd<4>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+  }
+  hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(2 * d, kWavesPerBlock))),
+                     dim3(kBlock), 0, stream, static_cast<const float*>(P.partial), grid, d, dgamma,
+                     dbeta);
+  return launch_status();
+}

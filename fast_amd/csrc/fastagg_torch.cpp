@@ -687,6 +687,67 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
   return out;
 }
 
+// -> [out [n, d], y [n, d], stats [n, 2]]
+std::vector<at::Tensor> tgat_epilogue_fwd(at::Tensor r1, std::optional<at::Tensor> r2,
+                                          at::Tensor gamma, at::Tensor beta, double eps,
+                                          uint64_t drop_seed, double drop_p) {
+  CHECK_CUDA(r1);
+  CHECK_DTYPE(r1, at::kFloat);
+  TORCH_CHECK(r1.dim() == 2 && r1.stride(1) == 1, "r1 must be a row-major [n, d] matrix");
+  const int64_t n = r1.size(0), d = r1.size(1);
+  const float* r2p = nullptr;
+  int64_t ld2 = d;
+  if (r2.has_value()) {
+    CHECK_CUDA((*r2));
+    CHECK_DTYPE((*r2), at::kFloat);
+    TORCH_CHECK(r2->dim() == 2 && r2->size(0) == n && r2->size(1) == d && r2->stride(1) == 1,
+                "r2 must match r1");
+    r2p = r2->data_ptr<float>();
+    ld2 = r2->stride(0);
+  }
+  CHECK_INPUT(gamma);
+  CHECK_INPUT(beta);
+  TORCH_CHECK(gamma.numel() == d && beta.numel() == d, "gamma / beta must have d entries");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(r1.device());
+  auto out = at::empty({n, d}, r1.options());
+  auto y = at::empty({n, d}, r1.options());
+  auto stats = at::empty({n, 2}, r1.options());
+  const int st = fa_tgat_epilogue_fwd_f32(n, static_cast<int32_t>(d), r1.data_ptr<float>(),
+                                          r1.stride(0), r2p, ld2, gamma.data_ptr<float>(),
+                                          beta.data_ptr<float>(), static_cast<float>(eps),
+                                          drop_seed, static_cast<float>(drop_p),
+                                          out.data_ptr<float>(), y.data_ptr<float>(),
+                                          stats.data_ptr<float>(), stream_of(r1));
+  check_status(st, "tgat_epilogue_fwd");
+  return {out, y, stats};
+}
+
+// -> [du [n, d], dgamma [d], dbeta [d]]
+std::vector<at::Tensor> tgat_epilogue_bwd(at::Tensor dout, at::Tensor y, at::Tensor stats,
+                                          at::Tensor gamma, double drop_p) {
+  CHECK_INPUT(dout);
+  CHECK_INPUT(y);
+  CHECK_INPUT(stats);
+  CHECK_INPUT(gamma);
+  TORCH_CHECK(dout.sizes() == y.sizes() && dout.dim() == 2, "dout must match y [n, d]");
+  const int64_t n = y.size(0), d = y.size(1);
+  TORCH_CHECK(stats.numel() == 2 * n && gamma.numel() == d, "stats / gamma do not match y");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(y.device());
+  auto du = at::empty({n, d}, y.options());
+  auto dgamma = at::empty({d}, y.options());
+  auto dbeta = at::empty({d}, y.options());
+  const size_t sb = fa_tgat_epilogue_bwd_scratch_bytes(n, static_cast<int32_t>(d));
+  auto scratch = at::empty({static_cast<int64_t>(sb > 0 ? sb : 1)}, y.options().dtype(at::kByte));
+  const int st = fa_tgat_epilogue_bwd_f32(n, static_cast<int32_t>(d), dout.data_ptr<float>(),
+                                          y.data_ptr<float>(), stats.data_ptr<float>(),
+                                          gamma.data_ptr<float>(), static_cast<float>(drop_p),
+                                          du.data_ptr<float>(), dgamma.data_ptr<float>(),
+                                          dbeta.data_ptr<float>(), scratch.data_ptr(), sb,
+                                          stream_of(y));
+  check_status(st, "tgat_epilogue_bwd");
+  return {du, dgamma, dbeta};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(fastAgg, m) {
@@ -759,5 +820,10 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("dst"), py::arg("scores"), py::arg("stats"));
   m.def("gather_rows", &gather_rows, "row gather tab[idx]", py::arg("tab"), py::arg("idx"),
         py::arg("n"));
+  m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2)))",
+        py::arg("r1"), py::arg("r2"), py::arg("gamma"), py::arg("beta"), py::arg("eps"),
+        py::arg("drop_seed"), py::arg("drop_p"));
+  m.def("tgat_epilogue_bwd", &tgat_epilogue_bwd, "backward of tgat_epilogue_fwd", py::arg("dout"),
+        py::arg("y"), py::arg("stats"), py::arg("gamma"), py::arg("drop_p"));
   m.attr("abi_version") = fa_abi_version();
 }

@@ -349,6 +349,26 @@ class RowLinear(torch.autograd.Function):
         return dx, dW, db
 
 
+class TgatEpilogue(torch.autograd.Function):
+    """LayerNorm(ReLU(dropout(r1 + r2))) in one kernel each way (layers.py:235-236); the
+    dropout is the counter hash of (seed, row*d + col), as fastAgg.dropout_mask."""
+
+    @staticmethod
+    def forward(ctx, r1, r2, gamma, beta, eps: float, seed: int, p: float):
+        out, y, stats = fastAgg.tgat_epilogue_fwd(r1, r2, gamma, beta, float(eps), int(seed),
+                                                  float(p))
+        ctx.save_for_backward(y, stats, gamma)
+        ctx.p = float(p)
+        ctx.has_r2 = r2 is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, stats, gamma = ctx.saved_tensors
+        du, dgamma, dbeta = fastAgg.tgat_epilogue_bwd(dout.contiguous(), y, stats, gamma, ctx.p)
+        return du, (du if ctx.has_r2 else None), dgamma, dbeta, None, None, None
+
+
 # ---------------------------------------------------------------------------------------
 # Layer
 # ---------------------------------------------------------------------------------------
@@ -394,18 +414,23 @@ class TransfomerAttentionLayer(torch.nn.Module):
         return bias
 
     def forward(self, b: Block, _layers: int = 0, _hist: int = 0) -> torch.Tensor:
-        p = self.att_dropout.p
-        if self.training and p > 0:
-            # seed of the kernels' counter-based dropout, drawn from torch's CPU generator
-            seed = int(torch.randint(0, 2**62, (1,)).item())
-            return self.attend(b, drop_seed=seed, drop_p=p)
-        return self.attend(b)
+        # Dropout seeds of the kernels' counter-based masks, drawn from torch's CPU
+        # generator, so torch.manual_seed makes a training run reproducible.
+        kw = {}
+        if self.training and self.att_dropout.p > 0:
+            kw.update(drop_seed=int(torch.randint(0, 2**62, (1,)).item()), drop_p=self.att_dropout.p)
+        if self.training and self.dropout.p > 0:
+            kw.update(out_drop_seed=int(torch.randint(0, 2**62, (1,)).item()),
+                      out_drop_p=self.dropout.p)
+        return self.attend(b, **kw)
 
     def attend(self, b: Block, drop: Optional[torch.Tensor] = None, drop_seed: int = 0,
-               drop_p: float = 0.0) -> torch.Tensor:
-        """The layer with an explicit attention dropout: ``drop`` [E, heads] multipliers
-        (0 or 1/(1-p) per entry), or, when ``drop`` is None and ``drop_p`` > 0, the kernels'
-        hashed dropout of seed ``drop_seed`` (fastAgg.dropout_mask gives its multipliers)."""
+               drop_p: float = 0.0, out_drop_seed: int = 0, out_drop_p: float = 0.0) -> torch.Tensor:
+        """The layer with explicit dropouts. Attention dropout: ``drop`` [E, heads]
+        multipliers (0 or 1/(1-p) per entry), or, when ``drop`` is None and ``drop_p`` > 0,
+        the kernels' hashed dropout of seed ``drop_seed``. Output dropout (before the ReLU):
+        the hashed dropout of seed ``out_drop_seed`` over the [N, D] entries when
+        ``out_drop_p`` > 0. fastAgg.dropout_mask gives the multipliers of either."""
         Dn, De, Dt = self.dim_node_feat, self.dim_edge_feat, self.dim_time
         H, D = self.num_head, self.dim_out
         dh = D // H
@@ -456,12 +481,13 @@ class TransfomerAttentionLayer(torch.nn.Module):
         Wo = self.w_out.weight
         xflat = xbar.view(N, H * kp)
         if Dn > 0:
-            rst = (RowLinear.apply(xflat, Wo[:, :D] @ wv_blk, None)
-                   + RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias))
+            r1 = RowLinear.apply(xflat, Wo[:, :D] @ wv_blk, None)
+            r2 = RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias)
         else:
-            rst = RowLinear.apply(xflat, Wo @ wv_blk, self.w_out.bias)
-        rst = F.relu(self.dropout(rst))
-        return self.layer_norm(rst)
+            r1 = RowLinear.apply(xflat, Wo @ wv_blk, self.w_out.bias)
+            r2 = None
+        ln = self.layer_norm
+        return TgatEpilogue.apply(r1, r2, ln.weight, ln.bias, ln.eps, out_drop_seed, out_drop_p)
 
 
 class TGATEncoder(torch.nn.Module):

@@ -265,9 +265,10 @@ def layer_params(layer) -> dict:
 
 def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src: torch.Tensor,
                dst: torch.Tensor, num_dst: int, slope: float = 0.2, att_drop=None,
-               dtype=torch.float64) -> torch.Tensor:
+               dtype=torch.float64, out_drop=None) -> torch.Tensor:
     """layers.py:98-240, TGAT branch with DGL semantics, eval-mode dropout except for an
-    optional attention multiplier ``att_drop`` [E,H] (keep/(1-p) or 0).
+    optional attention multiplier ``att_drop`` [E,H] and an optional output multiplier
+    ``out_drop`` [N,D] (keep/(1-p) or 0).
 
     h: [N+E, Dn] source-node features (row N+e feeds edge e); f: [E, De]; dt: [E];
     src/dst: int64 [E] source / destination ids.
@@ -304,6 +305,8 @@ def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src:
     agg = copy_u_sum(v_src, src, dst, N)
     rst = torch.cat([agg, cast(h[:N])], 1) if Dn else agg
     rst = torch.nn.functional.linear(rst, cast(P["w_out.weight"]), cast(P["w_out.bias"]))
+    if out_drop is not None:  # layers.py:235 self.dropout, as multipliers [N, D]
+        rst = rst * cast(out_drop)
     rst = torch.relu(rst)
     return torch.nn.functional.layer_norm(rst, (D,), cast(P["layer_norm.weight"]),
                                           cast(P["layer_norm.bias"]), P["_eps"])

@@ -18,7 +18,7 @@ def _mask(E, H, p, seed):
 
 
 def _check_layer(dev, dn, de, dt, H, D, degrees, seed=0, time_bias=False, p_drop=0.0,
-                 tol=FP32_TOL):
+                 p_out=0.0, tol=FP32_TOL):
     from fast_amd.tgat import TransfomerAttentionLayer
     from fast_amd.workloads import single_layer
 
@@ -36,13 +36,21 @@ def _check_layer(dev, dn, de, dt, H, D, degrees, seed=0, time_bias=False, p_drop
     blk.srcdata["h"].requires_grad_(True)
     E = cpu.num_edges()
     drop = _mask(E, H, p_drop, seed + 2) if p_drop > 0 else None
-    out = layer.attend(blk, None if drop is None else drop.to(dev))
+    out_seed = 1000 + seed
+    out = layer.attend(blk, None if drop is None else drop.to(dev), out_drop_seed=out_seed,
+                       out_drop_p=p_out)
     out.backward(inp.dout.to(dev))
 
     P = layer_params(layer)
     h64 = cpu.srcdata["h"].double().requires_grad_(True)
     src, dst = cpu.edges()
-    ref = tgat_layer(P, h64, cpu.edata["f"], cpu.edata["dt"], src, dst, N, att_drop=drop)
+    out_drop = None
+    if p_out > 0:
+        from oracle.ref_cpu import C
+
+        out_drop = torch.from_numpy(C.dropout_mask(N, D, out_seed, p_out))
+    ref = tgat_layer(P, h64, cpu.edata["f"], cpu.edata["dt"], src, dst, N, att_drop=drop,
+                     out_drop=out_drop)
     ref.backward(inp.dout.double())
     errs = {"out": assert_rel(out, ref, tol, "layer output")}
     for name, prm in layer.named_parameters():
@@ -63,7 +71,45 @@ def test_layer_small(dev, dims):
 
 
 def test_layer_time_bias_and_dropout(dev):
-    _check_layer(dev, 100, 172, 100, 2, 100, [10] * 50 + [0, 3, 20], time_bias=True, p_drop=0.1)
+    _check_layer(dev, 100, 172, 100, 2, 100, [10] * 50 + [0, 3, 20], time_bias=True, p_drop=0.1,
+                 p_out=0.1)
+
+
+@pytest.mark.parametrize("n,d,p,two", [(1000, 100, 0.0, True), (777, 100, 0.3, True),
+                                       (300, 256, 0.1, False), (5, 7, 0.0, True), (0, 100, 0.1, True),
+                                       (4096, 64, 0.2, False)])
+def test_epilogue_matches_torch(dev, n, d, p, two):
+    """LayerNorm(ReLU(dropout(r1 + r2))) fused kernel vs float64 torch with the same hashed
+    multipliers, forward and all gradients."""
+    import fast_amd
+    from fast_amd.tgat import TgatEpilogue
+    from oracle.ref_cpu import C
+
+    g = torch.Generator().manual_seed(n + d)
+    r1 = torch.randn(n, d, generator=g)
+    r2 = torch.randn(n, d, generator=g) if two else None
+    gamma = 1 + 0.1 * torch.randn(d, generator=g)
+    beta = 0.1 * torch.randn(d, generator=g)
+    dout = torch.randn(n, d, generator=g)
+    seed, eps = 4242, 1e-5
+    leaves = [t.to(dev).requires_grad_(True) if t is not None else None for t in (r1, r2, gamma, beta)]
+    out = TgatEpilogue.apply(leaves[0], leaves[1], leaves[2], leaves[3], eps, seed, p)
+    out.backward(dout.to(dev))
+    ref_leaves = [t.double().requires_grad_(True) if t is not None else None for t in (r1, r2, gamma, beta)]
+    u = ref_leaves[0] + (ref_leaves[1] if two else 0)
+    if p > 0:
+        u = u * torch.from_numpy(C.dropout_mask(n, d, seed, p)).double()
+    ref = torch.nn.functional.layer_norm(torch.relu(u), (d,), ref_leaves[2], ref_leaves[3], eps)
+    ref.backward(dout.double())
+    if n == 0:
+        assert out.shape == (0, d)
+        assert torch.count_nonzero(leaves[2].grad) == 0
+        return
+    assert_rel(out, ref, FP32_TOL, "epilogue out")
+    for got, want, name in zip(leaves, ref_leaves, ("r1", "r2", "gamma", "beta")):
+        if got is not None:
+            assert_rel(got.grad, want.grad, FP32_TOL, f"epilogue grad {name}")
+    assert fast_amd.fastAgg is not None
 
 
 def test_layer_c1_shape(dev):

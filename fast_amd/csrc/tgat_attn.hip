@@ -44,12 +44,12 @@ namespace {
 #ifndef FA_TGAT_BATCH
 #define FA_TGAT_BATCH 2
 #endif
-#ifndef FA_TGAT_FWD_WAVES
-#define FA_TGAT_FWD_WAVES 1
-#endif
-#ifndef FA_TGAT_BWD_WAVES
-#define FA_TGAT_BWD_WAVES 1
-#endif
+// Minimum waves per SIMD the fused kernels are compiled for (a register budget). For the
+// common shapes (up to 2 heads, Kp <= 512) the forward runs at 4 waves and the backward at 3,
+// which measured faster than the register-unconstrained builds despite a few spilled
+// values; other shapes leave the choice to the compiler.
+constexpr int fwd_min_waves(int H, int NS) { return (H <= 2 && NS <= 2) ? 4 : 1; }
+constexpr int bwd_min_waves(int H, int NS) { return (H <= 2 && NS <= 2) ? 3 : 1; }
 constexpr int kBatch = FA_TGAT_BATCH;
 constexpr int kMaxBlocks = 2048;      // grid cap of the grid-stride kernels (time-grad partial rows)
 constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every descriptor's range
@@ -151,6 +151,7 @@ struct LaneCtx {
   uint32_t toff[NS];      // element offset of the chunk in the LDS tile row (zero chunk for rows)
   bool is_node[NS], is_edge[NS];
   bool slot_node[NS], slot_time[NS];  // wave-uniform: slot k holds some node / time chunk
+  uint32_t time_off;      // LDS tile offset of this lane's time chunk (zero chunk if none)
   float w0, b0, w1, b1;   // time dims j = lane and lane + 64
 };
 
@@ -160,6 +161,7 @@ __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) 
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
     const int c = lane + k * kWave;
+    if (k == 0) L.time_off = 4u * static_cast<uint32_t>(P.ct + 1);
     L.slot_node[k] = k * kWave < P.cn;
     L.slot_time[k] = P.ct > 0 && k * kWave < P.cn + P.ce + P.ct && (k + 1) * kWave > P.cn + P.ce;
     L.noff[k] = kOob;
@@ -175,6 +177,7 @@ __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) 
       L.is_edge[k] = true;
     } else if (c < P.cn + P.ce + P.ct) {
       L.toff[k] = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
+      L.time_off = L.toff[k];
     } else if (c == P.cn + P.ce + P.ct) {
       L.toff[k] = 4u * static_cast<uint32_t>(P.ct);
     }
@@ -424,7 +427,7 @@ __device__ __forceinline__ void fwd_batch(const TgatParams& P, const LaneCtx<NS>
 }
 
 template <int H, int NS>
-__global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams P) {
+__global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatParams P) {
   extern __shared__ float lds[];
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = lane_id();
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_FWD_WAVES) void tgat_fwd(TgatParams
 template <int H, int NS>
 struct BwdState {
   float4 q[H][NS], g[H][NS], dq[H][NS];
-  float4 gw[NS], gb[NS];  // time-grad accumulators of this lane's time chunks (whole wave)
+  float4 gw, gb;  // time-grad accumulators of this lane's time chunk (at most one: ct <= 64)
   float mh[H], il[H], T[H];  // row max, 1 / softmax denominator, dxbar . xbar
 };
 
@@ -567,11 +570,11 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
         // the -sin tile is zero outside the time dims, so only time chunks contribute
         const float4 sn = *reinterpret_cast<const float4*>(ts + b * P.tvs + L.toff[k]);
         const float4 pr = make_float4(sn.x * dx.x, sn.y * dx.y, sn.z * dx.z, sn.w * dx.w);
-        S.gb[k].x += pr.x;
-        S.gb[k].y += pr.y;
-        S.gb[k].z += pr.z;
-        S.gb[k].w += pr.w;
-        fma4(S.gw[k], t, pr);
+        S.gb.x += pr.x;
+        S.gb.y += pr.y;
+        S.gb.z += pr.z;
+        S.gb.w += pr.w;
+        fma4(S.gw, t, pr);
       }
     }
     (void)lane;
@@ -579,7 +582,7 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
 }
 
 template <int H, int NS>
-__global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams P) {
+__global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatParams P) {
   extern __shared__ float lds[];
   const int wave = uniform(threadIdx.x / kWave);
   float* tc = lds + wave * (2 * kBatch * P.tvs);
@@ -590,8 +593,8 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
   setup_lane<NS>(P, L);
   init_tiles(P, tc, 2 * kBatch, kBatch);
   BwdState<H, NS> S;
-#pragma unroll
-  for (int k = 0; k < NS; ++k) { S.gw[k] = f4_zero(); S.gb[k] = f4_zero(); }
+  S.gw = f4_zero();
+  S.gb = f4_zero();
 
   const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; v < P.n_dst;
@@ -644,16 +647,14 @@ __global__ __launch_bounds__(kBlock, FA_TGAT_BWD_WAVES) void tgat_bwd(TgatParams
   }
 
   // Time-grad partials of this workgroup: waves combined in a fixed order. Every time dim
-  // is owned by exactly one (lane, slot); the other lanes hold zeros and write them to the
-  // bias or zero chunk, which the sum below does not read.
+  // is owned by exactly one lane (time chunks span at most 64 chunks); the other lanes hold
+  // zeros and write them to the zero chunk, which the sum below does not read.
   if (P.dt_dim <= 0) return;
-#pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    const uint32_t o = L.toff[k];
-    float* rw = red + (wave * 2 + 0) * P.tvs + o;
-    float* rb = red + (wave * 2 + 1) * P.tvs + o;
-    rw[0] = S.gw[k].x; rw[1] = S.gw[k].y; rw[2] = S.gw[k].z; rw[3] = S.gw[k].w;
-    rb[0] = S.gb[k].x; rb[1] = S.gb[k].y; rb[2] = S.gb[k].z; rb[3] = S.gb[k].w;
+  {
+    float* rw = red + (wave * 2 + 0) * P.tvs + L.time_off;
+    float* rb = red + (wave * 2 + 1) * P.tvs + L.time_off;
+    rw[0] = S.gw.x; rw[1] = S.gw.y; rw[2] = S.gw.z; rw[3] = S.gw.w;
+    rb[0] = S.gb.x; rb[1] = S.gb.y; rb[2] = S.gb.z; rb[3] = S.gb.w;
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < 2 * P.dt_dim; idx += kBlock) {
@@ -868,7 +869,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
     }
     return launch_status();
   }
-  if (bwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
+  if (bwd_lds_bytes(P) > kMaxLds || P.ct > kWave) return FA_EUNSUPPORTED;
   if (!xbar || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
   if (!aligned16(xbar) || !aligned16(dxbar) || !aligned16(dqt) || (xbar_rs & 3) || (dxbar_rs & 3) ||
       (dqt_rs & 3))

@@ -226,7 +226,8 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
  * gives each destination's softmax correction); dxbar: gradient of xbar. Outputs: dqt
  * (layout of qt, row stride dqt_rs); d_node [n_edges][ld_dnode] gradient of the
  * node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be NULL
- * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim). */
+ * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim).
+ * dt_dim <= 256 (FA_EUNSUPPORTED beyond). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                          int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,

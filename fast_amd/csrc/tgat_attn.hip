@@ -457,14 +457,16 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
       }
       continue;
     }
+    // Prologue: the first chunk's metadata and the q~ rows are fetched together, and the
+    // first batch's gathers are in flight before anything waits on q~.
+    int64_t c0 = e0;
+    int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+    EdgeMeta<H, false> M;
+    stage_meta<H, false>(P, c0, cnt, M);
     load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
-
-    for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
-      const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
-      EdgeMeta<H, false> M;
-      stage_meta<H, false>(P, c0, cnt, M);
-      float4 xa[kBatch][NS], xb[kBatch][NS];
-      issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    float4 xa[kBatch][NS], xb[kBatch][NS];
+    issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    for (;;) {
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
         const int nb2 = cnt - jb - kBatch;
@@ -478,6 +480,11 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
           fwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, xb, S);
         }
       }
+      c0 += kWave;
+      if (c0 >= e1) break;
+      cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      stage_meta<H, false>(P, c0, cnt, M);
+      issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     }
 
 #pragma unroll
@@ -609,26 +616,26 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
       store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
       continue;
     }
+    // Prologue: the first chunk's metadata and the per-destination rows (q~, dxbar, xbar)
+    // are fetched together; the first batch's gathers are issued before T waits on them.
+    int64_t c0 = e0;
+    int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+    EdgeMeta<H, true> M;
+    stage_meta<H, true>(P, c0, cnt, M);
     load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
     load_rows<H, NS>(P.dxbar, P.dxbar_rs, v, P.kp, S.g);
+    float4 xr[H][NS];
+    load_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, xr);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
       S.il[h] = 1.f / P.stats[(v * H + h) * 2 + 1];
     }
-    {
-      float4 xr[H][NS];
-      load_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, xr);
+    float4 xa[kBatch][NS], xb[kBatch][NS];
+    issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
 #pragma unroll
-      for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xr[h]));
-    }
-
-    for (int64_t c0 = e0; c0 < e1; c0 += kWave) {
-      const int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
-      EdgeMeta<H, true> M;
-      stage_meta<H, true>(P, c0, cnt, M);
-      float4 xa[kBatch][NS], xb[kBatch][NS];
-      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xr[h]));
+    for (;;) {
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
         const int nb2 = cnt - jb - kBatch;
@@ -642,6 +649,11 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
           bwd_batch<H, NS>(P, L, M, c0, jb + kBatch, nb, tc, ts, xb, S);
         }
       }
+      c0 += kWave;
+      if (c0 >= e1) break;
+      cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      stage_meta<H, true>(P, c0, cnt, M);
+      issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     }
     store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
   }

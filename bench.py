@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--cpu-roots", type=int, default=4000,
                     help="roots of the bounded CPU sample (same MFG shape, fewer roots)")
     ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--dropin", action="store_true",
+                    help="instead of the training step, time each drop-in fastAgg operator on the "
+                         "ragged config (one JSON line per operator)")
     ap.add_argument("--copy-probe-mb", type=int, default=256,
                     help="after the timed steps, one plain row copy of this many MiB "
                          "(fastAgg.gather_rows over rows of 1024 floats): the known-size kernel "
@@ -140,8 +143,74 @@ def cpu_baseline(roots: int, reps: int, seed: int) -> dict:
                        f"{t * 1e3:.1f} ms/step; CPU: {cpu_model()}")}
 
 
+def dropin_bench(reps: int = 20, seed: int = 0) -> None:
+    """Each drop-in operator (operators.cpp:606-625 names) on the ragged config C4: 200000
+    destinations, Zipf(1.5) degrees clipped to [1, 20], 5 % empty; 2 heads, D = 100 (dh 50).
+    Prints per operator the average call time (HIP events around the binding call, output
+    allocation and zero fill included) and its algorithmic bytes / time."""
+    import numpy as np
+    import torch
+
+    import fast_amd
+    from fast_amd.workloads import ragged_degrees
+
+    fa = fast_amd.fastAgg
+    dev = torch.device("cuda:0")
+    deg = ragged_degrees(200_000, seed)
+    N, E, H, D = deg.size, int(deg.sum()), 2, 100
+    nz = deg[deg > 0]
+    S = nz.size
+    g = torch.Generator(device=dev).manual_seed(seed)
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(nz)]).astype(np.int32)).to(dev)
+    dst = torch.from_numpy(np.repeat(np.arange(N), deg)).to(dev)
+    src = torch.arange(N, N + E, device=dev)
+    x = torch.randn(E, H, device=dev, generator=g)
+    y = fa.forward_edge_softmax(indptr, indptr, x, 512, H)[0]
+    feat = torch.randn(N + E, D, device=dev, generator=g)
+    dout = torch.randn(N, D, device=dev, generator=g)
+    V = torch.randn(E, H, D // H, device=dev, generator=g)
+    out, attn, mask = fa.forward_fused_attn(x, V, indptr, indptr, dst, src, N, H, 0.2, 0.1)
+    deg32 = torch.from_numpy(nz.astype(np.int32)).to(dev)
+    ids32 = dst.to(torch.int32)
+    cases = [
+        ("forward_edge_softmax", lambda: fa.forward_edge_softmax(indptr, indptr, x, 512, H), 8 * E * H + 4 * (S + 1)),
+        ("backward_edge_softmax", lambda: fa.backward_edge_softmax(indptr, indptr, x, y, 512, H), 12 * E * H + 4 * (S + 1)),
+        ("forward_csr_edge_softmax", lambda: fa.forward_csr_edge_softmax(indptr, indptr, x, 32, 16), 8 * E * H + 4 * (S + 1)),
+        ("backward_csr_edge_softmax", lambda: fa.backward_csr_edge_softmax(indptr, indptr, x, y, 32, 16), 12 * E * H + 4 * (S + 1)),
+        ("forward_tgat", lambda: fa.forward_tgat(dst, src, feat, N, 8, 128), 16 * E + 4 * E * D + 4 * N * D),
+        ("backward_tgat", lambda: fa.backward_tgat(dst, src, dout, N + E, 8, 128), 16 * E + 8 * E * D),
+        ("forward_tgat_shd", lambda: fa.forward_tgat_shd(indptr, indptr, dst, src, feat, N, 8, 32), 4 * (S + 1) + 16 * E + 4 * E * D + 4 * N * D),
+        ("backward_tgat_shd", lambda: fa.backward_tgat_shd(indptr, indptr, dst, src, dout, N + E, 8, 32), 4 * (S + 1) + 16 * E + 8 * E * D),
+        ("forward_fused_attn", lambda: fa.forward_fused_attn(x, V, indptr, indptr, dst, src, N, H, 0.2, 0.1), 16 * E + 4 * E * D + 16 * E * H + 4 * N * D),
+        ("backward_fused_attn", lambda: fa.backward_fused_attn(dout, V, attn, mask, indptr, indptr, dst, src, N + E, H, 0.2, 0.1), 16 * E + 8 * E * D + 16 * E * H + 4 * N * D),
+        ("exclusive_sum", lambda: fa.exclusive_sum(deg32), 8 * S + 4),
+        ("cal_deg", lambda: fa.cal_deg(ids32, N), 4 * E + 4 * N),
+        ("getBalancedPtr", lambda: fa.getBalancedPtr(indptr, 16), 8 * S),
+    ]
+    for name, fn, nbytes in cases:
+        fn()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            fn()
+        s1.record()
+        torch.cuda.synchronize()
+        us = s0.elapsed_time(s1) * 1e3 / reps
+        print(json.dumps({"op": name, "workload": f"C4 ragged: N={N}, S={S}, E={E}, H={H}, D={D}",
+                          "call_us": round(us, 2), "algorithmic_bytes": nbytes,
+                          "GB/s": round(nbytes / us / 1e3, 1),
+                          "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def main():
     args = parse()
+    if args.dropin:
+        if args.gpus != 1:
+            print("bench.py: this build runs on one GPU only", file=sys.stderr)
+            sys.exit(2)
+        dropin_bench()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
               "multi-GPU sharding is design-only (DESIGN.md)", file=sys.stderr)

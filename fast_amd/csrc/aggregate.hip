@@ -1,103 +1,213 @@
 // Sum aggregation of source rows into destination rows: COO edge scatter (run-reduced)
 // and CSR segment sum.
+//
+// Rows are read through buffer descriptors sized to the row (a row id out of range has an
+// empty descriptor and reads as zeros), as float4 chunks when every row start is 16-byte
+// aligned and the width a multiple of 4, else dword by dword. Lane l owns chunks l, l+64,
+// ... of a row (NS slots). Per-edge ids are loaded 64 at a time with one coalesced load
+// and broadcast with readlane; kBatch rows are in flight per wave.
 #include "fa_common.hpp"
 
 namespace fa {
 namespace {
 
-constexpr int kColSlots = 4;                    // columns per lane per tile
-constexpr int kColTile = kWave * kColSlots;     // 256 columns per tile
-constexpr int kRunChunk = 64;                   // consecutive edges per wave
+constexpr int kBatchRows = 8;   // rows in flight per wave
+constexpr int kMaxSlots = 4;    // float4 slots per lane: rows up to 1024 floats
 
-__device__ __forceinline__ void flush_run(float* out, int64_t ldo, int64_t n_out, int64_t row,
-                                          int col0, int dim, const float (&acc)[kColSlots]) {
-  if (row < 0 || row >= n_out) return;
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t row_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+template <bool VEC>
+__device__ __forceinline__ float4 load_chunk(rsrc_t r, uint32_t off) {
+  if (VEC) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+  }
+  const int o = static_cast<int>(off);
+  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4& x) {
+  if (VEC) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 v;
+    v[0] = __float_as_uint(x.x);
+    v[1] = __float_as_uint(x.y);
+    v[2] = __float_as_uint(x.z);
+    v[3] = __float_as_uint(x.w);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
+    return;
+  }
+  const int o = static_cast<int>(off);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
+}
+
+__device__ __forceinline__ int64_t lane_i64(int64_t v, int j) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffff), j));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), j));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+struct AggParams {
+  const int64_t* dst;
+  const int64_t* src;
+  int64_t n_edges;
+  const int32_t* indptr;
+  int64_t n_seg;
+  const float* x; int64_t ldx; int64_t n_x;
+  int dim;
+  int chunks;            // ceil(dim / 4)
+  float* out; int64_t ldo; int64_t n_out;
+};
+
+// Loads the rows of kBatchRows edges (ids broadcast from lanes j0.. of `ids`).
+template <int NS, bool VEC>
+__device__ __forceinline__ void load_batch(const AggParams& P, int64_t ids, int j0, int nb,
+                                           float4 (&r)[kBatchRows][NS]) {
   const int lane = lane_id();
 #pragma unroll
-  for (int k = 0; k < kColSlots; ++k) {
-    const int c = col0 + lane + k * kWave;
-    if (c < dim) atomicAdd(out + row * ldo + c, acc[k]);
+  for (int b = 0; b < kBatchRows; ++b) {
+    if (b < nb) {
+      const int64_t s = lane_i64(ids, j0 + b);
+      const bool ok = s >= 0 && s < P.n_x;
+      const rsrc_t rr = row_rsrc(P.x + (ok ? s : 0) * P.ldx, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        const int c = lane + k * kWave;
+        r[b][k] = c < P.chunks ? load_chunk<VEC>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
+      }
+    }
   }
 }
 
-// One wave per chunk of kRunChunk consecutive edges. Consecutive edges with the same
-// destination are summed in registers and flushed with one atomic add per column.
-__global__ __launch_bounds__(kBlock) void edge_scatter_sum(const int64_t* dst, const int64_t* src,
-                                                          int64_t n_edges, const int32_t* indptr,
-                                                          int64_t n_seg, const float* x,
-                                                          int64_t ldx, int64_t n_x, int dim,
-                                                          float* out, int64_t ldo,
-                                                          int64_t n_out) {
-  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  int64_t lo = 0, hi = n_edges;
-  if (indptr) {  // only the edges covered by the CSR segments
-    lo = indptr[0] < 0 ? 0 : indptr[0];
-    hi = indptr[n_seg] < hi ? indptr[n_seg] : hi;
+template <int NS>
+__device__ __forceinline__ void add_chunks(float4 (&acc)[NS], const float4 (&r)[NS]) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    acc[k].x += r[k].x;
+    acc[k].y += r[k].y;
+    acc[k].z += r[k].z;
+    acc[k].w += r[k].w;
   }
-  const int64_t e0 = wave * kRunChunk;
-  if (e0 >= n_edges) return;
-  int64_t e1 = e0 + kRunChunk < n_edges ? e0 + kRunChunk : n_edges;
-  const int64_t eb = e0 < lo ? lo : e0;
-  e1 = e1 > hi ? hi : e1;
+}
+
+// One wave per CSR segment (grid-stride); the segment's destination is dst of its first edge.
+template <int NS, bool VEC>
+__global__ __launch_bounds__(kBlock) void segment_sum(AggParams P) {
   const int lane = lane_id();
-  for (int col0 = 0; col0 < dim; col0 += kColTile) {
-    float acc[kColSlots] = {0.f, 0.f, 0.f, 0.f};
-    int64_t cur = -1;
-    for (int64_t e = eb; e < e1; ++e) {
-      const int64_t d = dst[e];
-      const int64_t s = src[e];
-      if (d != cur) {
-        flush_run(out, ldo, n_out, cur, col0, dim, acc);
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       s < P.n_seg; s += total) {
+    int64_t lb = P.indptr[s], le = P.indptr[s + 1];
+    lb = lb < 0 ? 0 : lb;
+    le = le > P.n_edges ? P.n_edges : le;
+    if (le <= lb) continue;
+    const int64_t d = P.dst[lb];
+    if (d < 0 || d >= P.n_out) continue;
+    float4 acc[NS];
 #pragma unroll
-        for (int k = 0; k < kColSlots; ++k) acc[k] = 0.f;
-        cur = d;
+    for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const int cnt = static_cast<int>(le - e0 < kWave ? le - e0 : kWave);
+      const int64_t ids = P.src[e0 + (lane < cnt ? lane : 0)];
+      for (int j = 0; j < cnt; j += kBatchRows) {
+        const int nb = cnt - j < kBatchRows ? cnt - j : kBatchRows;
+        float4 r[kBatchRows][NS];
+        load_batch<NS, VEC>(P, ids, j, nb, r);
+#pragma unroll
+        for (int b = 0; b < kBatchRows; ++b)
+          if (b < nb) add_chunks<NS>(acc, r[b]);
       }
-      if (s >= 0 && s < n_x) {
-        const float* row = x + s * ldx;
+    }
+    const rsrc_t orow = row_rsrc(P.out + d * P.ldo, 4u * static_cast<uint32_t>(P.dim));
 #pragma unroll
-        for (int k = 0; k < kColSlots; ++k) {
-          const int c = col0 + lane + k * kWave;
-          if (c < dim) acc[k] += row[c];
+    for (int k = 0; k < NS; ++k) {
+      const int c = lane + k * kWave;
+      if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
+    }
+  }
+}
+
+template <int NS>
+__device__ __forceinline__ void flush_run(const AggParams& P, int64_t row, const float4 (&acc)[NS],
+                                          float* stage) {
+  if (row < 0 || row >= P.n_out) return;
+  atomic_add_row<NS>(P.out + row * P.ldo, P.dim, acc, stage);
+}
+
+// One wave per 64 consecutive edges. Consecutive edges with the same destination are summed
+// in registers and flushed with one atomic add per column (issued lane-consecutively through
+// an LDS staging row), so for destination-sorted input a
+// run of at most 64 edges reaches its output row as at most two partial sums (whose sum does
+// not depend on their order).
+template <int NS, bool VEC>
+__global__ __launch_bounds__(kBlock) void edge_scatter_sum(AggParams P) {
+  __shared__ __attribute__((aligned(16))) float stage_all[kWavesPerBlock][4 * kWave * NS];
+  float* stage = stage_all[threadIdx.x / kWave];
+  const int lane = lane_id();
+  int64_t lo = 0, hi = P.n_edges;
+  if (P.indptr) {  // only the edges covered by the CSR segments
+    lo = P.indptr[0] < 0 ? 0 : P.indptr[0];
+    hi = P.indptr[P.n_seg] < hi ? P.indptr[P.n_seg] : hi;
+  }
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       w * kWave < P.n_edges; w += total) {
+    int64_t e0 = w * kWave, e1 = e0 + kWave < P.n_edges ? e0 + kWave : P.n_edges;
+    e0 = e0 < lo ? lo : e0;
+    e1 = e1 > hi ? hi : e1;
+    if (e1 <= e0) continue;
+    const int cnt = static_cast<int>(e1 - e0);
+    const int64_t my_dst = P.dst[e0 + (lane < cnt ? lane : 0)];
+    const int64_t my_src = P.src[e0 + (lane < cnt ? lane : 0)];
+    float4 acc[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
+    int64_t cur = lane_i64(my_dst, 0);
+    for (int j = 0; j < cnt; j += kBatchRows) {
+      const int nb = cnt - j < kBatchRows ? cnt - j : kBatchRows;
+      float4 r[kBatchRows][NS];
+      load_batch<NS, VEC>(P, my_src, j, nb, r);
+#pragma unroll
+      for (int b = 0; b < kBatchRows; ++b) {
+        if (b < nb) {
+          const int64_t d = lane_i64(my_dst, j + b);
+          if (d != cur) {
+            flush_run<NS>(P, cur, acc, stage);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
+            cur = d;
+          }
+          add_chunks<NS>(acc, r[b]);
         }
       }
     }
-    flush_run(out, ldo, n_out, cur, col0, dim, acc);
+    flush_run<NS>(P, cur, acc, stage);
   }
 }
 
-// One wave per CSR segment; the segment's destination is dst of its first edge.
-__global__ __launch_bounds__(kBlock) void segment_sum(const int32_t* indptr, int64_t n_seg,
-                                                     const int64_t* dst, const int64_t* src,
-                                                     int64_t n_edges, const float* x, int64_t ldx,
-                                                     int64_t n_x, int dim, float* out,
-                                                     int64_t ldo, int64_t n_out) {
-  const int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-  if (s >= n_seg) return;
-  int64_t lb = indptr[s], le = indptr[s + 1];
-  lb = lb < 0 ? 0 : lb;
-  le = le > n_edges ? n_edges : le;
-  if (le <= lb) return;
-  const int64_t d = dst[lb];
-  if (d < 0 || d >= n_out) return;
-  const int lane = lane_id();
-  for (int col0 = 0; col0 < dim; col0 += kColTile) {
-    float acc[kColSlots] = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t e = lb; e < le; ++e) {
-      const int64_t sr = src[e];
-      if (sr < 0 || sr >= n_x) continue;
-      const float* row = x + sr * ldx;
-#pragma unroll
-      for (int k = 0; k < kColSlots; ++k) {
-        const int c = col0 + lane + k * kWave;
-        if (c < dim) acc[k] += row[c];
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kColSlots; ++k) {
-      const int c = col0 + lane + k * kWave;
-      if (c < dim) out[d * ldo + c] = acc[k];
-    }
-  }
+constexpr int kAggMaxBlocks = 4096;
+
+int agg_grid(int64_t waves) {
+  const int64_t want = ceil_div(waves, kWavesPerBlock);
+  return static_cast<int>(want < kAggMaxBlocks ? (want < 1 ? 1 : want) : kAggMaxBlocks);
+}
+
+bool vec_ok(const AggParams& P) {
+  return (P.dim & 3) == 0 && (P.ldx & 3) == 0 && (P.ldo & 3) == 0 && aligned16(P.x) &&
+         aligned16(P.out);
 }
 
 }  // namespace
@@ -112,9 +222,22 @@ extern "C" int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, i
   if (n_edges < 0 || n_x < 0 || dim < 0 || n_out < 0 || n_seg < 0) return FA_EINVAL;
   if (n_edges == 0 || dim == 0 || n_out == 0) return FA_OK;
   if (!dst || !src || !out || (n_x > 0 && !x) || ldx < dim || ldo < dim) return FA_EINVAL;
-  const int64_t waves = ceil_div(n_edges, kRunChunk);
-  hipLaunchKernelGGL(edge_scatter_sum, dim3(ceil_div(waves, kWavesPerBlock)), dim3(kBlock), 0,
-                     stream, dst, src, n_edges, indptr, n_seg, x, ldx, n_x, dim, out, ldo, n_out);
+  if (dim > 4 * kWave * kMaxSlots) return FA_EUNSUPPORTED;
+  AggParams P{dst, src, n_edges, indptr, n_seg, x, ldx, n_x, dim, static_cast<int>(ceil_div(dim, 4)),
+              out, ldo, n_out};
+  const dim3 grid(agg_grid(ceil_div(n_edges, kWave)));
+  const int ns = static_cast<int>(ceil_div(P.chunks, kWave));
+  const bool vec = vec_ok(P);
+#define FA_AGG_LAUNCH(NSV)                                                                      \
+  if (vec) hipLaunchKernelGGL((edge_scatter_sum<NSV, true>), grid, dim3(kBlock), 0, stream, P); \
+  else hipLaunchKernelGGL((edge_scatter_sum<NSV, false>), grid, dim3(kBlock), 0, stream, P);
+  switch (ns) {
+    case 1: FA_AGG_LAUNCH(1) break;
+    case 2: FA_AGG_LAUNCH(2) break;
+    case 3: FA_AGG_LAUNCH(3) break;
+    default: FA_AGG_LAUNCH(4) break;
+  }
+#undef FA_AGG_LAUNCH
   return launch_status();
 }
 
@@ -126,7 +249,21 @@ extern "C" int fa_segment_sum_f32(const int32_t* indptr, int64_t n_seg, const in
   if (n_seg == 0 || dim == 0 || n_out == 0 || n_edges == 0) return FA_OK;
   if (!indptr || !dst || !src || !out || (n_x > 0 && !x) || ldx < dim || ldo < dim)
     return FA_EINVAL;
-  hipLaunchKernelGGL(segment_sum, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0, stream,
-                     indptr, n_seg, dst, src, n_edges, x, ldx, n_x, dim, out, ldo, n_out);
+  if (dim > 4 * kWave * kMaxSlots) return FA_EUNSUPPORTED;
+  AggParams P{dst, src, n_edges, indptr, n_seg, x, ldx, n_x, dim, static_cast<int>(ceil_div(dim, 4)),
+              out, ldo, n_out};
+  const dim3 grid(agg_grid(n_seg));
+  const int ns = static_cast<int>(ceil_div(P.chunks, kWave));
+  const bool vec = vec_ok(P);
+#define FA_AGG_LAUNCH(NSV)                                                                 \
+  if (vec) hipLaunchKernelGGL((segment_sum<NSV, true>), grid, dim3(kBlock), 0, stream, P); \
+  else hipLaunchKernelGGL((segment_sum<NSV, false>), grid, dim3(kBlock), 0, stream, P);
+  switch (ns) {
+    case 1: FA_AGG_LAUNCH(1) break;
+    case 2: FA_AGG_LAUNCH(2) break;
+    case 3: FA_AGG_LAUNCH(3) break;
+    default: FA_AGG_LAUNCH(4) break;
+  }
+#undef FA_AGG_LAUNCH
   return launch_status();
 }

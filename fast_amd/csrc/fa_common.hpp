@@ -76,6 +76,29 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// Orders this wave's LDS accesses across lanes (a wave-level barrier with workgroup-scope
+// release/acquire fences); enough when only this wave touches the LDS region.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Adds a row held as float4 chunks (lane l: columns 4l.. of slot k at 4(l + 64k)) into
+// out[0, dim) with atomics issued lane-consecutively (one 256-byte span per instruction),
+// transposing through this wave's LDS staging row `stage` (>= 4*64*NS floats).
+template <int NS>
+__device__ __forceinline__ void atomic_add_row(float* out, int dim, const float4 (&v)[NS],
+                                               float* stage) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    *reinterpret_cast<float4*>(stage + 4 * (lane + k * kWave)) = v[k];
+  lds_sync();
+  for (int c = lane; c < dim; c += kWave) atomicAdd(out + c, stage[c]);
+  lds_sync();
+}
+
 // Broadcast a wave-uniform integer into a scalar register.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 

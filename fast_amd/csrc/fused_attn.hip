@@ -16,9 +16,10 @@ __device__ __forceinline__ float keep_factor(const float* mask, int64_t idx, flo
   return mask[idx] > p ? static_cast<float>(1.0 / (1.0 - static_cast<double>(p))) : 0.f;
 }
 
-// One wave per segment. Lanes < heads hold the per-head max / sum; every lane then owns
-// output columns c = col0 + lane + 64k of the destination row.
-__global__ __launch_bounds__(kBlock) void fused_attn_fwd(const int32_t* indptr, int64_t n_seg,
+// Generic-head fallbacks (heads not in {1, 2, 4, 8}): one wave per segment. Lanes < heads
+// hold the per-head max / sum; every lane then owns output columns c = col0 + lane + 64k of
+// the destination row.
+__global__ __launch_bounds__(kBlock) void fused_attn_fwd_generic(const int32_t* indptr, int64_t n_seg,
                                                         const int64_t* dst, const int64_t* src,
                                                         int64_t n_edges, int64_t n_dst,
                                                         const float* score, const float* V,
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd(const int32_t* indptr, 
 // One wave per segment. Pass 1 scatters grad_V and records da[e,h] = keep*dout.V in
 // d_act (each lane h < heads writes and later re-reads only its own entries); pass 2
 // turns da into the softmax-input gradient.
-__global__ __launch_bounds__(kBlock) void fused_attn_bwd(const int32_t* indptr, int64_t n_seg,
+__global__ __launch_bounds__(kBlock) void fused_attn_bwd_generic(const int32_t* indptr, int64_t n_seg,
                                                         const int64_t* dst, const int64_t* src,
                                                         int64_t n_edges, int64_t n_dst,
                                                         int64_t n_src, const float* dout,
@@ -144,6 +145,324 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd(const int32_t* indptr, 
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Kernels for heads in {1, 2, 4, 8}: one wave per segment (grid-stride). Lane j holds
+// edge j of a 64-edge block of the segment (score, attention and dropout factors of every
+// head); V rows are read as float4 chunks (lane l owns chunks l, l+64, ...) through buffer
+// descriptors sized to the row, kRows rows in flight; the head of each chunk component is
+// (4c + i) / dh.
+// ---------------------------------------------------------------------------------
+constexpr int kRows = 8;
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t row_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+template <bool VEC>
+__device__ __forceinline__ float4 chunk_load(rsrc_t r, uint32_t off) {
+  if (VEC) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                       __uint_as_float(v[3]));
+  }
+  const int o = static_cast<int>(off);
+  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
+}
+
+__device__ __forceinline__ int64_t lane_i64(int64_t v, int j) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffff), j));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), j));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+struct FaParams {
+  const int32_t* indptr; int64_t n_seg;
+  const int64_t* dst; const int64_t* src;
+  int64_t n_edges, n_dst, n_src, n_v;
+  const float* score; const float* V; const float* mask; const float* attn_in;
+  const float* dout;
+  int dh, dim, chunks;
+  float slope, p;
+  float* attn; float* out; float* d_act; float* grad_V;
+};
+
+// Per-lane head of each component of its NS chunks (H = number of heads).
+template <int NS>
+struct ChunkHeads {
+  int h[NS][4];
+};
+
+template <int NS>
+__device__ __forceinline__ void chunk_heads(const FaParams& P, ChunkHeads<NS>& C) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = 4 * (lane + k * kWave) + i;
+      C.h[k][i] = col < P.dim ? col / P.dh : -1;
+    }
+}
+
+template <int H>
+__device__ __forceinline__ float pick(const float (&w)[H], int h) {
+  float r = 0.f;
+#pragma unroll
+  for (int q = 0; q < H; ++q) r = h == q ? w[q] : r;
+  return r;
+}
+
+// keep factor of a kept entry: 1/(1-p) in double, as fused_attention.cu:285-287
+__device__ __forceinline__ float drop_weight(float a, float m, float p) {
+  return m > p ? static_cast<float>(static_cast<double>(a) / (1.0 - static_cast<double>(p))) : 0.f;
+}
+
+template <int H, int NS, bool VEC>
+__global__ __launch_bounds__(kBlock) void fused_attn_fwd_k(FaParams P) {
+  const int lane = lane_id();
+  ChunkHeads<NS> C;
+  chunk_heads<NS>(P, C);
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       s < P.n_seg; s += total) {
+    int64_t lb = P.indptr[s], le = P.indptr[s + 1];
+    lb = lb < 0 ? 0 : lb;
+    le = le > P.n_edges ? P.n_edges : le;
+    if (le <= lb) continue;
+    // softmax statistics per head over the whole segment (edge order within lanes)
+    float mx[H], sm[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) { mx[h] = kMaxSeed; sm[h] = 0.f; }
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const bool in = e0 + lane < le;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const float l = in ? leaky(P.score[(e0 + lane) * H + h], P.slope) : kMaxSeed;
+        mx[h] = fmaxf(mx[h], wave_max(l));
+      }
+    }
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const bool in = e0 + lane < le;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const float v = in ? expf(leaky(P.score[(e0 + lane) * H + h], P.slope) - mx[h]) : 0.f;
+        sm[h] += wave_sum(v);
+      }
+    }
+    const int64_t d = P.dst[lb];
+    const bool write_out = d >= 0 && d < P.n_dst;
+    float4 acc[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const int cnt = static_cast<int>(le - e0 < kWave ? le - e0 : kWave);
+      const bool in = lane < cnt;
+      const int64_t e = e0 + (in ? lane : 0);
+      float w[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const float a = expf(leaky(P.score[e * H + h], P.slope) - mx[h]) / sm[h];
+        if (in) P.attn[e * H + h] = a;
+        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p) : a;
+      }
+      const int64_t my_src = P.src[e];
+      if (!write_out || P.dim == 0) continue;
+      for (int j = 0; j < cnt; j += kRows) {
+        const int nb = cnt - j < kRows ? cnt - j : kRows;
+        float4 r[kRows][NS];
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          if (b < nb) {
+            const int64_t row = lane_i64(my_src, j + b) - P.n_dst;
+            const bool ok = row >= 0 && row < P.n_v;
+            const rsrc_t rr = row_rsrc(P.V + (ok ? row : 0) * P.dim, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) r[b][k] = chunk_load<VEC>(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          if (b < nb) {
+            float wb[H];
+#pragma unroll
+            for (int h = 0; h < H; ++h) wb[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[h]), j + b));
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+              acc[k].x = fmaf(pick<H>(wb, C.h[k][0]), r[b][k].x, acc[k].x);
+              acc[k].y = fmaf(pick<H>(wb, C.h[k][1]), r[b][k].y, acc[k].y);
+              acc[k].z = fmaf(pick<H>(wb, C.h[k][2]), r[b][k].z, acc[k].z);
+              acc[k].w = fmaf(pick<H>(wb, C.h[k][3]), r[b][k].w, acc[k].w);
+            }
+          }
+        }
+      }
+    }
+    if (!write_out) continue;
+    float* o = P.out + d * P.dim;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int c4 = 4 * (lane + k * kWave);
+      if (c4 < P.dim) o[c4] = acc[k].x;
+      if (c4 + 1 < P.dim) o[c4 + 1] = acc[k].y;
+      if (c4 + 2 < P.dim) o[c4 + 2] = acc[k].z;
+      if (c4 + 3 < P.dim) o[c4 + 3] = acc[k].w;
+    }
+  }
+}
+
+template <int H, int NS, bool VEC>
+__global__ __launch_bounds__(kBlock) void fused_attn_bwd_k(FaParams P) {
+  __shared__ __attribute__((aligned(16))) float stage_all[kWavesPerBlock][4 * kWave * NS];
+  float* stage = stage_all[threadIdx.x / kWave];
+  const int lane = lane_id();
+  ChunkHeads<NS> C;
+  chunk_heads<NS>(P, C);
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const float keep = static_cast<float>(1.0 / (1.0 - static_cast<double>(P.p)));
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       s < P.n_seg; s += total) {
+    int64_t lb = P.indptr[s], le = P.indptr[s + 1];
+    lb = lb < 0 ? 0 : lb;
+    le = le > P.n_edges ? P.n_edges : le;
+    if (le <= lb) continue;
+    const int64_t d = P.dst[lb];
+    if (d < 0 || d >= P.n_dst) continue;
+    // dout row of the destination, chunked like the V rows
+    float4 g[NS];
+    {
+      const rsrc_t dr = row_rsrc(P.dout + d * P.dim, 4u * static_cast<uint32_t>(P.dim));
+#pragma unroll
+      for (int k = 0; k < NS; ++k) g[k] = chunk_load<VEC>(dr, 16u * static_cast<uint32_t>(lane + k * kWave));
+    }
+    float tsum[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) tsum[h] = 0.f;
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const int cnt = static_cast<int>(le - e0 < kWave ? le - e0 : kWave);
+      const bool in = lane < cnt;
+      const int64_t e = e0 + (in ? lane : 0);
+      float a[H], kf[H], da[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        a[h] = P.attn_in[e * H + h];
+        kf[h] = P.mask ? (P.mask[e * H + h] > P.p ? keep : 0.f) : 1.f;
+        da[h] = 0.f;
+      }
+      const int64_t my_src = P.src[e];
+      for (int j = 0; j < cnt; j += kRows) {
+        const int nb = cnt - j < kRows ? cnt - j : kRows;
+        float4 r[kRows][NS];
+        bool okb[kRows];
+        int64_t rowb[kRows];
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          okb[b] = false;
+          rowb[b] = 0;
+          if (b < nb) {
+            const int64_t sr = lane_i64(my_src, j + b);
+            const int64_t row = sr - P.n_dst;
+            okb[b] = row >= 0 && row < P.n_v && sr < P.n_src;
+            rowb[b] = okb[b] ? row : 0;
+            const rsrc_t rr = row_rsrc(P.V + rowb[b] * P.dim, okb[b] ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) r[b][k] = chunk_load<VEC>(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+          }
+        }
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          if (b < nb && okb[b]) {
+            float ab[H], kb[H], part[H];
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+              ab[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[h]), j + b));
+              kb[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kf[h]), j + b));
+              part[h] = 0.f;
+            }
+            float4 gvc[NS];  // this edge's grad_V row: a * keep * dout, per component head
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+              const float gx[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
+              const float vx[4] = {r[b][k].x, r[b][k].y, r[b][k].z, r[b][k].w};
+              float cx[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int hh = C.h[k][i];
+                cx[i] = pick<H>(ab, hh) * pick<H>(kb, hh) * gx[i];
+#pragma unroll
+                for (int h = 0; h < H; ++h) part[h] = hh == h ? fmaf(gx[i], vx[i], part[h]) : part[h];
+              }
+              gvc[k] = make_float4(cx[0], cx[1], cx[2], cx[3]);
+            }
+            atomic_add_row<NS>(P.grad_V + rowb[b] * P.dim, P.dim, gvc, stage);
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+              const float v = kb[h] * wave_sum(part[h]);
+              da[h] = lane == j + b ? v : da[h];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        if (in) P.d_act[e * H + h] = da[h];
+        tsum[h] += wave_sum(in ? a[h] * da[h] : 0.f);
+      }
+    }
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const int64_t e = e0 + lane;
+      if (e < le) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) P.d_act[e * H + h] = P.attn_in[e * H + h] * (P.d_act[e * H + h] - tsum[h]);
+      }
+    }
+  }
+}
+
+constexpr int kFaMaxBlocks = 4096;
+
+int fa_grid(int64_t n_seg) {
+  const int64_t want = ceil_div(n_seg, kWavesPerBlock);
+  return static_cast<int>(want < kFaMaxBlocks ? (want < 1 ? 1 : want) : kFaMaxBlocks);
+}
+
+template <int H>
+int launch_fa(const FaParams& P, bool bwd, hipStream_t stream) {
+  const int ns = static_cast<int>(ceil_div(P.chunks, kWave));
+  const bool vec = (P.dim & 3) == 0 && aligned16(P.V) && (!bwd || aligned16(P.dout));
+  const dim3 grid(fa_grid(P.n_seg));
+#define FA_FA_LAUNCH(NSV)                                                                      \
+  if (bwd) {                                                                                  \
+    if (vec) hipLaunchKernelGGL((fused_attn_bwd_k<H, NSV, true>), grid, dim3(kBlock), 0, stream, P); \
+    else hipLaunchKernelGGL((fused_attn_bwd_k<H, NSV, false>), grid, dim3(kBlock), 0, stream, P);    \
+  } else {                                                                                    \
+    if (vec) hipLaunchKernelGGL((fused_attn_fwd_k<H, NSV, true>), grid, dim3(kBlock), 0, stream, P); \
+    else hipLaunchKernelGGL((fused_attn_fwd_k<H, NSV, false>), grid, dim3(kBlock), 0, stream, P);    \
+  }
+  switch (ns) {
+    case 0:
+    case 1: FA_FA_LAUNCH(1) break;
+    case 2: FA_FA_LAUNCH(2) break;
+    default: FA_FA_LAUNCH(4) break;
+  }
+#undef FA_FA_LAUNCH
+  return launch_status();
+}
+
+int launch_fa_heads(const FaParams& P, int heads, bool bwd, hipStream_t stream) {
+  switch (heads) {
+    case 1: return launch_fa<1>(P, bwd, stream);
+    case 2: return launch_fa<2>(P, bwd, stream);
+    case 4: return launch_fa<4>(P, bwd, stream);
+    case 8: return launch_fa<8>(P, bwd, stream);
+    default: return -1000;  // no specialised kernel
+  }
+}
+
 }  // namespace
 }  // namespace fa
 
@@ -158,7 +477,14 @@ extern "C" int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const
   if (heads > kWave) return FA_EUNSUPPORTED;
   if (n_seg == 0 || heads == 0) return FA_OK;
   if (!indptr || !dst || !src || !score || !attn || (dh > 0 && (!V || !out))) return FA_EINVAL;
-  hipLaunchKernelGGL(fused_attn_fwd, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0,
+  if (static_cast<int64_t>(heads) * dh <= 4 * kWave * 4) {
+    FaParams P{indptr, n_seg, dst, src, n_edges, n_dst, 0, n_edges, score, V, mask, nullptr,
+               nullptr, dh, heads * dh, static_cast<int>(ceil_div(heads * dh, 4)), slope, p,
+               attn, out, nullptr, nullptr};
+    const int st = launch_fa_heads(P, heads, false, stream);
+    if (st != -1000) return st;
+  }
+  hipLaunchKernelGGL(fused_attn_fwd_generic, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0,
                      stream, indptr, n_seg, dst, src, n_edges, n_dst, score, V, n_edges, heads,
                      dh, slope, p, mask, attn, out);
   return launch_status();
@@ -175,7 +501,14 @@ extern "C" int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const
   if (n_seg == 0 || heads == 0) return FA_OK;
   if (!indptr || !dst || !src || !attn || !d_act || (dh > 0 && (!V || !dout || !grad_V)))
     return FA_EINVAL;
-  hipLaunchKernelGGL(fused_attn_bwd, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0,
+  if (static_cast<int64_t>(heads) * dh <= 4 * kWave * 4) {
+    FaParams P{indptr, n_seg, dst, src, n_edges, n_dst, n_src, n_edges, nullptr, V, mask, attn,
+               dout, dh, heads * dh, static_cast<int>(ceil_div(heads * dh, 4)), 0.f, p, nullptr,
+               nullptr, d_act, grad_V};
+    const int st = launch_fa_heads(P, heads, true, stream);
+    if (st != -1000) return st;
+  }
+  hipLaunchKernelGGL(fused_attn_bwd_generic, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0,
                      stream, indptr, n_seg, dst, src, n_edges, n_dst, n_src, dout, V, n_edges,
                      attn, mask, heads, dh, p, d_act, grad_V);
   return launch_status();

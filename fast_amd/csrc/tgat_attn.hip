@@ -127,13 +127,6 @@ __device__ __forceinline__ int64_t clamp_edge(int64_t e, int64_t n_edges) {
   return e < 0 ? 0 : (e > n_edges ? n_edges : e);
 }
 
-// Orders this wave's LDS accesses across lanes of the same wave.
-__device__ __forceinline__ void lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
-
 __device__ __forceinline__ int lane_int(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
 __device__ __forceinline__ float lane_flt(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));

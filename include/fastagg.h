@@ -125,6 +125,7 @@ int fa_group_softmax_bwd_f32(const int64_t* batch_ptr, int64_t n_batch, const in
  * every edge covered. Also the backward of forward_tgat / forward_tgat_shd with the
  * roles of dst and src swapped (aggregate_acc_kernel.cu:97-161,
  * aggregate_shd_kernel.cu:212-368). */
+/* (dim <= 1024 for this and fa_segment_sum_f32; FA_EUNSUPPORTED beyond.) */
 int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_edges,
                             const int32_t* indptr, int64_t n_seg, const float* x, int64_t ldx,
                             int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,

@@ -119,13 +119,13 @@ int fa_group_softmax_bwd_f32(const int64_t* batch_ptr, int64_t n_batch, const in
 /* out[dst[e], :] += x[src[e], :] for e < n_edges (COO, any order; ids outside
  * [0, n_out) / [0, n_x) are skipped). When indptr is not NULL only the edges
  * indptr[0] <= e < indptr[n_seg] are used. out must be zeroed by the caller. Runs of equal
- * consecutive dst are reduced in registers, so for dst-sorted input every output row
- * receives at most two partial sums (deterministic).
+ * consecutive dst are reduced in registers, so for dst-sorted input the output row of a
+ * run of at most 64 edges receives at most two partial sums (deterministic).
+ * dim <= 1024 (FA_EUNSUPPORTED beyond).
  * Replaces computation_aware_forward_tgat_cuda (aggregate_acc_kernel.cu:36-94), with
  * every edge covered. Also the backward of forward_tgat / forward_tgat_shd with the
  * roles of dst and src swapped (aggregate_acc_kernel.cu:97-161,
  * aggregate_shd_kernel.cu:212-368). */
-/* (dim <= 1024 for this and fa_segment_sum_f32; FA_EUNSUPPORTED beyond.) */
 int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_edges,
                             const int32_t* indptr, int64_t n_seg, const float* x, int64_t ldx,
                             int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,
@@ -133,8 +133,8 @@ int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_ed
 
 /* CSR segment sum: for segment s, out[dst[indptr[s]], :] = sum_e x[src[e], :] over the
  * segment (edges of a segment share one destination). Rows of out outside every segment
- * are not written. Replaces computation_aware_forward_tgat_shd_cuda
- * (aggregate_shd_kernel.cu:37-94, 161-209). */
+ * are not written. dim <= 1024 (FA_EUNSUPPORTED beyond). Replaces
+ * computation_aware_forward_tgat_shd_cuda (aggregate_shd_kernel.cu:37-94, 161-209). */
 int fa_segment_sum_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
                        const int64_t* src, int64_t n_edges, const float* x, int64_t ldx,
                        int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,

@@ -492,8 +492,23 @@ at::Tensor rowptr_from_dst(at::Tensor dst, int64_t n_dst) {
 void check_table(const at::Tensor& t, const char* name) {
   CHECK_CUDA(t);
   TORCH_CHECK(t.dim() == 2, name, " must be 2-D");
-  TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be float32");
+  TORCH_CHECK(t.scalar_type() == at::kFloat || t.scalar_type() == at::kBFloat16, name,
+              " must be float32 or bfloat16");
   TORCH_CHECK(t.size(1) == 0 || t.stride(1) == 1, name, " rows must be contiguous");
+}
+
+int32_t table_dtype(const at::Tensor& t) {
+  return t.scalar_type() == at::kBFloat16 ? FA_BF16 : FA_F32;
+}
+
+// Rows with a leading dimension that is a multiple of 4 may be read up to the next multiple
+// of 4 past their width (the padding values are ignored): the allocation must cover that.
+void check_row_padding(const at::Tensor& t, const char* name) {
+  const int64_t n = t.size(0), d = t.size(1), ld = d > 0 ? t.stride(0) : 0;
+  if (n == 0 || d == 0 || (ld & 3) || !(d & 3)) return;
+  const int64_t need = (t.storage_offset() + (n - 1) * ld + ((d + 3) / 4) * 4) * t.element_size();
+  TORCH_CHECK(static_cast<int64_t>(t.storage().nbytes()) >= need, name,
+              ": rows with a leading dimension divisible by 4 must be padded to a multiple of 4");
 }
 
 const int64_t* opt_index(const std::optional<at::Tensor>& idx, int64_t n, const at::Tensor& ref,
@@ -521,6 +536,8 @@ fa_tgat_graph make_graph(const at::Tensor& rowptr, const at::Tensor& node_tab,
   CHECK_DTYPE(time_b, at::kFloat);
   check_table(node_tab, "node_tab");
   check_table(edge_tab, "edge_tab");
+  check_row_padding(node_tab, "node_tab");
+  check_row_padding(edge_tab, "edge_tab");
   TORCH_CHECK(time_w.numel() == time_b.numel(), "time_w and time_b must have the same length");
   const int64_t E = dt.numel();
   for (const at::Tensor* t : {&node_tab, &edge_tab, &dt, &time_w, &time_b})
@@ -529,12 +546,14 @@ fa_tgat_graph make_graph(const at::Tensor& rowptr, const at::Tensor& node_tab,
   g.n_dst = rowptr.numel() - 1;
   g.n_edges = E;
   g.rowptr = rowptr.data_ptr<int32_t>();
-  g.node_tab = node_tab.data_ptr<float>();
+  g.node_tab = node_tab.data_ptr();
+  g.node_dtype = table_dtype(node_tab);
   g.ld_node = node_tab.size(1) > 0 ? node_tab.stride(0) : 0;
   g.n_node = node_tab.size(0);
   g.dn = static_cast<int32_t>(node_tab.size(1));
   g.node_idx = opt_index(node_idx, E, rowptr, "node_idx");
-  g.edge_tab = edge_tab.data_ptr<float>();
+  g.edge_tab = edge_tab.data_ptr();
+  g.edge_dtype = table_dtype(edge_tab);
   g.ld_edge = edge_tab.size(1) > 0 ? edge_tab.stride(0) : 0;
   g.n_edge_rows = edge_tab.size(0);
   g.de = static_cast<int32_t>(edge_tab.size(1));
@@ -679,10 +698,15 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
     ip = idx->data_ptr<int64_t>();
   }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(tab.device());
-  auto out = at::empty({n, tab.size(1)}, tab.options());
-  const int st = fa_gather_rows_f32(tab.data_ptr<float>(), tab.size(1) > 0 ? tab.stride(0) : 0,
-                                    tab.size(0), ip, n, static_cast<int32_t>(tab.size(1)),
-                                    out.data_ptr<float>(), tab.size(1), stream_of(tab));
+  auto out = at::empty({n, tab.size(1)}, tab.options().dtype(at::kFloat));
+  const int64_t ld = tab.size(1) > 0 ? tab.stride(0) : 0;
+  const int32_t dim = static_cast<int32_t>(tab.size(1));
+  const int st = tab.scalar_type() == at::kBFloat16
+                     ? fa_gather_rows_bf16_f32(reinterpret_cast<const uint16_t*>(tab.data_ptr()), ld,
+                                               tab.size(0), ip, n, dim, out.data_ptr<float>(), dim,
+                                               stream_of(tab))
+                     : fa_gather_rows_f32(tab.data_ptr<float>(), ld, tab.size(0), ip, n, dim,
+                                          out.data_ptr<float>(), dim, stream_of(tab));
   check_status(st, "gather_rows");
   return out;
 }
@@ -818,7 +842,7 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("n_edges"), py::arg("heads"), py::arg("seed"), py::arg("p"), py::arg("device"));
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
         py::arg("dst"), py::arg("scores"), py::arg("stats"));
-  m.def("gather_rows", &gather_rows, "row gather tab[idx]", py::arg("tab"), py::arg("idx"),
+  m.def("gather_rows", &gather_rows, "row gather tab[idx] (float32 or bf16 table, float32 rows)", py::arg("tab"), py::arg("idx"),
         py::arg("n"));
   m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2)))",
         py::arg("r1"), py::arg("r2"), py::arg("gamma"), py::arg("beta"), py::arg("eps"),

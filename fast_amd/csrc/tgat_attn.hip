@@ -57,9 +57,15 @@ constexpr uint32_t kOob = 0x7ffffff0u;  // buffer offset past every descriptor's
 struct TgatParams {
   int64_t n_dst, n_edges;
   const int32_t* rowptr;
-  const float* node_tab; int64_t ld_node; int64_t n_node; int dn; const int64_t* node_idx;
-  const float* edge_tab; int64_t ld_edge; int64_t n_erow; int de; const int64_t* edge_idx;
-  int node_tail, edge_tail;           // row width not a multiple of 4: per-dword access
+  const char* node_tab; int64_t ld_node; int64_t n_node; int dn; const int64_t* node_idx;
+  const char* edge_tab; int64_t ld_edge; int64_t n_erow; int de; const int64_t* edge_idx;
+  int node_bf16, edge_bf16;           // table element type: bf16 (else float32)
+  // Row access mode: 0 = chunk loads (aligned rows, width a multiple of 4); 1 = chunk loads
+  // over the padded row (aligned rows, ld a multiple of 4, width not), the components past
+  // the width zeroed; 2 = element loads (unaligned rows).
+  int node_tail, edge_tail;
+  uint32_t node_row_bytes, edge_row_bytes;  // descriptor range of a valid row
+  int dnode_dwords;                   // node-gradient rows stored dword by dword
   const float* dt; const float* time_w; const float* time_b; int dt_dim;
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
   int tvs;                            // LDS row stride of the tiles: 4*ct + bias chunk + zero chunk
@@ -101,6 +107,35 @@ __device__ __forceinline__ float4 bload4_dwords(rsrc_t r, uint32_t off) {
                      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
                      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
                      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Four bf16 values widened to float: one 8-byte load (chunk-aligned rows) ...
+__device__ __forceinline__ float4 bload4_bf16(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0);
+  return make_float4(bf16_lo(v[0]), bf16_hi(v[0]), bf16_lo(v[1]), bf16_hi(v[1]));
+}
+
+// ... or four 2-byte loads, each range-checked (row ends, unaligned rows).
+__device__ __forceinline__ float4 bload4_bf16_elems(rsrc_t r, uint32_t off) {
+  const int o = static_cast<int>(off);
+  return make_float4(bf16_lo(__builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0)),
+                     bf16_lo(__builtin_amdgcn_raw_buffer_load_b16(r, o + 2, 0, 0)),
+                     bf16_lo(__builtin_amdgcn_raw_buffer_load_b16(r, o + 4, 0, 0)),
+                     bf16_lo(__builtin_amdgcn_raw_buffer_load_b16(r, o + 6, 0, 0)));
+}
+
+// One row chunk of 4 values as float (the branches are wave-uniform).
+__device__ __forceinline__ float4 load_chunk(rsrc_t r, uint32_t off, int bf16, int mode) {
+  if (bf16) return mode == 2 ? bload4_bf16_elems(r, off) : bload4_bf16(r, off);
+  return mode == 2 ? bload4_dwords(r, off) : bload4(r, off);
+}
+
+// Keeps the first `valid` components (a chunk that crosses the end of a feature row).
+__device__ __forceinline__ float4 keep_first(const float4& v, int valid) {
+  return make_float4(v.x, valid > 1 ? v.y : 0.f, valid > 2 ? v.z : 0.f, valid > 3 ? v.w : 0.f);
 }
 
 // Four dword stores: each dword is range-checked on its own, so a chunk that crosses the end
@@ -163,10 +198,10 @@ __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) 
     L.is_node[k] = false;
     L.is_edge[k] = false;
     if (c < P.cn) {
-      L.noff[k] = 16u * static_cast<uint32_t>(c);
+      L.noff[k] = (P.node_bf16 ? 8u : 16u) * static_cast<uint32_t>(c);
       L.is_node[k] = true;
     } else if (c < P.cn + P.ce) {
-      L.eoff[k] = 16u * static_cast<uint32_t>(c - P.cn);
+      L.eoff[k] = (P.edge_bf16 ? 8u : 16u) * static_cast<uint32_t>(c - P.cn);
       L.is_edge[k] = true;
     } else if (c < P.cn + P.ce + P.ct) {
       L.toff[k] = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
@@ -256,14 +291,22 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
       const int64_t erow = meta_edge(M, jb + b);
       const bool nok = nrow >= 0 && nrow < P.n_node;
       const bool eok = erow >= 0 && erow < P.n_erow;
-      const rsrc_t nr = make_rsrc(P.node_tab + (nok ? nrow : 0) * P.ld_node,
-                                  nok ? 4u * static_cast<uint32_t>(P.dn) : 0u);
-      const rsrc_t er = make_rsrc(P.edge_tab + (eok ? erow : 0) * P.ld_edge,
-                                  eok ? 4u * static_cast<uint32_t>(P.de) : 0u);
+      const int64_t nes = P.node_bf16 ? 2 : 4, ees = P.edge_bf16 ? 2 : 4;  // element bytes
+      const rsrc_t nr = make_rsrc(P.node_tab + (nok ? nrow : 0) * P.ld_node * nes,
+                                  nok ? P.node_row_bytes : 0u);
+      const rsrc_t er = make_rsrc(P.edge_tab + (eok ? erow : 0) * P.ld_edge * ees,
+                                  eok ? P.edge_row_bytes : 0u);
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
-        if (L.is_node[k]) x[b][k] = P.node_tail ? bload4_dwords(nr, L.noff[k]) : bload4(nr, L.noff[k]);
-        else if (L.is_edge[k]) x[b][k] = P.edge_tail ? bload4_dwords(er, L.eoff[k]) : bload4(er, L.eoff[k]);
+        if (L.is_node[k]) {
+          float4 v = load_chunk(nr, L.noff[k], P.node_bf16, P.node_tail);
+          if (P.node_tail == 1) v = keep_first(v, P.dn - static_cast<int>(L.noff[k] >> (P.node_bf16 ? 1 : 2)));
+          x[b][k] = v;
+        } else if (L.is_edge[k]) {
+          float4 v = load_chunk(er, L.eoff[k], P.edge_bf16, P.edge_tail);
+          if (P.edge_tail == 1) v = keep_first(v, P.de - static_cast<int>(L.eoff[k] >> (P.edge_bf16 ? 1 : 2)));
+          x[b][k] = v;
+        }
       }
     }
   }
@@ -562,7 +605,7 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
       }
       // node-row gradient (the descriptor drops the lanes outside the node part)
       if (want_node) {
-        if (P.node_tail) bstore4_dwords(rd, L.noff[k], dx);
+        if (P.dnode_dwords) bstore4_dwords(rd, L.noff[k], dx);
         else bstore4(rd, L.noff[k], dx);
       }
       // d cos(w t + b) = -sin(w t + b) * (t dw + db); the pad dims carry dx = 0
@@ -705,14 +748,19 @@ __global__ __launch_bounds__(kBlock) void attn_weights(const int64_t* dst, int64
   att[i] = expf(scores[i] - stats[(v * heads + h) * 2]) / stats[(v * heads + h) * 2 + 1];
 }
 
-__global__ __launch_bounds__(kBlock) void gather_rows(const float* tab, int64_t ld_tab, int64_t n_tab,
+__device__ __forceinline__ float to_float(float v) { return v; }
+__device__ __forceinline__ float to_float(uint16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gather_rows(const T* tab, int64_t ld_tab, int64_t n_tab,
                                                      const int64_t* idx, int64_t n, int dim,
                                                      float* out, int64_t ld_out) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
   if (r >= n) return;
   const int64_t src = idx ? idx[r] : r;
   const bool ok = src >= 0 && src < n_tab;
-  for (int c = lane_id(); c < dim; c += kWave) out[r * ld_out + c] = ok ? tab[src * ld_tab + c] : 0.f;
+  for (int c = lane_id(); c < dim; c += kWave)
+    out[r * ld_out + c] = ok ? to_float(tab[src * ld_tab + c]) : 0.f;
 }
 
 // ---------------------------------------------------------------------------------
@@ -731,13 +779,29 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_r
   }
   P = TgatParams{};
   P.n_dst = g->n_dst; P.n_edges = g->n_edges; P.rowptr = g->rowptr;
-  P.node_tab = g->node_tab; P.ld_node = g->ld_node; P.n_node = g->dn > 0 ? g->n_node : 0;
+  if ((g->node_dtype != FA_F32 && g->node_dtype != FA_BF16) ||
+      (g->edge_dtype != FA_F32 && g->edge_dtype != FA_BF16))
+    return FA_EINVAL;
+  P.node_tab = static_cast<const char*>(g->node_tab); P.ld_node = g->ld_node;
+  P.n_node = g->dn > 0 ? g->n_node : 0;
   P.dn = g->dn; P.node_idx = g->node_idx;
-  P.edge_tab = g->edge_tab; P.ld_edge = g->ld_edge; P.n_erow = g->de > 0 ? g->n_edge_rows : 0;
+  P.edge_tab = static_cast<const char*>(g->edge_tab); P.ld_edge = g->ld_edge;
+  P.n_erow = g->de > 0 ? g->n_edge_rows : 0;
   P.de = g->de; P.edge_idx = g->edge_idx;
-  // Row chunks are read as float4 when every row start is 16-byte aligned, else dword-wise.
-  P.node_tail = g->dn > 0 && ((g->dn & 3) || (g->ld_node & 3) || !aligned16(g->node_tab));
-  P.edge_tail = g->de > 0 && ((g->de & 3) || (g->ld_edge & 3) || !aligned16(g->edge_tab));
+  //   // Row chunks are read whole when every row start is chunk-aligned (16 bytes for float32,
+  // 8 for bf16), else element by element.
+  P.node_bf16 = g->node_dtype == FA_BF16;
+  P.edge_bf16 = g->edge_dtype == FA_BF16;
+  const uintptr_t nmask = P.node_bf16 ? 7u : 15u, emask = P.edge_bf16 ? 7u : 15u;
+  const bool nal = !(g->ld_node & 3) && !(reinterpret_cast<uintptr_t>(g->node_tab) & nmask);
+  const bool eal = !(g->ld_edge & 3) && !(reinterpret_cast<uintptr_t>(g->edge_tab) & emask);
+  P.node_tail = g->dn <= 0 ? 0 : (!nal ? 2 : ((g->dn & 3) ? 1 : 0));
+  P.edge_tail = g->de <= 0 ? 0 : (!eal ? 2 : ((g->de & 3) ? 1 : 0));
+  const int64_t nes = P.node_bf16 ? 2 : 4, ees = P.edge_bf16 ? 2 : 4;
+  // mode 1 reads up to the padded width (ld rounded down to whole chunks >= dn)
+  P.node_row_bytes = static_cast<uint32_t>(nes * (P.node_tail == 1 ? round_up(g->dn, 4) : g->dn));
+  P.edge_row_bytes = static_cast<uint32_t>(ees * (P.edge_tail == 1 ? round_up(g->de, 4) : g->de));
+  P.dnode_dwords = (g->dn & 3) != 0;
   if (g->n_edges > 0 && ((g->dn > 0 && g->n_node <= 0) || (g->de > 0 && g->n_edge_rows <= 0)))
     return FA_EINVAL;
   P.dt = g->dt; P.time_w = g->time_w; P.time_b = g->time_b; P.dt_dim = g->dt_dim;
@@ -882,6 +946,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   if (xbar_rs < P.kp * heads || dxbar_rs < P.kp * heads || dqt_rs < P.kp * heads)
     return FA_EINVAL;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
+  if (d_node && P.node_bf16) return FA_EUNSUPPORTED;  // node gradients for float32 rows only
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   const int grid = bwd_grid(P.n_dst);
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
@@ -890,7 +955,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dqt = dqt; P.dqt_rs = dqt_rs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
   // 16-byte node-gradient stores need 16-byte aligned gradient rows as well
-  if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.node_tail = true;
+  if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.dnode_dwords = 1;
   P.stats = const_cast<float*>(stats); P.partial = static_cast<float*>(scratch);
   if (static_cast<int64_t>(kBatch) * heads > kWave) return FA_EUNSUPPORTED;
   switch (heads) {
@@ -923,13 +988,25 @@ extern "C" int fa_dropout_mask_f32(uint64_t seed, float p, int64_t n, float* out
   return launch_status();
 }
 
-extern "C" int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab,
-                                  const int64_t* idx, int64_t n, int32_t dim, float* out,
-                                  int64_t ld_out, hipStream_t stream) {
+template <typename T>
+int gather_rows_launch(const T* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx, int64_t n,
+                       int32_t dim, float* out, int64_t ld_out, hipStream_t stream) {
   if (n < 0 || dim < 0 || n_tab < 0) return FA_EINVAL;
   if (n == 0 || dim == 0) return FA_OK;
   if (!tab || !out || ld_tab < dim || ld_out < dim) return FA_EINVAL;
-  hipLaunchKernelGGL(gather_rows, dim3(static_cast<unsigned>(ceil_div(n, kWavesPerBlock))), dim3(kBlock), 0,
-                     stream, tab, ld_tab, n_tab, idx, n, dim, out, ld_out);
+  hipLaunchKernelGGL(gather_rows<T>, dim3(static_cast<unsigned>(ceil_div(n, kWavesPerBlock))), dim3(kBlock),
+                     0, stream, tab, ld_tab, n_tab, idx, n, dim, out, ld_out);
   return launch_status();
+}
+
+extern "C" int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab,
+                                  const int64_t* idx, int64_t n, int32_t dim, float* out,
+                                  int64_t ld_out, hipStream_t stream) {
+  return gather_rows_launch(tab, ld_tab, n_tab, idx, n, dim, out, ld_out, stream);
+}
+
+extern "C" int fa_gather_rows_bf16_f32(const uint16_t* tab, int64_t ld_tab, int64_t n_tab,
+                                       const int64_t* idx, int64_t n, int32_t dim, float* out,
+                                       int64_t ld_out, hipStream_t stream) {
+  return gather_rows_launch(tab, ld_tab, n_tab, idx, n, dim, out, ld_out, stream);
 }

@@ -180,18 +180,20 @@ def to_kspace(W: torch.Tensor, b: torch.Tensor, dn: int, de: int, dt: int) -> to
 
 
 def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, heads: int,
-                       node_idx: bool, edge_idx: bool, d_node: bool = False) -> dict:
+                       node_idx: bool, edge_idx: bool, d_node: bool = False,
+                       node_bytes: int = 4, edge_bytes: int = 4) -> dict:
     """Algorithmic HBM bytes of one launch of the fused forward / backward kernel (float32):
     every byte the kernel must read or write once, gathered rows counted once per use.
 
     per edge : node id (8, when gathered) + edge id (8, when gathered) + dt (4)
-               + node row (4*dn) + edge row (4*de) + score (4*heads, written / read)
+               + node row (node_bytes*dn) + edge row (edge_bytes*de)
+               + score (4*heads, written / read)
                [+ d_node row (4*dn) written in backward when requested]
     per dst  : forward  qt read + xbar written (2 * 4*heads*Kp) + stats written (8*heads)
                backward qt, xbar, dxbar read + dqt written (4 * 4*heads*Kp) + stats read (8*heads)
     plus the row offsets 4*(n_dst+1) and the time parameters 8*dt."""
     kp = kspace_width(dn, de, dt)
-    edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + 4 * dn + 4 * de
+    edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + node_bytes * dn + edge_bytes * de
     common = 4 * (n_dst + 1) + 8 * dt
     fwd = common + n_edges * (edge_in + 4 * heads) + n_dst * (2 * 4 * heads * kp + 8 * heads)
     bwd = (common + n_edges * (edge_in + 4 * heads + (4 * dn if d_node else 0))
@@ -273,7 +275,9 @@ class TgatAttention(torch.autograd.Function):
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
-                                    g.node_idx is not None, g.edge_idx is not None)["fwd"]
+                                    g.node_idx is not None, g.edge_idx is not None,
+                                    node_bytes=node_src.element_size(),
+                                    edge_bytes=g.edge_tab.element_size())["fwd"]
             timer.end("tgat_fwd", t0, nb)
         ctx.g = g
         ctx.slope = float(slope)
@@ -304,7 +308,8 @@ class TgatAttention(torch.autograd.Function):
             nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
                                     g.node_idx is not None, g.edge_idx is not None,
-                                    need_node)["bwd"]
+                                    need_node, node_bytes=node_src.element_size(),
+                                    edge_bytes=g.edge_tab.element_size())["bwd"]
             timer.end("tgat_bwd", t0, nb)
         d_src = None
         if need_node:

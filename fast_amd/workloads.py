@@ -84,13 +84,14 @@ def two_layer(roots: int = 4000, fanout=(10, 10), n_nodes: int = 1_000_000,
               n_edge_rows: int = 10_000_000, dn: int = 100, de: int = 172, dt_dim: int = 100,
               heads: int = 2, dim_out: int = 100, seed: int = 0, device="cpu",
               hot_frac: float = 0.0, hot_share: float = 0.0,
-              dtype=torch.float32) -> StackInputs:
+              dtype=torch.float32, row_align: int = 1) -> StackInputs:
     """Two-layer TGAT MFG in the reference sampler's shape (modules.py:48-64, sampler_core
     re-sampling every source of the layer above): the top block has N1 = 3*roots
     destinations and N1*fanout[1] edges; the bottom block's destinations are all N1 + E1
     sources of the top block, each with fanout[0] edges. Node rows come from a node table
     (n_nodes x dn) and edge rows from an edge table (n_edge_rows x de), gathered by
-    uniform random ids (``hot_share`` of them drawn from a ``hot_frac`` hot set)."""
+    uniform random ids (``hot_share`` of them drawn from a ``hot_frac`` hot set). Table
+    rows are allocated with a leading dimension rounded up to ``row_align`` elements."""
     N1 = 3 * roots
     E1 = N1 * fanout[1]
     N0 = N1 + E1
@@ -106,8 +107,12 @@ def two_layer(roots: int = 4000, fanout=(10, 10), n_nodes: int = 1_000_000,
             return torch.where(hsel, hr, r)
         return torch.randint(0, high, (n,), generator=gd, device=device)
 
-    node_table = torch.randn(n_nodes, dn, generator=gd, device=device, dtype=dtype)
-    edge_table = torch.randn(n_edge_rows, de, generator=gd, device=device, dtype=dtype)
+    def table(n, d):
+        ld = -(-d // row_align) * row_align
+        return torch.randn(n, ld, generator=gd, device=device, dtype=dtype)[:, :d]
+
+    node_table = table(n_nodes, dn)
+    edge_table = table(n_edge_rows, de)
     b0 = Block.from_fanout(N0, torch.full((N0,), fanout[0], dtype=torch.int64, device=device))
     b0.node_table = node_table
     b0.edge_table = edge_table

@@ -180,15 +180,22 @@ int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* d
  * W_v,aug. Destination v owns edges rowptr[v]..rowptr[v+1] (clamped to [0, n_edges]).
  * ------------------------------------------------------------------------------- */
 
+enum { FA_F32 = 0, FA_BF16 = 1 };  /* element type of a feature table */
+
 typedef struct fa_tgat_graph {
   int64_t n_dst;           /* destinations (including zero-degree ones) */
   int64_t n_edges;
   const int32_t* rowptr;   /* [n_dst+1] full CSR over dst-sorted edges */
-  /* node part: row of edge e = node_idx ? node_idx[e] : e; rows >= n_node read as 0 */
-  const float* node_tab; int64_t ld_node; int64_t n_node; int32_t dn; const int64_t* node_idx;
+  /* node part: row of edge e = node_idx ? node_idx[e] : e; rows >= n_node read as 0.
+   * node_dtype FA_F32 or FA_BF16 (widened to float in registers); ld in elements. When
+   * ld is a multiple of 4 and the table 16-byte (float32) / 8-byte (bf16) aligned, each row
+   * may be read up to the next multiple of 4 past dn (values ignored), so the allocation
+   * must cover that padding; otherwise rows are read element by element. Same for edges. */
+  const void* node_tab; int64_t ld_node; int64_t n_node; int32_t dn; const int64_t* node_idx;
+  int32_t node_dtype;
   /* edge part: row of edge e = edge_idx ? edge_idx[e] : e; rows >= n_edge_rows read as 0 */
-  const float* edge_tab; int64_t ld_edge; int64_t n_edge_rows; int32_t de;
-  const int64_t* edge_idx;
+  const void* edge_tab; int64_t ld_edge; int64_t n_edge_rows; int32_t de;
+  const int64_t* edge_idx; int32_t edge_dtype;
   /* time part */
   const float* dt;         /* [n_edges] */
   const float* time_w;     /* [dt_dim] */
@@ -228,7 +235,7 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
  * (layout of qt, row stride dqt_rs); d_node [n_edges][ld_dnode] gradient of the
  * node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be NULL
  * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim).
- * dt_dim <= 256 (FA_EUNSUPPORTED beyond). */
+ * dt_dim <= 256, and d_node only with a float32 node table (FA_EUNSUPPORTED otherwise). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                          int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,
@@ -265,6 +272,10 @@ int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const floa
 /* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
 int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,
                        int64_t n, int32_t dim, float* out, int64_t ld_out, hipStream_t stream);
+/* The same from a bf16 table (raw 16-bit words), widened to float. */
+int fa_gather_rows_bf16_f32(const uint16_t* tab, int64_t ld_tab, int64_t n_tab,
+                            const int64_t* idx, int64_t n, int32_t dim, float* out,
+                            int64_t ld_out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

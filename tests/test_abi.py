@@ -61,7 +61,7 @@ def test_status_strings_and_version(lib):
         assert lib.fa_status_string(st)
     assert lib.fa_status_string(FA_OK) == b"success"
     assert lib.fa_status_string(-99) == b"unknown status"
-    assert lib.fa_abi_version() // 100 == 1
+    assert lib.fa_abi_version() // 100 == 2
 
 
 def test_kspace_width(lib):
@@ -92,9 +92,10 @@ class TgatGraph(ctypes.Structure):
                 ("rowptr", ctypes.c_void_p),
                 ("node_tab", ctypes.c_void_p), ("ld_node", ctypes.c_int64),
                 ("n_node", ctypes.c_int64), ("dn", ctypes.c_int32), ("node_idx", ctypes.c_void_p),
+                ("node_dtype", ctypes.c_int32),
                 ("edge_tab", ctypes.c_void_p), ("ld_edge", ctypes.c_int64),
                 ("n_edge_rows", ctypes.c_int64), ("de", ctypes.c_int32),
-                ("edge_idx", ctypes.c_void_p),
+                ("edge_idx", ctypes.c_void_p), ("edge_dtype", ctypes.c_int32),
                 ("dt", ctypes.c_void_p), ("time_w", ctypes.c_void_p), ("time_b", ctypes.c_void_p),
                 ("dt_dim", ctypes.c_int32)]
 

@@ -154,6 +154,72 @@ def test_gathered_tables_match_dense(dev):
     assert torch.equal(oa, ob)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["exact", "padded", "unaligned"])
+def test_table_access_modes(dev, dtype, layout):
+    """Rows gathered from float32 / bf16 tables whose rows are chunk-aligned, padded to a
+    multiple of 4 or unaligned give exactly the layer computed on the same values given as
+    dense float32 features (bf16 widened)."""
+    from fast_amd.tgat import Block, TransfomerAttentionLayer
+
+    dn, de = (12, 8) if layout == "exact" else (13, 6)
+    ldn, lde = {"exact": (dn, de), "padded": (16, 8), "unaligned": (dn, 7)}[layout]
+    torch.manual_seed(0)
+    layer = TransfomerAttentionLayer(dn, de, 9, 2, 0.0, 0.0, 16).to(dev)
+    g = torch.Generator().manual_seed(5)
+    ntab = torch.randn(400, ldn, generator=g).to(dtype)[:, :dn]
+    etab = torch.randn(900, lde, generator=g).to(dtype)[:, :de]
+    N, fan = 120, 10
+    blk = Block.from_fanout(N, torch.full((N,), fan, dtype=torch.int64))
+    E = blk.num_edges()
+    nid = torch.randint(0, 400, (N + E,), generator=g)
+    eid = torch.randint(0, 900, (E,), generator=g)
+    dt = torch.empty(E).exponential_(1e-4, generator=g)
+    a = blk.to(dev)
+    a.node_table, a.edge_table = ntab.to(dev), etab.to(dev)
+    a.srcdata["ID"], a.edata["ID"], a.edata["dt"] = nid.to(dev), eid.to(dev), dt.to(dev)
+    b = blk.to(dev)
+    b.srcdata["h"] = ntab.float()[nid].contiguous().to(dev)
+    b.edata["f"] = etab.float()[eid].contiguous().to(dev)
+    b.edata["dt"] = dt.to(dev)
+    with torch.no_grad():
+        oa, ob = layer(a), layer(b)
+    assert torch.equal(oa, ob)
+
+
+def test_two_layer_c5_dims_bf16(dev):
+    """Config 5 shapes (node 413, edge 186, time 100, 8 heads, hidden 256) with bf16
+    tables (rows padded to 416 / 188) and skewed ids, forward and backward, against the
+    float64 restatement evaluated on the same bf16 values."""
+    from fast_amd.tgat import TGATEncoder
+    from fast_amd.workloads import two_layer
+
+    torch.manual_seed(0)
+    enc = TGATEncoder(413, 186, 100, 8, 256, num_layers=2, dropout=0.0, att_dropout=0.0).to(dev)
+    inp = two_layer(roots=6, n_nodes=3000, n_edge_rows=20000, dn=413, de=186, heads=8,
+                    dim_out=256, seed=2, device="cpu", hot_frac=0.05, hot_share=0.8,
+                    dtype=torch.bfloat16, row_align=4)
+    blocks = [b.to(dev) for b in inp.blocks]
+    out = enc(blocks)
+    out.backward(inp.dout.to(dev))
+
+    b0, b1 = inp.blocks
+    P0 = layer_params(enc.layers["l0h0"])
+    P1 = layer_params(enc.layers["l1h0"])
+    h0 = b0.node_table.double()[b0.srcdata["ID"]]
+    f0 = b0.edge_table.double()[b0.edata["ID"]]
+    s0, d0 = b0.edges()
+    r0 = tgat_layer(P0, h0, f0, b0.edata["dt"], s0, d0, b0.num_dst_nodes())
+    f1 = b1.edge_table.double()[b1.edata["ID"]]
+    s1, d1 = b1.edges()
+    r1 = tgat_layer(P1, r0, f1, b1.edata["dt"], s1, d1, b1.num_dst_nodes())
+    r1.backward(inp.dout.double())
+    assert_rel(out, r1, FP32_TOL, "C5 2-layer output")
+    for lname, P in (("l0h0", P0), ("l1h0", P1)):
+        for name, prm in enc.layers[lname].named_parameters():
+            assert_rel(prm.grad, P[name].grad, FP32_TOL, f"grad {lname}.{name}")
+
+
 def test_two_layer_stack(dev):
     """2-layer TGAT (modules.py:48-64) on gathered tables vs the float64 restatement."""
     from fast_amd.tgat import TGATEncoder

@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "fastagg.h"
 
 namespace fa {
@@ -184,6 +188,15 @@ __host__ __device__ inline float drop_mult(uint64_t seed, uint64_t i, float p, f
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+namespace {
+// Zero fill by a kernel rather than hipMemsetAsync, so the call is safe under graph capture.
+__global__ __launch_bounds__(kBlock) void fill_zero(float* p, int64_t n) {
+  for (int64_t i = threadIdx.x + static_cast<int64_t>(blockIdx.x) * kBlock; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kBlock)
+    p[i] = 0.f;
+}
+}  // namespace
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? FA_OK : static_cast<int>(e);
@@ -191,5 +204,30 @@ inline int launch_status() {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// Workgroups of `kernel` (`block` threads, `lds` bytes of dynamic LDS) that the current
+// device holds at once: a grid-stride (persistent) launch of exactly this many runs in
+// one round, with no partly filled last round. Cached per (kernel, device, lds).
+inline int resident_blocks(const void* kernel, size_t lds, int block = kBlock) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, size_t>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(kernel, dev, lds);
+  const auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 1;
+  (void)hipGetLastError();
+  const int n = per_cu * cus;
+  cache.emplace(key, n);
+  return n;
+}
 
 }  // namespace fa

@@ -566,15 +566,26 @@ fa_tgat_graph make_graph(const at::Tensor& rowptr, const at::Tensor& node_tab,
   return g;
 }
 
-void check_kspace(const at::Tensor& t, const fa_tgat_graph& g, int64_t heads, const char* name) {
-  CHECK_INPUT(t);
-  CHECK_DTYPE(t, at::kFloat);
-  const int64_t kp = fa_tgat_kspace(g.dn, g.de, g.dt_dim);
-  TORCH_CHECK(t.dim() == 3 && t.size(0) == g.n_dst && t.size(1) == heads && t.size(2) == kp, name,
-              " must be [n_dst, heads, ", kp, "]");
+// A [groups, n, c] block whose rows start on 128-byte boundaries (row stride rounded up to
+// 32 floats): rows then never share a cache line, so rows written by different waves do
+// not leave partly written lines behind. Returned as the [groups, n, c] view.
+at::Tensor new_block(int64_t groups, int64_t n, int64_t c, const at::TensorOptions& opt) {
+  const int64_t ld = (c + 31) / 32 * 32;
+  return at::empty({groups, n, ld}, opt).narrow(2, 0, c);
 }
 
-// -> [xbar [N, H, Kp], scores [E, H], stats [N, H, 2]]
+// A per-destination block given as a [heads, n_dst, Kp] tensor of any strides with unit
+// stride along Kp (head-major when contiguous; a permuted [n_dst, heads, Kp] works too).
+void check_kspace(const at::Tensor& t, const fa_tgat_graph& g, int64_t heads, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  CHECK_DTYPE(t, at::kFloat);
+  const int64_t kp = fa_tgat_kspace(g.dn, g.de, g.dt_dim);
+  TORCH_CHECK(t.dim() == 3 && t.size(0) == heads && t.size(1) == g.n_dst && t.size(2) == kp, name,
+              " must be [heads, n_dst, ", kp, "]");
+  TORCH_CHECK(t.stride(2) == 1 || kp <= 1, name, " must have unit stride along Kp");
+}
+
+// qt [H, N, Kp] -> [xbar [H, N, Kp], scores [E, H], stats [N, H, 2]]
 std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> node_idx, at::Tensor edge_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
@@ -582,8 +593,8 @@ std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
                                       double slope, std::optional<at::Tensor> drop,
                                       uint64_t drop_seed, double drop_p) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
-  TORCH_CHECK(qt.dim() == 3, "qt must be [n_dst, heads, Kp]");
-  const int64_t H = qt.size(1);
+  TORCH_CHECK(qt.dim() == 3, "qt must be [heads, n_dst, Kp]");
+  const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
   const float* dptr = nullptr;
   if (drop.has_value()) {
@@ -594,13 +605,13 @@ std::vector<at::Tensor> tgat_attn_fwd(at::Tensor rowptr, at::Tensor node_tab,
     dptr = drop->data_ptr<float>();
   }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(qt.device());
-  auto xbar = at::empty_like(qt);
+  auto xbar = new_block(H, g.n_dst, qt.size(2), qt.options());
   auto scores = at::empty({g.n_edges, H}, qt.options());
   auto stats = at::empty({g.n_dst, H, 2}, qt.options());
   const int st = fa_tgat_attn_fwd_f32(&g, static_cast<int32_t>(H), qt.data_ptr<float>(),
-                                      qt.stride(0), static_cast<float>(slope), dptr, drop_seed,
-                                      static_cast<float>(drop_p), xbar.data_ptr<float>(),
-                                      xbar.stride(0),
+                                      qt.stride(1), qt.stride(0), static_cast<float>(slope), dptr,
+                                      drop_seed, static_cast<float>(drop_p),
+                                      xbar.data_ptr<float>(), xbar.stride(1), xbar.stride(0),
                                       scores.data_ptr<float>(), stats.data_ptr<float>(),
                                       stream_of(qt));
   check_status(st, "tgat_attn_fwd");
@@ -617,8 +628,8 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
                                       bool need_d_node) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
-  TORCH_CHECK(qt.dim() == 3, "qt must be [n_dst, heads, Kp]");
-  const int64_t H = qt.size(1);
+  TORCH_CHECK(qt.dim() == 3, "qt must be [heads, n_dst, Kp]");
+  const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
   check_kspace(xbar, g, H, "xbar");
   check_kspace(dxbar, g, H, "dxbar");
@@ -634,7 +645,7 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
     dptr = drop->data_ptr<float>();
   }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(qt.device());
-  auto dqt = at::empty_like(qt);
+  auto dqt = new_block(H, g.n_dst, qt.size(2), qt.options());
   at::Tensor d_node;
   if (need_d_node) d_node = at::empty({g.n_edges, g.dn}, qt.options());
   auto d_tw = at::empty({g.dt_dim}, qt.options());
@@ -642,11 +653,11 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
   const size_t sb = fa_tgat_attn_bwd_scratch_bytes(g.n_dst, g.dt_dim);
   auto scratch = at::empty({static_cast<int64_t>(sb)}, qt.options().dtype(at::kByte));
   const int st = fa_tgat_attn_bwd_f32(
-      &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(0), static_cast<float>(slope),
-      dptr, drop_seed, static_cast<float>(drop_p), xbar.data_ptr<float>(), xbar.stride(0),
-      scores.data_ptr<float>(),
-      stats.data_ptr<float>(), dxbar.data_ptr<float>(),
-      dxbar.stride(0), dqt.data_ptr<float>(), dqt.stride(0),
+      &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(1), qt.stride(0),
+      static_cast<float>(slope), dptr, drop_seed, static_cast<float>(drop_p),
+      xbar.data_ptr<float>(), xbar.stride(1), xbar.stride(0), scores.data_ptr<float>(),
+      stats.data_ptr<float>(), dxbar.data_ptr<float>(), dxbar.stride(1), dxbar.stride(0),
+      dqt.data_ptr<float>(), dqt.stride(1), dqt.stride(0),
       need_d_node && g.n_edges > 0 && g.dn > 0 ? d_node.data_ptr<float>() : nullptr,
       need_d_node ? g.dn : 0, d_tw.data_ptr<float>(), d_tb.data_ptr<float>(), scratch.data_ptr(),
       sb, stream_of(qt));
@@ -772,6 +783,95 @@ std::vector<at::Tensor> tgat_epilogue_bwd(at::Tensor dout, at::Tensor y, at::Ten
   return {du, dgamma, dbeta};
 }
 
+// ----- per-head projections --------------------------------------------------------
+
+// x: [n, groups*j] with unit column stride; w: [groups, j, c] contiguous; y: [groups, n, c]
+// with unit stride along c.
+void check_rowmat(const at::Tensor& t, const char* name) {
+  CHECK_CUDA(t);
+  CHECK_DTYPE(t, at::kFloat);
+  TORCH_CHECK(t.dim() == 2 && (t.stride(1) == 1 || t.size(1) <= 1), name,
+              " must be a [n, d] matrix with unit column stride");
+}
+
+void check_block(const at::Tensor& t, const char* name) {
+  CHECK_CUDA(t);
+  CHECK_DTYPE(t, at::kFloat);
+  TORCH_CHECK(t.dim() == 3 && (t.stride(2) == 1 || t.size(2) <= 1), name,
+              " must be a [groups, n, c] block with unit stride along c");
+}
+
+// y[g] = x[:, g*J:(g+1)*J] @ w[g] (+ bias[g])  -> [groups, n, c]
+at::Tensor head_proj(at::Tensor x, at::Tensor w, std::optional<at::Tensor> bias) {
+  check_rowmat(x, "x");
+  CHECK_INPUT(w);
+  CHECK_DTYPE(w, at::kFloat);
+  TORCH_CHECK(w.dim() == 3, "w must be [groups, j, c]");
+  const int64_t G = w.size(0), J = w.size(1), C = w.size(2), n = x.size(0);
+  TORCH_CHECK(x.size(1) == G * J, "x must have groups*j columns");
+  const float* bp = nullptr;
+  if (bias.has_value()) {
+    CHECK_INPUT((*bias));
+    CHECK_DTYPE((*bias), at::kFloat);
+    TORCH_CHECK(bias->numel() == G * C, "bias must be [groups, c]");
+    bp = bias->data_ptr<float>();
+  }
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+  auto y = new_block(G, n, C, x.options());
+  if (n == 0 || G == 0 || C == 0) return y;
+  TORCH_CHECK(J > 0, "head_proj: j must be positive");
+  const int st = fa_head_proj_f32(n, static_cast<int32_t>(J), static_cast<int32_t>(C),
+                                  static_cast<int32_t>(G), x.data_ptr<float>(), x.stride(0), J,
+                                  w.data_ptr<float>(), J * C, C, bp, C, y.data_ptr<float>(),
+                                  y.stride(0), y.stride(1), stream_of(x));
+  check_status(st, "head_proj");
+  return y;
+}
+
+// z[:, g*J:(g+1)*J] = y[g] @ w[g]^T  -> [n, groups*j]
+at::Tensor head_reduce(at::Tensor y, at::Tensor w) {
+  check_block(y, "y");
+  CHECK_INPUT(w);
+  CHECK_DTYPE(w, at::kFloat);
+  TORCH_CHECK(w.dim() == 3 && w.size(0) == y.size(0) && w.size(2) == y.size(2),
+              "w must be [groups, j, c] matching y");
+  const int64_t G = w.size(0), J = w.size(1), C = w.size(2), n = y.size(1);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(y.device());
+  auto z = at::empty({n, G * J}, y.options());
+  if (n == 0 || G == 0 || J == 0) return z;
+  if (C == 0) return z.zero_();
+  const int st = fa_head_reduce_f32(n, static_cast<int32_t>(J), static_cast<int32_t>(C),
+                                    static_cast<int32_t>(G), y.data_ptr<float>(), y.stride(0),
+                                    y.stride(1), w.data_ptr<float>(), J * C, C,
+                                    z.data_ptr<float>(), G * J, J, stream_of(y));
+  check_status(st, "head_reduce");
+  return z;
+}
+
+// dw[g] = x[:, g*J:(g+1)*J]^T @ y[g] (row J: column sums of y[g] when ones) -> [groups, j+ones, c]
+at::Tensor head_wgrad(at::Tensor x, at::Tensor y, int64_t groups, bool ones) {
+  check_rowmat(x, "x");
+  check_block(y, "y");
+  const int64_t G = groups, n = x.size(0), C = y.size(2);
+  TORCH_CHECK(G > 0 && y.size(0) == G && y.size(1) == n && x.size(1) % G == 0,
+              "head_wgrad: x [n, groups*j] and y [groups, n, c] do not match");
+  const int64_t J = x.size(1) / G;
+  TORCH_CHECK(J > 0 && C > 0, "head_wgrad: empty j or c");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(y.device());
+  auto dw = at::empty({G, J + (ones ? 1 : 0), C}, y.options());
+  const size_t sb = fa_head_wgrad_scratch_bytes(n, static_cast<int32_t>(J),
+                                                static_cast<int32_t>(C),
+                                                static_cast<int32_t>(G), ones ? 1 : 0);
+  auto scratch = at::empty({static_cast<int64_t>(sb > 0 ? sb : 1)}, y.options().dtype(at::kByte));
+  const int st = fa_head_wgrad_f32(n, static_cast<int32_t>(J), static_cast<int32_t>(C),
+                                   static_cast<int32_t>(G), n > 0 ? x.data_ptr<float>() : nullptr,
+                                   x.stride(0), J, n > 0 ? y.data_ptr<float>() : nullptr,
+                                   y.stride(0), y.stride(1), ones ? 1 : 0, dw.data_ptr<float>(),
+                                   scratch.data_ptr(), sb, stream_of(y));
+  check_status(st, "head_wgrad");
+  return dw;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(fastAgg, m) {
@@ -844,6 +944,12 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("dst"), py::arg("scores"), py::arg("stats"));
   m.def("gather_rows", &gather_rows, "row gather tab[idx] (float32 or bf16 table, float32 rows)", py::arg("tab"), py::arg("idx"),
         py::arg("n"));
+  m.def("head_proj", &head_proj, "per-head projection y[g] = x[:, g-block] @ w[g] (+ bias[g])",
+        py::arg("x"), py::arg("w"), py::arg("bias") = py::none());
+  m.def("head_reduce", &head_reduce, "per-head transpose product z[:, g-block] = y[g] @ w[g]^T",
+        py::arg("y"), py::arg("w"));
+  m.def("head_wgrad", &head_wgrad, "per-head weight gradient x[:, g-block]^T @ y[g]",
+        py::arg("x"), py::arg("y"), py::arg("groups"), py::arg("ones") = false);
   m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2)))",
         py::arg("r1"), py::arg("r2"), py::arg("gamma"), py::arg("beta"), py::arg("eps"),
         py::arg("drop_seed"), py::arg("drop_p"));

@@ -1,0 +1,668 @@
+// Per-head projections between the K-space blocks [G][N][C] of the fused kernels and the
+// head-blocked feature rows [N][G*J] of the layer (G heads, J = dim_out/heads <= 64,
+// C = Kp). The layer needs three products per weight W[g] ([J][C] per head):
+//   proj   Y[g][n][:] = X[n][g*J : g*J+J] W[g]  (+ bias[g])     (q~ = Q W_k, dxbar = dagg W_v)
+//   reduce Z[n][g*J : g*J+J] = Y[g][n][:] W[g]^T                (agg = xbar W_v^T, dQ = dq~ W_k^T)
+//   wgrad  dW[g] = sum_n X[n][g-block]^T Y[g][n][:]  (+ sum_n Y[g][n][:] as row J)
+// They are tall and skinny (N ~ 1e5 rows, J ~ 32..64, C ~ 400..700): their cost is the
+// stream over the [G][N][C] block, and each runs on the fp32 matrix cores,
+//   MFMA 16x16x4 f32, lane l: A[l%16][l/16], B[l/16][l%16], D[4*(l/16)+r][l%16], r < 4,
+// with every global access of the block a 16-byte-per-lane load or store (the texture
+// unit takes one lane per clock whatever the width, so narrower accesses to the block
+// would cap the bandwidth). The small operands are staged in LDS: the X rows of a tile,
+// read with coalesced loads by the whole workgroup, and (reduce) the whole of W[g].
+// Because a product does not depend on the order of the contraction, the k-slot of a
+// lane may stand for any index as long as A and B agree; reduce uses that to read four
+// consecutive columns of a row with one 16-byte load, and wgrad to give each lane four
+// consecutive columns (tile t takes columns 4m + t).
+#include "fa_common.hpp"
+
+namespace fa {
+namespace {
+
+using f4 = __attribute__((ext_vector_type(4))) float;
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (unformatted) 32-bit buffer
+constexpr uint32_t kOob = 0x7ffffff0u;  // offset past every range used here (< 2 GiB)
+
+// Buffer descriptor over [base, base + bytes): loads past the range return 0 and stores
+// past it are dropped, which covers the ragged last tile without branches.
+__device__ __forceinline__ rsrc_t rsrc(const void* base, int64_t bytes) {
+  const int64_t b = bytes < 0 ? 0 : (bytes > 0xffffffffLL ? 0xffffffffLL : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(static_cast<uint32_t>(b)), kRsrcWord3);
+}
+__device__ __forceinline__ float ld1(rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0));
+}
+__device__ __forceinline__ void st1(rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ f4 ld4(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+  return f4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+            __uint_as_float(v[3])};
+}
+__device__ __forceinline__ void st4(rsrc_t r, uint32_t off, f4 v) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  u4 u;
+  u[0] = __float_as_uint(v[0]);
+  u[1] = __float_as_uint(v[1]);
+  u[2] = __float_as_uint(v[2]);
+  u[3] = __float_as_uint(v[3]);
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, static_cast<int>(off), 0, 0);
+}
+
+__device__ __forceinline__ f4 mfma4(float a, float b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Keeps the instruction scheduler from moving anything across this point: a prefetch
+// issued before it stays ahead of the work after it (the scheduler would otherwise sink
+// the loads next to their first use, and the wait for them would expose their latency).
+__device__ __forceinline__ void pin() { __builtin_amdgcn_sched_barrier(0); }
+
+// Descriptor over rows [n0, n0+16) of a row-major array (row stride ld, width w): empty
+// past the last row, so a prefetch beyond the end reads zeros.
+__device__ __forceinline__ rsrc_t tile_rsrc(const float* base, int64_t n, int64_t n0, int64_t ld,
+                                            int64_t w) {
+  const int64_t rows = n - n0 < 16 ? n - n0 : 16;
+  return rsrc(base + n0 * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
+}
+
+// ----- proj ------------------------------------------------------------------------------
+struct ProjParams {
+  int64_t n; int j, c, g;
+  const float* x; int64_t ldx; int64_t xg;   // X row n, group g: x + n*ldx + g*xg
+  const float* w; int64_t wg; int64_t ldw;   // W[g][j][c] = w[g*wg + j*ldw + c]
+  const float* bias; int64_t bg;             // bias[g][c] = bias[g*bg + c] (may be null)
+  float* y; int64_t yg; int64_t ldy;         // Y[g][n][c] = y[g*yg + n*ldy + c]
+  int ncg4;                                  // workgroups per group along the columns
+  int vec;                                   // Y rows 16-byte aligned and c % 4 == 0
+};
+
+constexpr int kProjCt = 6;   // 16-column tiles per wave (96 columns)
+#ifndef FA_PROJ_RT
+#define FA_PROJ_RT 2
+#endif
+constexpr int kProjRt = FA_PROJ_RT;  // 16-row tiles per workgroup step (one LDS sync each)
+
+// Workgroup: one head g, four 96-column groups (one per wave), 16-row tiles grid-stride.
+// The product is formed transposed, Y^T tile = W^T (A: registers for the whole kernel,
+// KS = ceil(J/4) k-steps x CT tiles, zero past J and C) times X^T (B: from the tile's X
+// rows in LDS), so that each lane ends up with four consecutive columns of one row and
+// stores them as one float4. The workgroup loads the next tile's X rows (coalesced, one
+// element per thread and load) while the current tile is multiplied and stored.
+template <int KS, int CT, bool BIAS, bool VEC>
+__global__ __launch_bounds__(kBlock) void head_proj(ProjParams P) {
+  constexpr int RT = kProjRt;                          // 16-row tiles per step
+  constexpr int XW = 4 * KS + 1;                       // odd LDS row: rows in distinct banks
+  constexpr int XL = (RT * 16 * 4 * KS + kBlock - 1) / kBlock;
+  __shared__ float xs[2][RT * 16][XW];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int g = blockIdx.y / P.ncg4;
+  const int c0 = ((blockIdx.y - g * P.ncg4) * kWavesPerBlock + wave) * (16 * CT);
+  const bool active = c0 < P.c;                         // idle waves still load X
+  const int li = lane & 15, lk = lane >> 4;
+  const float* w = P.w + g * P.wg;
+  float wf[KS][CT];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+      const int jj = 4 * s + lk, cc = c0 + 16 * t + li;
+      wf[s][t] = (active && jj < P.j && cc < P.c) ? w[jj * P.ldw + cc] : 0.f;
+    }
+  }
+  // output of tile t: columns cb .. cb+3 (cb = c0 + 16t + 4lk) of row n0 + li
+  f4 bias4[BIAS ? CT : 1];
+  uint32_t yo[CT];
+#pragma unroll
+  for (int t = 0; t < CT; ++t) {
+    const int cb = c0 + 16 * t + 4 * lk;
+    if (BIAS) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bias4[t][r] = cb + r < P.c ? P.bias[g * P.bg + cb + r] : 0.f;
+    }
+    yo[t] = cb < P.c ? 4u * static_cast<uint32_t>(li * P.ldy + cb) : kOob;
+  }
+  // X elements of this thread: e = tid + kBlock*i of the RT*16 x J step block
+  uint32_t xo[XL];
+  int xl[XL];                                           // LDS slot (row*XW + col), -1: none
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int e = tid + kBlock * i;
+    const int r = e / P.j, cc = e - r * P.j;
+    const bool ok = e < RT * 16 * P.j;
+    xo[i] = ok ? 4u * static_cast<uint32_t>(r * P.ldx + cc) : kOob;
+    xl[i] = ok ? r * XW + cc : -1;
+  }
+  // columns J .. 4KS of both buffers stay zero
+  for (int e = tid; e < 2 * RT * 16 * (XW - P.j); e += kBlock) {
+    const int b = e / (RT * 16 * (XW - P.j)), rem = e - b * RT * 16 * (XW - P.j);
+    const int r = rem / (XW - P.j);
+    xs[b][r][P.j + (rem - r * (XW - P.j))] = 0.f;
+  }
+  const float* xbase = P.x + g * P.xg;
+  float* ybase = P.y + g * P.yg;
+  const int64_t tiles = (P.n + 16 * RT - 1) / (16 * RT);   // steps of RT*16 rows
+  float xv[XL];
+  auto gload = [&](int64_t tile) {
+    const int64_t n0 = tile * 16 * RT;
+    const int64_t rows = P.n - n0 < 16 * RT ? P.n - n0 : 16 * RT;
+    const rsrc_t rx = rsrc(xbase + n0 * P.ldx, rows > 0 ? 4 * ((rows - 1) * P.ldx + P.j) : 0);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xv[i] = ld1(rx, xo[i]);
+  };
+  auto lstore = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      if (xl[i] >= 0) (&xs[b][0][0])[xl[i]] = xv[i];
+  };
+  int64_t tile = blockIdx.x;
+  gload(tile);
+  lstore(0);
+  __syncthreads();
+  int b = 0;
+  for (; tile < tiles; tile += gridDim.x) {
+    gload(tile + gridDim.x);
+    pin();
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (!active) break;
+      // all of the tile's B values first: one LDS wait, not one per k-step
+      float bx[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) bx[s] = xs[b][16 * rt + li][4 * s + lk];
+      pin();
+      f4 acc[CT];
+#pragma unroll
+      for (int t = 0; t < CT; ++t) acc[t] = BIAS ? bias4[t] : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int t = 0; t < CT; ++t) acc[t] = mfma4(wf[s][t], bx[s], acc[t]);
+      }
+      const rsrc_t ry = tile_rsrc(ybase, P.n, (tile * RT + rt) * 16, P.ldy, P.c);
+#pragma unroll
+      for (int t = 0; t < CT; ++t) {
+        if (VEC) {
+          st4(ry, yo[t], acc[t]);
+        } else {
+          const int cb = c0 + 16 * t + 4 * lk;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            st1(ry, (yo[t] == kOob || cb + r >= P.c) ? kOob : yo[t] + 4u * r, acc[t][r]);
+        }
+      }
+    }
+    lstore(b ^ 1);
+    __syncthreads();
+    b ^= 1;
+  }
+}
+
+// ----- reduce ----------------------------------------------------------------------------
+struct ReduceParams {
+  int64_t n; int j, c, g;
+  const float* y; int64_t yg; int64_t ldy;   // Y[g][n][c] = y[g*yg + n*ldy + c]
+  const float* w; int64_t wg; int64_t ldw;   // W[g][j][c] = w[g*wg + j*ldw + c]
+  float* z; int64_t ldz; int64_t zg;         // Z[n][g*J + j] = z[n*ldz + g*zg + j]
+  int c16;                                   // 16-column groups of a row, rounded up to kRedDepth
+};
+
+constexpr int kRedWaves = 8;                 // waves per reduce workgroup
+#ifndef FA_RED_DEPTH
+#define FA_RED_DEPTH 8
+#endif
+constexpr int kRedDepth = FA_RED_DEPTH;      // column groups of Y in flight per wave
+constexpr int kRedBlock = kRedWaves * kWave;
+
+// LDS bytes of reduce: W[g] as float4 rows [J+1][4*c16 + 1] (the extra float4 staggers
+// the rows over the banks), row J zero.
+size_t reduce_lds_bytes(int j, int c16) { return static_cast<size_t>(j + 1) * (4 * c16 + 1) * 16; }
+
+// Workgroup: one head g, its W[g] in LDS; each wave takes whole 16-row tiles (grid-stride)
+// and runs over all C columns, 16 at a time: k-step 4q + t of lane l stands for column
+// 16q + 4*(l/16) + t, so a lane's A values for four k-steps are one float4 of its row and
+// its B values one float4 of W[g][j] from LDS. Four column groups of Y are in flight
+// ahead of the one multiplied (four register sets, named, so no copies between them).
+template <int JT, bool VEC>
+__global__ __launch_bounds__(kRedBlock) void head_reduce(ReduceParams P) {
+  extern __shared__ f4 wl[];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int g = blockIdx.y;
+  const int c4n = 4 * P.c16 + 1;               // LDS row stride in float4
+  const float* w = P.w + g * P.wg;
+  const bool wvec = !(P.ldw & 3) && !(reinterpret_cast<uintptr_t>(w) & 15);
+  for (int i = tid; i < (P.j + 1) * c4n; i += kRedBlock) {
+    const int jr = i / c4n, c4 = i - jr * c4n;
+    f4 v = f4{0.f, 0.f, 0.f, 0.f};
+    if (jr < P.j && wvec && 4 * c4 + 3 < P.c) {
+      v = *reinterpret_cast<const f4*>(w + jr * P.ldw + 4 * c4);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (jr < P.j && 4 * c4 + t < P.c) v[t] = w[jr * P.ldw + 4 * c4 + t];
+    }
+    wl[i] = v;
+  }
+  __syncthreads();
+  const int li = lane & 15, lk = lane >> 4;
+  int wrow[JT];
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) wrow[jt] = (16 * jt + li < P.j ? 16 * jt + li : P.j) * c4n + lk;
+  const float* ybase = P.y + g * P.yg;
+  const int64_t tiles = (P.n + 15) / 16;
+  const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
+  for (int64_t tile = static_cast<int64_t>(blockIdx.x) * kRedWaves + wave; tile < tiles;
+       tile += static_cast<int64_t>(gridDim.x) * kRedWaves) {
+    const int64_t n0 = tile * 16;
+    const rsrc_t ry = tile_rsrc(ybase, P.n, n0, P.ldy, P.c);
+    auto ly = [&](int q) -> f4 {
+      const int cq = 16 * q + 4 * lk;
+      if (VEC) return ld4(ry, cq < P.c ? yrow + 4u * cq : kOob);
+      f4 a;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) a[t] = ld1(ry, cq + t < P.c ? yrow + 4u * (cq + t) : kOob);
+      return a;
+    };
+    f4 acc[JT];
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) acc[jt] = f4{0.f, 0.f, 0.f, 0.f};
+    // W values of column group q (clamped to the row), read one group ahead of their use
+    auto lw = [&](int q, f4 (&wv)[JT]) {
+      const int qq = q < P.c16 ? q : P.c16 - 1;
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) wv[jt] = wl[wrow[jt] + 4 * qq];
+    };
+    auto mm = [&](const f4& a, const f4 (&wv)[JT]) {
+      // consecutive products go to different accumulators
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) acc[jt] = mfma4(a[t], wv[jt][t], acc[jt]);
+      }
+    };
+    // issued in order (the loop's waits count on ay[0] being the oldest); kRedDepth column
+    // groups are in flight ahead of the one multiplied
+    f4 ay[kRedDepth];
+#pragma unroll
+    for (int d = 0; d < kRedDepth; ++d) {
+      ay[d] = ly(d);
+      pin();
+    }
+    f4 wa[JT], wb[JT];
+    lw(0, wa);
+    for (int q = 0; q < P.c16; q += kRedDepth) {   // c16 is a multiple of kRedDepth
+#pragma unroll
+      for (int d = 0; d < kRedDepth; d += 2) {
+        lw(q + d + 1, wb);
+        mm(ay[d], wa);
+        pin();
+        ay[d] = ly(q + d + kRedDepth);
+        pin();
+        lw(q + d + 2, wa);
+        mm(ay[d + 1], wb);
+        pin();
+        ay[d + 1] = ly(q + d + 1 + kRedDepth);
+        pin();
+      }
+    }
+    // D row 4lk + r, column 16jt + li
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      const int jj = 16 * jt + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = n0 + 4 * lk + r;
+        if (jj < P.j && row < P.n) P.z[row * P.ldz + g * P.zg + jj] = acc[jt][r];
+      }
+    }
+  }
+}
+
+// ----- wgrad -----------------------------------------------------------------------------
+struct WgradParams {
+  int64_t n; int j, c, g, jr;                // jr = j (+1 with the ones row)
+  const float* x; int64_t ldx; int64_t xg;   // X row n, group g: x + n*ldx + g*xg
+  const float* y; int64_t yg; int64_t ldy;   // Y[g][n][c] = y[g*yg + n*ldy + c]
+  float* part;                               // [chunks][g][jr][c]
+  int64_t rows;                              // rows per chunk (multiple of 16)
+  int ncw4, njg;                             // column workgroups, 64-row j groups per head
+  int vec;                                   // Y rows 16-byte aligned and c % 4 == 0
+};
+
+constexpr int kWcols = 64;  // columns per wave in wgrad
+#ifndef FA_WGRAD_STAGE
+#define FA_WGRAD_STAGE 2
+#endif
+constexpr int kWgradStage = FA_WGRAD_STAGE;  // 16-row blocks per LDS stage
+
+// Workgroup (chunk, g, j group, column quad): each wave accumulates X^T Y over the chunk's
+// rows for 16*NJT rows j and 64 columns, 16 rows (4 k-steps, k-slot of lane l = row
+// l/16) at a time. The A values come from the block's X rows, staged in LDS by the whole
+// workgroup (coalesced loads; the ones row is a column of ones over the valid rows). Tile
+// t of the wave stands for the columns cw + 4m + t (m < 16), so the four B values of a
+// lane in a k-step are one float4, Y[row][cw + 4*(l%16) .. +3]. The next block's X and Y
+// are loaded while the current one is multiplied.
+template <int NJT, bool VEC>
+__global__ __launch_bounds__(kBlock) void head_wgrad(WgradParams P) {
+  constexpr int XW = 65;
+  constexpr int SR = 16 * kWgradStage;         // rows per stage
+  constexpr int KK = SR / 4;                   // k-steps per stage
+  constexpr int XE = SR * 64 / kBlock;         // X elements per thread and stage
+  __shared__ float xs[2][SR][XW];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int per_g = P.njg * P.ncw4;
+  const int g = blockIdx.y / per_g;
+  const int rem = blockIdx.y - g * per_g;
+  const int jg = rem / P.ncw4;
+  const int cw = ((rem - jg * P.ncw4) * kWavesPerBlock + wave) * kWcols;
+  const bool active = cw < P.c;
+  const int j0 = jg * 64;
+  const int li = lane & 15, lk = lane >> 4;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * P.rows;
+  const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
+  const float* xbase = P.x + g * P.xg;
+  const float* ybase = P.y + g * P.yg;
+  // X elements of this thread: e = tid + kBlock*i of the SR x 64 stage (row e/64, col e%64)
+  int xr[XE], xj[XE];
+  uint32_t xo[XE];
+#pragma unroll
+  for (int i = 0; i < XE; ++i) {
+    const int e = tid + kBlock * i;
+    xr[i] = e >> 6;
+    xj[i] = j0 + (e & 63);
+    xo[i] = xj[i] < P.j ? 4u * static_cast<uint32_t>(xr[i] * P.ldx + xj[i]) : kOob;
+  }
+  const int cl = cw + 4 * li;                  // first of this lane's four B columns
+  const uint32_t yo = (active && cl < P.c) ? 4u * static_cast<uint32_t>(lk * P.ldy + cl) : kOob;
+  const uint32_t ystep = 16u * static_cast<uint32_t>(P.ldy);   // 4 rows
+  // a stage's rows [nb, nb + SR) of X (rows past r1 read 0)
+  auto stage_rsrc = [&](const float* base, int64_t nb, int64_t ld, int64_t w) {
+    const int64_t rows = r1 - nb < SR ? r1 - nb : SR;
+    return rsrc(base + nb * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
+  };
+  float xv[XE];
+  auto xload = [&](int64_t nb) {
+    const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
+#pragma unroll
+    for (int i = 0; i < XE; ++i) xv[i] = ld1(rx, xo[i]);
+  };
+  auto xstore = [&](int b, int64_t nb) {
+#pragma unroll
+    for (int i = 0; i < XE; ++i) {
+      float v = xv[i];
+      if (xj[i] >= P.j) v = (xj[i] < P.jr && nb + xr[i] < r1) ? 1.f : 0.f;
+      xs[b][xr[i]][xj[i] - j0] = v;
+    }
+  };
+  auto yload = [&](int64_t nb, f4 (&bv)[KK]) {
+    const rsrc_t ry = stage_rsrc(ybase, nb, P.ldy, P.c);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (VEC) {
+        bv[kk] = ld4(ry, yo == kOob ? kOob : yo + kk * ystep);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          bv[kk][t] = ld1(ry, (yo == kOob || cl + t >= P.c) ? kOob : yo + kk * ystep + 4u * t);
+      }
+    }
+  };
+  f4 acc[NJT][4];
+#pragma unroll
+  for (int a = 0; a < NJT; ++a)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[a][t] = f4{0.f, 0.f, 0.f, 0.f};
+  auto stage = [&](int b, const f4 (&bv)[KK]) {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      // the k-step's A values first: one LDS wait per k-step, not per product
+      float av[NJT];
+#pragma unroll
+      for (int a = 0; a < NJT; ++a) av[a] = xs[b][4 * kk + lk][16 * a + li];
+#pragma unroll
+      for (int a = 0; a < NJT; ++a) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[a][t] = mfma4(av[a], bv[kk][t], acc[a][t]);
+      }
+    }
+  };
+  f4 ba[KK], bb[KK];
+  int64_t nb = r0;
+  xload(nb);
+  yload(nb, ba);
+  xstore(0, nb);
+  __syncthreads();
+  int b = 0;
+  while (nb < r1) {
+    xload(nb + SR);
+    yload(nb + SR, bb);
+    pin();
+    if (active) stage(b, ba);
+    xstore(b ^ 1, nb + SR);
+    __syncthreads();
+    b ^= 1;
+    nb += SR;
+    if (nb >= r1) break;
+    xload(nb + SR);
+    yload(nb + SR, ba);
+    pin();
+    if (active) stage(b, bb);
+    xstore(b ^ 1, nb + SR);
+    __syncthreads();
+    b ^= 1;
+    nb += SR;
+  }
+  if (!active) return;
+  // D[i][m] of tile t: row j0 + 16a + 4lk + r, column cw + 4*li + t
+  float* part = P.part + (static_cast<int64_t>(blockIdx.x) * P.g + g) * P.jr * P.c;
+#pragma unroll
+  for (int a = 0; a < NJT; ++a) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int jj = j0 + 16 * a + 4 * lk + r;
+      if (jj < P.jr) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (cl + t < P.c) part[static_cast<int64_t>(jj) * P.c + cl + t] = acc[a][t][r];
+      }
+    }
+  }
+}
+
+// out[i] = sum over chunks k of part[k*stride + i], in chunk order: 32 outputs per
+// workgroup, 8 threads per output each summing every 8th chunk, then the 8 partial sums
+// in order through LDS.
+__global__ __launch_bounds__(kBlock) void chunk_sums(const float* part, int chunks, int64_t stride,
+                                                     float* out) {
+  __shared__ float red[8][33];
+  const int o = threadIdx.x & 31, kg = threadIdx.x >> 5;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 32 + o;
+  float s = 0.f;
+  if (i < stride)
+    for (int k = kg; k < chunks; k += 8) s += part[k * stride + i];
+  red[kg][o] = s;
+  __syncthreads();
+  if (kg == 0 && i < stride) {
+    float t = red[0][o];
+#pragma unroll
+    for (int q = 1; q < 8; ++q) t += red[q][o];
+    out[i] = t;
+  }
+}
+
+constexpr int kGemmBlocks = 1024;  // workgroups of the row-tile launches
+constexpr size_t kMaxReduceLds = 160 * 1024;
+
+// Byte offsets inside a 16-row tile stay below the out-of-range marker.
+bool tile_fits(int64_t ld) { return ld >= 0 && 17 * ld * 4 < static_cast<int64_t>(kOob); }
+
+// Workgroups per grid row of the persistent proj launch: the resident workgroups shared
+// out over the grid rows, at most one per step of 16*kProjRt rows.
+int row_grid(int64_t n, int per_tile_groups, const void* kernel) {
+  const int64_t tiles = ceil_div(n, 16 * kProjRt);
+  const int64_t want = resident_blocks(kernel, 0) / (per_tile_groups > 0 ? per_tile_groups : 1);
+  const int64_t g = tiles < want ? tiles : want;
+  return static_cast<int>(g < 1 ? 1 : g);
+}
+
+// Chunks of the wgrad reduction: about kGemmBlocks workgroups in all, at least 64 rows each.
+int64_t wgrad_chunks(int64_t n, int groups) {
+  int64_t chunks = kGemmBlocks / (groups > 0 ? groups : 1);
+  if (chunks < 1) chunks = 1;
+  const int64_t by_rows = ceil_div(n, 64);
+  return chunks < by_rows ? chunks : (by_rows < 1 ? 1 : by_rows);
+}
+
+// Workgroup rows of a wgrad launch: groups x 64-row j groups x column quads.
+int wgrad_groups(int j, int c, int groups, int ones) {
+  const int jr = j + (ones ? 1 : 0);
+  const int ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), kWavesPerBlock));
+  return groups * static_cast<int>(ceil_div(jr, 64)) * ncw4;
+}
+
+void launch_proj(void (*k)(ProjParams), int64_t n, int gy, const ProjParams& P,
+                 hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(row_grid(n, gy, reinterpret_cast<const void*>(k))),
+                  static_cast<unsigned>(gy));
+  hipLaunchKernelGGL(k, grid, dim3(kBlock), 0, stream, P);
+}
+
+}  // namespace
+}  // namespace fa
+
+using namespace fa;
+
+extern "C" int fa_head_proj_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const float* x,
+                                int64_t ldx, int64_t xg, const float* w, int64_t wg, int64_t ldw,
+                                const float* bias, int64_t bg, float* y, int64_t yg, int64_t ldy,
+                                hipStream_t stream) {
+  if (n < 0 || j <= 0 || c <= 0 || groups <= 0 || j > 64) return j > 64 ? FA_EUNSUPPORTED : FA_EINVAL;
+  if (n == 0) return FA_OK;
+  if (!x || !w || !y || ldx < j || ldw < c || ldy < c) return FA_EINVAL;
+  if (!tile_fits(ldx) || !tile_fits(ldy)) return FA_EUNSUPPORTED;
+  ProjParams P;
+  P.n = n; P.j = j; P.c = c; P.g = groups;
+  P.x = x; P.ldx = ldx; P.xg = xg; P.w = w; P.wg = wg; P.ldw = ldw;
+  P.bias = bias; P.bg = bg; P.y = y; P.yg = yg; P.ldy = ldy;
+  P.vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
+  const int ncg = static_cast<int>(ceil_div(c, 16 * kProjCt));
+  P.ncg4 = static_cast<int>(ceil_div(ncg, kWavesPerBlock));
+  const int gy = groups * P.ncg4;
+  switch (static_cast<int>(ceil_div(j, 4))) {
+#define FA_PROJ_CASE(K)                                                                    \
+  case K:                                                                                  \
+    if (bias && P.vec)                                                                     \
+      launch_proj(head_proj<K, kProjCt, true, true>, n, gy, P, stream);                    \
+    else if (bias)                                                                         \
+      launch_proj(head_proj<K, kProjCt, true, false>, n, gy, P, stream);                   \
+    else if (P.vec)                                                                        \
+      launch_proj(head_proj<K, kProjCt, false, true>, n, gy, P, stream);                   \
+    else                                                                                   \
+      launch_proj(head_proj<K, kProjCt, false, false>, n, gy, P, stream);                  \
+    break;
+    FA_PROJ_CASE(1) FA_PROJ_CASE(2) FA_PROJ_CASE(3) FA_PROJ_CASE(4) FA_PROJ_CASE(5)
+    FA_PROJ_CASE(6) FA_PROJ_CASE(7) FA_PROJ_CASE(8) FA_PROJ_CASE(9) FA_PROJ_CASE(10)
+    FA_PROJ_CASE(11) FA_PROJ_CASE(12) FA_PROJ_CASE(13) FA_PROJ_CASE(14) FA_PROJ_CASE(15)
+    FA_PROJ_CASE(16)
+#undef FA_PROJ_CASE
+    default: return FA_EUNSUPPORTED;
+  }
+  return launch_status();
+}
+
+extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
+                                  const float* y, int64_t yg, int64_t ldy, const float* w,
+                                  int64_t wg, int64_t ldw, float* z, int64_t ldz, int64_t zg,
+                                  hipStream_t stream) {
+  if (n < 0 || j <= 0 || c <= 0 || groups <= 0) return FA_EINVAL;
+  if (j > 64) return FA_EUNSUPPORTED;
+  if (n == 0) return FA_OK;
+  if (!y || !w || !z || ldy < c || ldw < c || ldz < 0 || zg < 0) return FA_EINVAL;
+  if (!tile_fits(ldy)) return FA_EUNSUPPORTED;
+  ReduceParams P;
+  P.n = n; P.j = j; P.c = c; P.g = groups;
+  P.y = y; P.yg = yg; P.ldy = ldy; P.w = w; P.wg = wg; P.ldw = ldw;
+  P.z = z; P.ldz = ldz; P.zg = zg;
+  P.c16 = static_cast<int>(round_up(ceil_div(c, 16), kRedDepth));
+  const bool vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
+  const size_t lds = reduce_lds_bytes(j, P.c16);
+  if (lds > kMaxReduceLds) return FA_EUNSUPPORTED;
+  void (*k)(ReduceParams) = nullptr;
+  switch (static_cast<int>(ceil_div(j, 16))) {
+    case 1: k = vec ? head_reduce<1, true> : head_reduce<1, false>; break;
+    case 2: k = vec ? head_reduce<2, true> : head_reduce<2, false>; break;
+    case 3: k = vec ? head_reduce<3, true> : head_reduce<3, false>; break;
+    default: k = vec ? head_reduce<4, true> : head_reduce<4, false>; break;
+  }
+  const void* kp = reinterpret_cast<const void*>(k);
+  if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return launch_status();
+  const int64_t tiles = ceil_div(n, 16);
+  int64_t gx = resident_blocks(kp, lds, kRedBlock) / groups;
+  if (gx > ceil_div(tiles, kRedWaves)) gx = ceil_div(tiles, kRedWaves);
+  if (gx < 1) gx = 1;
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(groups)),
+                     dim3(kRedBlock), lds, stream, P);
+  return launch_status();
+}
+
+extern "C" size_t fa_head_wgrad_scratch_bytes(int64_t n, int32_t j, int32_t c, int32_t groups,
+                                              int32_t ones) {
+  if (n <= 0 || j <= 0 || c <= 0 || groups <= 0) return 0;
+  const int jr = j + (ones ? 1 : 0);
+  const int gy = wgrad_groups(j, c, groups, ones);
+  return static_cast<size_t>(wgrad_chunks(n, gy)) * groups * jr * c * sizeof(float);
+}
+
+extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
+                                 const float* x, int64_t ldx, int64_t xg, const float* y,
+                                 int64_t yg, int64_t ldy, int32_t ones, float* dw,
+                                 void* scratch, size_t scratch_bytes, hipStream_t stream) {
+  if (n < 0 || j <= 0 || c <= 0 || groups <= 0 || !dw) return FA_EINVAL;
+  const int jr = j + (ones ? 1 : 0);
+  const int64_t out = static_cast<int64_t>(groups) * jr * c;
+  if (n == 0) {
+    hipLaunchKernelGGL(fill_zero, dim3(static_cast<unsigned>(ceil_div(out, kBlock))), dim3(kBlock),
+                       0, stream, dw, out);
+    return launch_status();
+  }
+  if (!x || !y || ldx < j || ldy < c) return FA_EINVAL;
+  WgradParams P;
+  P.n = n; P.j = j; P.c = c; P.g = groups; P.jr = jr;
+  P.x = x; P.ldx = ldx; P.xg = xg; P.y = y; P.yg = yg; P.ldy = ldy;
+  P.vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
+  P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), kWavesPerBlock));
+  P.njg = static_cast<int>(ceil_div(jr, 64));
+  const int gy = wgrad_groups(j, c, groups, ones);
+  const int64_t chunks = wgrad_chunks(n, gy);
+  P.rows = round_up(ceil_div(n, chunks), 16 * kWgradStage);
+  // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
+  if ((P.rows + 64) * (ldx > ldy ? ldx : ldy) * 4 >= static_cast<int64_t>(kOob)) return FA_EUNSUPPORTED;
+  const int64_t used = ceil_div(n, P.rows);
+  if (!scratch || scratch_bytes < fa_head_wgrad_scratch_bytes(n, j, c, groups, ones))
+    return FA_ESCRATCH;
+  P.part = static_cast<float*>(scratch);
+  const dim3 grid(static_cast<unsigned>(used), static_cast<unsigned>(gy));
+  void (*k)(WgradParams) = nullptr;
+  switch (P.njg > 1 ? 4 : static_cast<int>(ceil_div(jr, 16))) {
+    case 1: k = P.vec ? head_wgrad<1, true> : head_wgrad<1, false>; break;
+    case 2: k = P.vec ? head_wgrad<2, true> : head_wgrad<2, false>; break;
+    case 3: k = P.vec ? head_wgrad<3, true> : head_wgrad<3, false>; break;
+    default: k = P.vec ? head_wgrad<4, true> : head_wgrad<4, false>; break;
+  }
+  hipLaunchKernelGGL(k, grid, dim3(kBlock), 0, stream, P);
+  hipLaunchKernelGGL(chunk_sums, dim3(static_cast<unsigned>(ceil_div(out, 32))), dim3(kBlock), 0,
+                     stream, static_cast<const float*>(P.part), static_cast<int>(used), out, dw);
+  return launch_status();
+}

@@ -70,16 +70,16 @@ struct TgatParams {
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
   int tvs;                            // LDS row stride of the tiles: 4*ct + bias chunk + zero chunk
   int64_t kp;                         // row stride of qt / xbar = 4*cp
-  const float* qt; int64_t qt_rs;
+  const float* qt; int64_t qt_rs, qt_hs;    // row (destination) and head strides
   float slope;
   const float* drop;                  // explicit [E][H] multipliers, or
   uint64_t drop_seed; float drop_p, drop_scale; int drop_hash;  // hashed dropout
   // forward outputs / backward input
-  float* xbar; int64_t xbar_rs;
+  float* xbar; int64_t xbar_rs, xbar_hs;
   float* scores; float* stats;
   // backward
-  const float* dxbar; int64_t dxbar_rs;
-  float* dqt; int64_t dqt_rs;
+  const float* dxbar; int64_t dxbar_rs, dxbar_hs;
+  float* dqt; int64_t dqt_rs, dqt_hs;
   float* d_node; int64_t ld_dnode;
   float* partial;                     // [gridDim.x][2][dt_dim]
 };
@@ -365,27 +365,27 @@ __device__ __forceinline__ void assemble_x(const TgatParams& P, const LaneCtx<NS
   }
 }
 
-// Rows of a per-destination [heads][Kp] block: destination v starts at base + v*rs, head h
-// at + h*kp.
+// Rows of a per-destination [heads][Kp] block: destination v, head h starts at
+// base + v*rs + h*hs.
 template <int H, int NS>
-__device__ __forceinline__ void load_rows(const float* base, int64_t rs, int64_t v, int64_t kp,
-                                          float4 (&r)[H][NS]) {
+__device__ __forceinline__ void load_rows(const float* base, int64_t rs, int64_t hs, int64_t v,
+                                          int64_t kp, float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const rsrc_t rr = make_rsrc(base + v * rs + h * kp, 4u * static_cast<uint32_t>(kp));
+    const rsrc_t rr = make_rsrc(base + v * rs + h * hs, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
     for (int k = 0; k < NS; ++k) r[h][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
   }
 }
 
 template <int H, int NS>
-__device__ __forceinline__ void store_rows(float* base, int64_t rs, int64_t v, int64_t kp,
-                                           const float4 (&r)[H][NS]) {
+__device__ __forceinline__ void store_rows(float* base, int64_t rs, int64_t hs, int64_t v,
+                                           int64_t kp, const float4 (&r)[H][NS]) {
   const int lane = lane_id();
 #pragma unroll
   for (int h = 0; h < H; ++h) {
-    const rsrc_t rr = make_rsrc(base + v * rs + h * kp, 4u * static_cast<uint32_t>(kp));
+    const rsrc_t rr = make_rsrc(base + v * rs + h * hs, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
     for (int k = 0; k < NS; ++k) bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), r[h][k]);
   }
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
       for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
     }
     if (e1 <= e0) {  // zero-degree destination: xbar = 0
-      store_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, S.acc);
+      store_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, S.acc);
       if (lane < H) {
         P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
         P.stats[(v * H + lane) * 2 + 1] = 0.f;
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
     int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
     EdgeMeta<H, false> M;
     stage_meta<H, false>(P, c0, cnt, M);
-    load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
+    load_rows<H, NS>(P.qt, P.qt_rs, P.qt_hs, v, P.kp, S.q);
     float4 xa[kBatch][NS], xb[kBatch][NS];
     issue_rows<NS, H, false>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     for (;;) {
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
 #pragma unroll
       for (int k = 0; k < NS; ++k) scale4(S.acc[h][k], inv);
     }
-    store_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, S.acc);
+    store_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, S.acc);
     if (lane < H) {
       float mm = 0.f, ll = 0.f;
 #pragma unroll
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
     if (e1 <= e0) {
-      store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
+      store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
       continue;
     }
     // Prologue: the first chunk's metadata and the per-destination rows (q~, dxbar, xbar)
@@ -658,10 +658,10 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
     EdgeMeta<H, true> M;
     stage_meta<H, true>(P, c0, cnt, M);
-    load_rows<H, NS>(P.qt, P.qt_rs, v, P.kp, S.q);
-    load_rows<H, NS>(P.dxbar, P.dxbar_rs, v, P.kp, S.g);
+    load_rows<H, NS>(P.qt, P.qt_rs, P.qt_hs, v, P.kp, S.q);
+    load_rows<H, NS>(P.dxbar, P.dxbar_rs, P.dxbar_hs, v, P.kp, S.g);
     float4 xr[H][NS];
-    load_rows<H, NS>(P.xbar, P.xbar_rs, v, P.kp, xr);
+    load_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, xr);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
@@ -691,7 +691,7 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
       stage_meta<H, true>(P, c0, cnt, M);
       issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     }
-    store_rows<H, NS>(P.dqt, P.dqt_rs, v, P.kp, S.dq);
+    store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
   }
 
   // Time-grad partials of this workgroup: waves combined in a fixed order. Every time dim
@@ -728,13 +728,6 @@ __global__ __launch_bounds__(kBlock) void time_grad_reduce(const float* partial,
   if (lane_id() == 0) (which == 0 ? d_w : d_b)[j] = s;
 }
 
-// Zero fill by a kernel rather than hipMemsetAsync, so the call is safe under graph capture.
-__global__ __launch_bounds__(kBlock) void fill_zero(float* p, int64_t n) {
-  for (int64_t i = threadIdx.x + static_cast<int64_t>(blockIdx.x) * kBlock; i < n;
-       i += static_cast<int64_t>(gridDim.x) * kBlock)
-    p[i] = 0.f;
-}
-
 __global__ __launch_bounds__(kBlock) void attn_weights(const int64_t* dst, int64_t n_edges,
                                                       int64_t n_dst, int heads,
                                                       const float* scores, const float* stats,
@@ -766,7 +759,8 @@ __global__ __launch_bounds__(kBlock) void gather_rows(const T* tab, int64_t ld_t
 // ---------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------
-int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_rs, float slope,
+int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_rs, int64_t qt_hs,
+                float slope,
                 const float* drop, uint64_t drop_seed, float drop_p, TgatParams& P) {
   if (!g || heads <= 0) return FA_EINVAL;
   if (g->n_dst < 0 || g->n_edges < 0 || g->dn < 0 || g->de < 0 || g->dt_dim < 0) return FA_EINVAL;
@@ -811,16 +805,31 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_r
   P.cp = P.cn + P.ce + P.ct + 1;
   P.tvs = 4 * (P.ct + 2);
   P.kp = 4 * static_cast<int64_t>(P.cp);
-  P.qt = qt; P.qt_rs = qt_rs; P.slope = slope; P.drop = drop;
+  P.qt = qt; P.qt_rs = qt_rs; P.qt_hs = qt_hs; P.slope = slope; P.drop = drop;
   if (!(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
   P.drop_seed = drop_seed;
   P.drop_p = drop_p;
   P.drop_scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
   P.drop_hash = (drop == nullptr && drop_p > 0.f) ? 1 : 0;
-  if (!aligned16(qt)) return FA_EALIGN;
-  if (qt_rs & 3) return FA_EALIGN;
-  if (qt_rs < P.kp * heads) return FA_EINVAL;
+  if (!aligned16(qt) || (qt_rs & 3) || (qt_hs & 3)) return FA_EALIGN;
+  if (qt_rs < 0 || qt_hs < 0) return FA_EINVAL;  // an input block may repeat (stride 0)
   return FA_OK;
+}
+
+// An output block: 16-byte aligned, strides multiples of 4, and no two (destination, head)
+// rows overlap, i.e. destination-major ([n_dst][heads][Kp]-like) or head-major
+// ([heads][n_dst][Kp]-like).
+int check_out_rows(const void* p, int64_t rs, int64_t hs, int64_t kp, int heads, int64_t n_dst) {
+  if (!aligned16(p) || (rs & 3) || (hs & 3)) return FA_EALIGN;
+  const bool dst_major = rs >= kp && (heads == 1 || (hs >= kp && rs >= hs * heads));
+  const bool head_major = hs >= kp && rs >= kp && hs >= rs * n_dst;
+  return dst_major || head_major ? FA_OK : FA_EINVAL;
+}
+
+// An input block read alongside the outputs: aligned, non-negative strides.
+int check_in_rows(const void* p, int64_t rs, int64_t hs) {
+  if (!aligned16(p) || (rs & 3) || (hs & 3)) return FA_EALIGN;
+  return rs < 0 || hs < 0 ? FA_EINVAL : FA_OK;
 }
 
 size_t fwd_lds_bytes(const TgatParams& P) {
@@ -837,18 +846,28 @@ int stride_grid(int64_t n_dst) {
   return static_cast<int>(want < kMaxBlocks ? (want < 1 ? 1 : want) : kMaxBlocks);
 }
 
+// Persistent launch: at most the resident workgroups, so every workgroup runs in the first
+// (and only) round.
+int persistent_grid(int64_t n_dst, const void* kernel, size_t lds) {
+  const int want = stride_grid(n_dst);
+  const int res = resident_blocks(kernel, lds);
+  return want < res ? want : res;
+}
+
 template <int H>
 int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
-  const dim3 grid(static_cast<unsigned>(stride_grid(P.n_dst)));
   const size_t lds = fwd_lds_bytes(P);
+  void (*k)(TgatParams) = nullptr;
   switch (ns) {
-    case 1: hipLaunchKernelGGL((tgat_fwd<H, 1>), grid, dim3(kBlock), lds, stream, P); break;
-    case 2: hipLaunchKernelGGL((tgat_fwd<H, 2>), grid, dim3(kBlock), lds, stream, P); break;
-    case 3: hipLaunchKernelGGL((tgat_fwd<H, 3>), grid, dim3(kBlock), lds, stream, P); break;
-    case 4: hipLaunchKernelGGL((tgat_fwd<H, 4>), grid, dim3(kBlock), lds, stream, P); break;
+    case 1: k = tgat_fwd<H, 1>; break;
+    case 2: k = tgat_fwd<H, 2>; break;
+    case 3: k = tgat_fwd<H, 3>; break;
+    case 4: k = tgat_fwd<H, 4>; break;
     default: return FA_EUNSUPPORTED;
   }
+  const dim3 grid(static_cast<unsigned>(persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds)));
+  hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, stream, P);
   return launch_status();
 }
 
@@ -856,17 +875,21 @@ constexpr size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup used by the 
 
 int bwd_grid(int64_t n_dst) { return stride_grid(n_dst); }
 
+// `grid` returns the workgroups launched (rows of the time-gradient partials).
 template <int H>
-int launch_bwd_h(const TgatParams& P, int grid, hipStream_t stream) {
+int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
   const size_t lds = bwd_lds_bytes(P);
+  void (*k)(TgatParams) = nullptr;
   switch (ns) {
-    case 1: hipLaunchKernelGGL((tgat_bwd<H, 1>), dim3(grid), dim3(kBlock), lds, stream, P); break;
-    case 2: hipLaunchKernelGGL((tgat_bwd<H, 2>), dim3(grid), dim3(kBlock), lds, stream, P); break;
-    case 3: hipLaunchKernelGGL((tgat_bwd<H, 3>), dim3(grid), dim3(kBlock), lds, stream, P); break;
-    case 4: hipLaunchKernelGGL((tgat_bwd<H, 4>), dim3(grid), dim3(kBlock), lds, stream, P); break;
+    case 1: k = tgat_bwd<H, 1>; break;
+    case 2: k = tgat_bwd<H, 2>; break;
+    case 3: k = tgat_bwd<H, 3>; break;
+    case 4: k = tgat_bwd<H, 4>; break;
     default: return FA_EUNSUPPORTED;
   }
+  grid = persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds);
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(kBlock), lds, stream, P);
   return launch_status();
 }
 
@@ -881,19 +904,19 @@ extern "C" int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim) {
 }
 
 extern "C" int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_rs, float slope, const float* drop,
+                                    int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
                                     uint64_t drop_seed, float drop_p, float* xbar,
-                                    int64_t xbar_rs, float* scores, float* stats,
+                                    int64_t xbar_rs, int64_t xbar_hs, float* scores, float* stats,
                                     hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_rs, slope, drop, drop_seed, drop_p, P);
+  int st = fill_params(g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) return FA_OK;
   if (fwd_lds_bytes(P) > kMaxLds) return FA_EUNSUPPORTED;
   if (!xbar || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if (!aligned16(xbar) || (xbar_rs & 3)) return FA_EALIGN;
-  if (xbar_rs < P.kp * heads) return FA_EINVAL;
-  P.xbar = xbar; P.xbar_rs = xbar_rs; P.scores = scores; P.stats = stats;
+  st = check_out_rows(xbar, xbar_rs, xbar_hs, P.kp, heads, P.n_dst);
+  if (st != FA_OK) return st;
+  P.xbar = xbar; P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs; P.scores = scores; P.stats = stats;
   if (static_cast<int64_t>(kBatch) * heads > kWave) return FA_EUNSUPPORTED;
   switch (heads) {
     case 1: return launch_fwd_h<1>(P, stream);
@@ -921,15 +944,16 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
 }
 
 extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_rs, float slope, const float* drop,
-                                    uint64_t drop_seed, float drop_p,
-                                    const float* xbar, int64_t xbar_rs, const float* scores,
+                                    int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
+                                    uint64_t drop_seed, float drop_p, const float* xbar,
+                                    int64_t xbar_rs, int64_t xbar_hs, const float* scores,
                                     const float* stats, const float* dxbar, int64_t dxbar_rs,
-                                    float* dqt, int64_t dqt_rs, float* d_node, int64_t ld_dnode,
+                                    int64_t dxbar_hs, float* dqt, int64_t dqt_rs, int64_t dqt_hs,
+                                    float* d_node, int64_t ld_dnode,
                                     float* d_time_w, float* d_time_b, void* scratch,
                                     size_t scratch_bytes, hipStream_t stream) {
   TgatParams P;
-  int st = fill_params(g, heads, qt, qt_rs, slope, drop, drop_seed, drop_p, P);
+  int st = fill_params(g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
   if (P.n_dst == 0) {
     if (P.dt_dim > 0 && d_time_w && d_time_b) {
@@ -940,19 +964,18 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   }
   if (bwd_lds_bytes(P) > kMaxLds || P.ct > kWave) return FA_EUNSUPPORTED;
   if (!xbar || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if (!aligned16(xbar) || !aligned16(dxbar) || !aligned16(dqt) || (xbar_rs & 3) || (dxbar_rs & 3) ||
-      (dqt_rs & 3))
-    return FA_EALIGN;
-  if (xbar_rs < P.kp * heads || dxbar_rs < P.kp * heads || dqt_rs < P.kp * heads)
-    return FA_EINVAL;
+  if ((st = check_in_rows(xbar, xbar_rs, xbar_hs)) != FA_OK) return st;
+  if ((st = check_in_rows(dxbar, dxbar_rs, dxbar_hs)) != FA_OK) return st;
+  if ((st = check_out_rows(dqt, dqt_rs, dqt_hs, P.kp, heads, P.n_dst)) != FA_OK) return st;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
   if (d_node && P.node_bf16) return FA_EUNSUPPORTED;  // node gradients for float32 rows only
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
-  const int grid = bwd_grid(P.n_dst);
+  int grid = bwd_grid(P.n_dst);   // the most workgroups a launch uses (scratch rows)
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
-  P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs;
-  P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dqt = dqt; P.dqt_rs = dqt_rs;
+  P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs;
+  P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dxbar_hs = dxbar_hs;
+  P.dqt = dqt; P.dqt_rs = dqt_rs; P.dqt_hs = dqt_hs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
   // 16-byte node-gradient stores need 16-byte aligned gradient rows as well
   if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.dnode_dwords = 1;

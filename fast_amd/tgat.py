@@ -5,16 +5,18 @@ order, initialisation) and ``forward(b, _layers, _hist)`` of the reference layer
 (layers.py:53-240, TGAT/TGN branch) and computes the same function. Its data path differs:
 
   reference                                   this layer
-  K = w_k(cat[h_src, f, cos(w dt+b)])  [E,D]  qt[v,h] = Q[v,h] W_k[h] (+ b_k column)   [N,H,Kp]
-  V = w_v(cat[...])                    [E,D]  xbar[v,h] = sum_e a'[e,h] x_e (one kernel) [N,H,Kp]
-  score = sum(Q[dst]*K), softmax, V*att,      rst = w_out([W_v xbar | h_dst])
-  update_all(copy_u, sum), w_out
+  K = w_k(cat[h_src, f, cos(w dt+b)])  [E,D]  qt[h,v] = Q[v,h] W_k[h] (+ b_k column)   [H,N,Kp]
+  V = w_v(cat[...])                    [E,D]  xbar[h,v] = sum_e a'[e,h] x_e (one kernel) [H,N,Kp]
+  score = sum(Q[dst]*K), softmax, V*att,      agg[v,h] = W_v[h] xbar[h,v]               [N,D]
+  update_all(copy_u, sum), w_out              rst = w_out([agg | h_dst])
 
-so the K/V projections run over the N destinations instead of the E edges (and fold into
-the neighbouring projections: qt comes from h_dst in one product, xbar goes through
-W_o[:, :D] W_v in one product), and the neighbour gather, time encoding, scoring, segment
-softmax and weighted reduction happen in one pass over the gathered rows x_e (never
-written to memory).
+so the K/V projections run over the N destinations instead of the E edges, one head at a
+time (Q[v,h] has D/H entries, so the per-head products cost D*Kp per destination, where
+one folded product over all heads would cost H*D*Kp), and the neighbour gather, time
+encoding, scoring, segment softmax and weighted reduction happen in one pass over the
+gathered rows x_e (never written to memory). The per-head products run on the matrix
+cores (fastAgg.head_proj / head_reduce / head_wgrad), head-major so that each head's
+block [N, Kp] is contiguous.
 """
 from __future__ import annotations
 
@@ -260,7 +262,7 @@ class _Graph:
 class TgatAttention(torch.autograd.Function):
     """xbar = fused gather/time-encode/score/softmax/reduce (see module docstring).
 
-    Differentiable inputs: ``qt`` [N,H,Kp], ``time_w`` [Dt], ``time_b`` [Dt] and
+    Differentiable inputs: ``qt`` [H,N,Kp], ``time_w`` [Dt], ``time_b`` [Dt] and
     ``node_src`` (the node rows feeding the edges: one row per edge when ``node_idx`` is
     None, else a table gathered by ``node_idx``)."""
 
@@ -273,8 +275,8 @@ class TgatAttention(torch.autograd.Function):
                                                     float(slope), drop, int(drop_seed),
                                                     float(drop_p))
         if t0 is not None:
-            nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
-                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
+            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
                                     g.node_idx is not None, g.edge_idx is not None,
                                     node_bytes=node_src.element_size(),
                                     edge_bytes=g.edge_tab.element_size())["fwd"]
@@ -305,8 +307,8 @@ class TgatAttention(torch.autograd.Function):
                                                         ctx.drop_seed, ctx.drop_p, xbar,
                                                         scores, stats, dxbar, need_node)
         if t0 is not None:
-            nb = fused_kernel_bytes(qt.shape[0], g.dt.numel(), node_src.shape[1],
-                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[1],
+            nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
+                                    g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
                                     g.node_idx is not None, g.edge_idx is not None,
                                     need_node, node_bytes=node_src.element_size(),
                                     edge_bytes=g.edge_tab.element_size())["bwd"]
@@ -352,6 +354,45 @@ class RowLinear(torch.autograd.Function):
         dW = _rows_t_mm(dy, x) if ctx.needs_input_grad[1] else None
         db = dy.sum(0) if ctx.has_b and ctx.needs_input_grad[2] else None
         return dx, dW, db
+
+
+class HeadProj(torch.autograd.Function):
+    """y[g] = x[:, g*J:(g+1)*J] @ w[g] (+ bias[g]) for x [N, G*J], w [G, J, C] -> [G, N, C]."""
+
+    @staticmethod
+    def forward(ctx, x, w, bias):
+        ctx.save_for_backward(x, w)
+        ctx.has_bias = bias is not None
+        return fastAgg.head_proj(x, w, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = fastAgg.head_reduce(dy, w)
+        if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
+            gw = fastAgg.head_wgrad(x, dy, w.shape[0], ctx.has_bias)
+            dw = gw[:, :w.shape[1]]
+            db = gw[:, w.shape[1]] if ctx.has_bias else None
+        return dx, dw, db
+
+
+class HeadReduce(torch.autograd.Function):
+    """z[:, g*J:(g+1)*J] = y[g] @ w[g]^T for y [G, N, C], w [G, J, C] -> [N, G*J]."""
+
+    @staticmethod
+    def forward(ctx, y, w):
+        ctx.save_for_backward(y, w)
+        return fastAgg.head_reduce(y, w)
+
+    @staticmethod
+    def backward(ctx, dz):
+        y, w = ctx.saved_tensors
+        dz = dz.contiguous()
+        dy = fastAgg.head_proj(dz, w, None) if ctx.needs_input_grad[0] else None
+        dw = fastAgg.head_wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
+        return dy, dw
 
 
 class TgatEpilogue(torch.autograd.Function):
@@ -445,19 +486,14 @@ class TransfomerAttentionLayer(torch.nn.Module):
             return torch.zeros((N, D), device=dev)
         hdst = b.dst_node_feats() if Dn > 0 else None
         kp = kspace_width(Dn, De, Dt)
-        # Absorbed keys: qt[v, h, :] = Q[v, h, :] W_k,aug[h], as one product
-        # hdst (Wk_blk W_q)^T + Wk_blk b_q with Wk_blk = blockdiag_h(W_k,aug[h]^T).
+        # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h].
         wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
-        wk_blk = torch.block_diag(*[wk[h].t() for h in range(H)])          # [H*kp, D]
-        if Dn + Dt == 0:  # layers.py:137-140: Q = 1
-            qt = wk_blk.sum(1).expand(N, H * kp).contiguous()
-        else:
-            qb = wk_blk @ self._query_bias()
-            if Dn > 0:
-                qt = RowLinear.apply(hdst, wk_blk @ self.w_q.weight[:, :Dn], qb)
-            else:
-                qt = qb.expand(N, H * kp).contiguous()
-        qt = qt.view(N, H, kp)
+        if Dn > 0:
+            q = RowLinear.apply(hdst, self.w_q.weight[:, :Dn], self._query_bias())
+            qt = HeadProj.apply(q, wk, None)
+        else:  # one query for every destination: the time part alone (or 1, layers.py:137-140)
+            q1 = self._query_bias() if Dt > 0 else torch.ones(D, device=dev)
+            qt = HeadProj.apply(q1.view(1, D), wk, None).expand(H, N, kp)
 
         node_src, node_idx = b.src_node_source() if Dn > 0 else (None, None)
         edge_tab, edge_idx = b.edge_source() if De > 0 else (None, None)
@@ -478,18 +514,16 @@ class TransfomerAttentionLayer(torch.nn.Module):
         xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop, drop_seed,
                                    drop_p)
 
-        # Absorbed values and output projection: agg = xbar Wv_blk^T with
-        # Wv_blk = blockdiag_h(W_v,aug[h]), then rst = w_out([agg | hdst]) as
-        # xbar (W_o[:, :D] Wv_blk)^T + hdst W_o[:, D:]^T + b_o.
+        # Absorbed values, head by head: agg[v, h, :] = W_v,aug[h] xbar[h, v, :], then
+        # rst = w_out([agg | hdst]) as agg W_o[:, :D]^T + hdst W_o[:, D:]^T + b_o.
         wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
-        wv_blk = torch.block_diag(*[wv[h] for h in range(H)])              # [D, H*kp]
+        agg = HeadReduce.apply(xbar, wv)
         Wo = self.w_out.weight
-        xflat = xbar.view(N, H * kp)
         if Dn > 0:
-            r1 = RowLinear.apply(xflat, Wo[:, :D] @ wv_blk, None)
+            r1 = RowLinear.apply(agg, Wo[:, :D], None)
             r2 = RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias)
         else:
-            r1 = RowLinear.apply(xflat, Wo @ wv_blk, self.w_out.bias)
+            r1 = RowLinear.apply(agg, Wo, self.w_out.bias)
             r2 = None
         ln = self.layer_norm
         return TgatEpilogue.apply(r1, r2, ln.weight, ln.bias, ln.eps, out_drop_seed, out_drop_p)

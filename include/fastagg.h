@@ -206,19 +206,21 @@ typedef struct fa_tgat_graph {
 /* K-space width Kp for the given dims (all > = 0). */
 int64_t fa_tgat_kspace(int32_t dn, int32_t de, int32_t dt_dim);
 
-/* Forward. Per-destination blocks are [heads][Kp] rows: qt row of destination v, head h
- * at qt + v*qt_rs + h*Kp (qt_rs >= heads*Kp, a multiple of 4), i.e. a [n_dst][heads][Kp]
- * array when qt_rs = heads*Kp; xbar, dxbar and dqt below use the same layout with their own
- * row strides.
+/* Forward. Per-destination blocks are rows of Kp floats: the qt row of destination v and
+ * head h starts at qt + v*qt_rs + h*qt_hs (16-byte aligned, strides multiples of 4), so
+ * (qt_rs, qt_hs) = (heads*Kp, Kp) is a [n_dst][heads][Kp] array and (Kp, n_dst*Kp) a
+ * [heads][n_dst][Kp] one; xbar, dxbar and dqt below take their own strides. Inputs may
+ * repeat rows (stride 0); the rows of an output must not overlap (destination-major:
+ * rs >= heads*hs, hs >= Kp; or head-major: hs >= n_dst*rs, rs >= Kp).
  * Attention dropout: drop = optional explicit [n_edges][heads] multipliers (keep/(1-p) or
  * 0); when drop is NULL and drop_p > 0, entry (e,h) is kept iff the counter-based hash of
  * (drop_seed, e*heads+h) clears drop_p (see fa_dropout_mask_f32); drop_p = 0: no dropout.
- * Outputs: xbar (row stride xbar_rs), scores [n_edges][heads] (post-LeakyReLU),
+ * Outputs: xbar, scores [n_edges][heads] (post-LeakyReLU),
  * stats [n_dst][heads][2] = (max, sum of exp). */
 int fa_tgat_attn_fwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,
-                         float drop_p, float* xbar, int64_t xbar_rs, float* scores,
-                         float* stats, hipStream_t stream);
+                         int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
+                         uint64_t drop_seed, float drop_p, float* xbar, int64_t xbar_rs,
+                         int64_t xbar_hs, float* scores, float* stats, hipStream_t stream);
 
 /* The multipliers of the hashed attention dropout: out[i] = 1/(1-p) if
  * (hash(seed, i) >> 8) / 2^24 >= p else 0, for i < n (i = e*heads + h). */
@@ -232,18 +234,49 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
 
 /* Backward, one pass over the edges. xbar: the forward output (its dot product with dxbar
  * gives each destination's softmax correction); dxbar: gradient of xbar. Outputs: dqt
- * (layout of qt, row stride dqt_rs); d_node [n_edges][ld_dnode] gradient of the
+ * (strides dqt_rs, dqt_hs); d_node [n_edges][ld_dnode] gradient of the
  * node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be NULL
  * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim).
  * dt_dim <= 256, and d_node only with a float32 node table (FA_EUNSUPPORTED otherwise). */
 size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                         int64_t qt_rs, float slope, const float* drop, uint64_t drop_seed,
-                         float drop_p, const float* xbar,
-                         int64_t xbar_rs, const float* scores, const float* stats,
-                         const float* dxbar, int64_t dxbar_rs, float* dqt, int64_t dqt_rs,
-                         float* d_node, int64_t ld_dnode, float* d_time_w, float* d_time_b,
-                         void* scratch, size_t scratch_bytes, hipStream_t stream);
+                         int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
+                         uint64_t drop_seed, float drop_p, const float* xbar, int64_t xbar_rs,
+                         int64_t xbar_hs, const float* scores, const float* stats,
+                         const float* dxbar, int64_t dxbar_rs, int64_t dxbar_hs, float* dqt,
+                         int64_t dqt_rs, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
+                         float* d_time_w, float* d_time_b, void* scratch,
+                         size_t scratch_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------------
+ * Per-head projections of the K-space blocks (new ops: the reference applies w_q, w_k,
+ * w_v per edge as torch GEMMs, layers.py:162-169). G heads, J = dim_out/heads (<= 64),
+ * C = Kp columns; W[g][j][c] = w[g*wg + j*ldw + c]. All float32 on the matrix cores.
+ * ------------------------------------------------------------------------------- */
+
+/* Y[g][n][c] = sum_j X[n][j] W[g][j][c] (+ bias[g*bg + c] when bias != NULL), with
+ * X[n][j] = x[n*ldx + g*xg + j] and Y[g][n][c] = y[g*yg + n*ldy + c]. */
+int fa_head_proj_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const float* x,
+                     int64_t ldx, int64_t xg, const float* w, int64_t wg, int64_t ldw,
+                     const float* bias, int64_t bg, float* y, int64_t yg, int64_t ldy,
+                     hipStream_t stream);
+
+/* Z[n][g][j] = z[n*ldz + g*zg + j] = sum_c Y[g][n][c] W[g][j][c]
+ * (the transpose product of fa_head_proj_f32), Y[g][n][c] = y[g*yg + n*ldy + c]. */
+int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const float* y,
+                       int64_t yg, int64_t ldy, const float* w, int64_t wg, int64_t ldw,
+                       float* z, int64_t ldz, int64_t zg, hipStream_t stream);
+
+/* dw[g][j][c] = sum_n X[n][j] Y[g][n][c] (X, Y as in fa_head_proj_f32 / fa_head_reduce_f32),
+ * [groups][j + ones][c] contiguous; with ones != 0 row j holds sum_n Y[g][n][c] (the
+ * gradient of a per-column bias). Partial sums over row chunks go to scratch
+ * (fa_head_wgrad_scratch_bytes) and are added in a fixed order: results are deterministic. */
+size_t fa_head_wgrad_scratch_bytes(int64_t n, int32_t j, int32_t c, int32_t groups,
+                                   int32_t ones);
+int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const float* x,
+                      int64_t ldx, int64_t xg, const float* y, int64_t yg, int64_t ldy,
+                      int32_t ones, float* dw, void* scratch, size_t scratch_bytes,
+                      hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------
  * Fused layer epilogue (layers.py:224-237: w_out, dropout, ReLU, LayerNorm). New op: the

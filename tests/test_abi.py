@@ -36,7 +36,8 @@ def test_header_declares_the_path():
     for must in ("fa_tgat_attn_fwd_f32", "fa_tgat_attn_bwd_f32", "fa_edge_softmax_fwd_f32",
                  "fa_edge_softmax_bwd_f32", "fa_edge_scatter_sum_f32", "fa_segment_sum_f32",
                  "fa_exclusive_sum_i32", "fa_degree_count_i32", "fa_balance_mask_i32",
-                 "fa_fused_attn_fwd_f32", "fa_fused_attn_bwd_f32", "fa_group_softmax_fwd_f32"):
+                 "fa_fused_attn_fwd_f32", "fa_fused_attn_bwd_f32", "fa_group_softmax_fwd_f32",
+                 "fa_head_proj_f32", "fa_head_reduce_f32", "fa_head_wgrad_f32"):
         assert must in names
 
 
@@ -61,7 +62,7 @@ def test_status_strings_and_version(lib):
         assert lib.fa_status_string(st)
     assert lib.fa_status_string(FA_OK) == b"success"
     assert lib.fa_status_string(-99) == b"unknown status"
-    assert lib.fa_abi_version() // 100 == 2
+    assert lib.fa_abi_version() // 100 == 3
 
 
 def test_kspace_width(lib):
@@ -85,6 +86,15 @@ def test_scratch_sizes(lib):
     assert 0 < small <= big
     assert big <= 64 << 20  # per-workgroup partials of the time gradients: bounded
     assert lib.fa_exclusive_sum_scratch_bytes(ctypes.c_int64(10 ** 6)) >= 0
+    lib.fa_head_wgrad_scratch_bytes.restype = ctypes.c_size_t
+    hw = lambda n, ones: lib.fa_head_wgrad_scratch_bytes(ctypes.c_int64(n), ctypes.c_int32(50),
+                                                         ctypes.c_int32(376), ctypes.c_int32(2),
+                                                         ctypes.c_int32(ones))
+    assert hw(0, 0) == 0
+    # one [heads][j(+1)][c] partial per row chunk; the chunk count is capped
+    assert hw(16, 0) == 1 * 2 * 50 * 376 * 4
+    assert hw(16, 1) == 1 * 2 * 51 * 376 * 4
+    assert 0 < hw(132000, 1) <= 1024 * 2 * 51 * 376 * 4
 
 
 class TgatGraph(ctypes.Structure):
@@ -100,17 +110,21 @@ class TgatGraph(ctypes.Structure):
                 ("dt_dim", ctypes.c_int32)]
 
 
-def _fwd(lib, g, heads=2, qt=None, qt_hs=0):
+def _fwd(lib, g, heads=2, qt=None, qt_rs=0, qt_hs=0, xbar=None, xbar_rs=0, xbar_hs=0,
+         scores=None, stats=None):
     return lib.fa_tgat_attn_fwd_f32(ctypes.byref(g), ctypes.c_int32(heads), ctypes.c_void_p(qt),
-                                    ctypes.c_int64(qt_hs), ctypes.c_float(0.2), None,
-                                    ctypes.c_uint64(0), ctypes.c_float(0.0), None,
-                                    ctypes.c_int64(0), None, None, None)
+                                    ctypes.c_int64(qt_rs), ctypes.c_int64(qt_hs),
+                                    ctypes.c_float(0.2), None, ctypes.c_uint64(0),
+                                    ctypes.c_float(0.0), ctypes.c_void_p(xbar),
+                                    ctypes.c_int64(xbar_rs), ctypes.c_int64(xbar_hs),
+                                    ctypes.c_void_p(scores), ctypes.c_void_p(stats), None)
 
 
 def test_tgat_fwd_rejects_bad_arguments(lib):
     """Argument errors come back as FA_E* codes before anything touches a device."""
-    assert lib.fa_tgat_attn_fwd_f32(None, 2, None, 0, ctypes.c_float(0.2), None, 0,
-                                    ctypes.c_float(0.0), None, 0, None, None, None) == FA_EINVAL
+    assert lib.fa_tgat_attn_fwd_f32(None, 2, None, 0, 0, ctypes.c_float(0.2), None, 0,
+                                    ctypes.c_float(0.0), None, 0, 0, None, None,
+                                    None) == FA_EINVAL
     g = TgatGraph(n_dst=-1)
     assert _fwd(lib, g) == FA_EINVAL
     g = TgatGraph(n_dst=4, n_edges=8, rowptr=None, dn=4, ld_node=4)
@@ -121,6 +135,49 @@ def test_tgat_fwd_rejects_bad_arguments(lib):
     assert _fwd(lib, g, qt=64) == FA_EINVAL  # time encoding without dt / w / b
     g = TgatGraph(n_dst=4, n_edges=8, rowptr=16)
     assert _fwd(lib, g, heads=0, qt=64) == FA_EINVAL
+
+
+def test_tgat_block_layouts_are_checked(lib):
+    """Per-destination blocks: 16-byte alignment, strides in whole float4s, and output rows
+    that do not overlap (destination-major or head-major); all rejected before a launch."""
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=16)           # Kp = 4
+    ok = dict(scores=4096, stats=8192)
+    assert _fwd(lib, g, qt=68, qt_rs=8, qt_hs=4) == FA_EALIGN
+    assert _fwd(lib, g, qt=64, qt_rs=6, qt_hs=4) == FA_EALIGN
+    assert _fwd(lib, g, qt=64, qt_rs=-8, qt_hs=4) == FA_EINVAL
+    # the two heads of a destination on top of each other, or on the next destination
+    assert _fwd(lib, g, qt=64, xbar=128, xbar_rs=8, xbar_hs=0, **ok) == FA_EINVAL
+    assert _fwd(lib, g, qt=64, xbar=128, xbar_rs=4, xbar_hs=4, **ok) == FA_EINVAL
+    # head-major rows that run into the next head
+    assert _fwd(lib, g, qt=64, xbar=128, xbar_rs=4, xbar_hs=12, **ok) == FA_EINVAL
+    assert _fwd(lib, g, qt=64, xbar=132, xbar_rs=8, xbar_hs=4, **ok) == FA_EALIGN
+
+
+def test_head_gemm_rejects_bad_arguments(lib):
+    f = lib.fa_head_proj_f32
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    # (n, j, c, groups, x, ldx, xg, w, wg, ldw, bias, bg, y, yg, ldy, stream)
+    args = [i64(16), i32(50), i32(376), i32(2), ctypes.c_void_p(64), i64(100), i64(50),
+            ctypes.c_void_p(128), i64(50 * 376), i64(376), None, i64(0), ctypes.c_void_p(256),
+            i64(16 * 376), i64(376), None]
+    bad = list(args); bad[1] = i32(65)
+    assert f(*bad) == FA_EUNSUPPORTED           # J above 64
+    bad = list(args); bad[5] = i64(10)
+    assert f(*bad) == FA_EINVAL                 # ldx below J
+    bad = list(args); bad[14] = i64(100)
+    assert f(*bad) == FA_EINVAL                 # ldy below C
+    bad = list(args); bad[4] = None
+    assert f(*bad) == FA_EINVAL
+    r = lib.fa_head_reduce_f32
+    # (n, j, c, groups, y, yg, ldy, w, wg, ldw, z, ldz, zg, stream)
+    assert r(i64(16), i32(70), i32(376), i32(2), ctypes.c_void_p(64), i64(0), i64(376),
+             ctypes.c_void_p(128), i64(0), i64(376), ctypes.c_void_p(256), i64(140), i64(70),
+             None) == FA_EUNSUPPORTED
+    w = lib.fa_head_wgrad_f32
+    # (n, j, c, groups, x, ldx, xg, y, yg, ldy, ones, dw, scratch, bytes, stream)
+    assert w(i64(16), i32(50), i32(376), i32(2), ctypes.c_void_p(64), i64(100), i64(50),
+             ctypes.c_void_p(128), i64(16 * 376), i64(376), i32(1), ctypes.c_void_p(256),
+             ctypes.c_void_p(512), ctypes.c_size_t(16), None) == FA_ESCRATCH
 
 
 def test_softmax_rejects_bad_arguments(lib):

@@ -1,12 +1,12 @@
 // Fused epilogue of the temporal attention layer (layers.py:224-237):
-//   u   = r1 + r2                       (the two halves of w_out([agg | h_dst]), bias included)
+//   u   = r1 + r2 + bias                (w_out([agg | h_dst]) from its two halves and bias)
 //   y   = relu(dropout(u))              (counter-hash dropout, multiplier 1/(1-p) or 0)
 //   out = (y - mean(y)) * rstd * gamma + beta,   rstd = 1/sqrt(var(y) + eps)   (LayerNorm)
 // and its backward. One wave per row (grid-stride); lane l holds columns l, l+64, ... of the
 // row (coalesced), so rows up to 64*kMaxPer columns wide are handled in registers. Row sums
 // use the wave reductions of fa_common.hpp. The weight / bias gradients of the LayerNorm
-// are accumulated per wave, combined per workgroup in a fixed order and summed over
-// workgroups by a second kernel (no float atomics).
+// (and of the bias of u) are accumulated per wave, combined per workgroup in a fixed order
+// and summed over workgroups by a second kernel (no float atomics).
 #include "fa_common.hpp"
 
 namespace fa {
@@ -20,6 +20,7 @@ struct EpiParams {
   int d;
   const float* r1; int64_t ld1;
   const float* r2; int64_t ld2;     // may be null
+  const float* bias;                // [d] added to u, may be null
   const float* gamma;
   const float* beta;
   float eps;
@@ -47,6 +48,7 @@ __global__ __launch_bounds__(kBlock) void epilogue_fwd(EpiParams P) {
       if (c < P.d) {
         u = P.r1[r * P.ld1 + c];
         if (P.r2) u += P.r2[r * P.ld2 + c];
+        if (P.bias) u += P.bias[c];
         if (P.drop) u *= drop_mult(P.seed, static_cast<uint64_t>(r * P.d + c), P.p, P.scale);
         u = u > 0.f ? u : 0.f;
       }
@@ -86,19 +88,20 @@ struct EpiBwdParams {
   const float* gamma;
   float scale;                      // dropout multiplier of kept entries (1 without dropout)
   float* du;
-  float* partial;                   // [grid][2][d]: sums of dout*yhat and dout
+  int nsum;                         // 2, or 3 with the bias gradient
+  float* partial;                   // [grid][nsum][d]: sums of dout*yhat, dout (and du)
 };
 
 template <int PER>
 __global__ __launch_bounds__(kBlock) void epilogue_bwd(EpiBwdParams P) {
-  __shared__ float red[kWavesPerBlock][2][kMaxPer * kWave];
+  __shared__ float red[kWavesPerBlock][3][kMaxPer * kWave];
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x / kWave);
   const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   const float inv_d = 1.f / static_cast<float>(P.d);
-  float gg[PER], gb[PER];
+  float gg[PER], gb[PER], gu[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) gg[i] = gb[i] = 0.f;
+  for (int i = 0; i < PER; ++i) gg[i] = gb[i] = gu[i] = 0.f;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; r < P.n; r += total) {
     const float mean = P.stats[2 * r], rstd = P.stats[2 * r + 1];
     float yh[PER], g[PER], yv[PER];
@@ -128,7 +131,9 @@ __global__ __launch_bounds__(kBlock) void epilogue_bwd(EpiBwdParams P) {
       if (c < P.d) {
         const float dyv = rstd * (g[i] - m1 - yh[i] * m2);
         // y = relu(u * mult): dy/du = mult where y > 0, else 0
-        P.du[r * P.d + c] = yv[i] > 0.f ? dyv * P.scale : 0.f;
+        const float du = yv[i] > 0.f ? dyv * P.scale : 0.f;
+        P.du[r * P.d + c] = du;
+        gu[i] += du;
       }
     }
   }
@@ -136,29 +141,33 @@ __global__ __launch_bounds__(kBlock) void epilogue_bwd(EpiBwdParams P) {
   for (int i = 0; i < PER; ++i) {
     red[wave][0][lane + i * kWave] = gg[i];
     red[wave][1][lane + i * kWave] = gb[i];
+    red[wave][2][lane + i * kWave] = gu[i];
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 2 * P.d; idx += kBlock) {
+  for (int idx = threadIdx.x; idx < P.nsum * P.d; idx += kBlock) {
     const int which = idx / P.d;
     const int c = idx - which * P.d;
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < kWavesPerBlock; ++w) s += red[w][which][c];
-    P.partial[(static_cast<int64_t>(blockIdx.x) * 2 + which) * P.d + c] = s;
+    P.partial[(static_cast<int64_t>(blockIdx.x) * P.nsum + which) * P.d + c] = s;
   }
 }
 
-// out[which][c] = sum over rows r of partial[r][which][c]: one wave per output, fixed order.
+// out_which[c] = sum over rows r of partial[r][which][c] (which < nsum): one wave per
+// output, fixed order.
 __global__ __launch_bounds__(kBlock) void column_sums(const float* partial, int rows, int d,
-                                                     float* out0, float* out1) {
+                                                     int nsum, float* out0, float* out1,
+                                                     float* out2) {
   const int o = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
-  if (o >= 2 * d) return;
+  if (o >= nsum * d) return;
   const int which = o / d;
   const int c = o - which * d;
   float s = 0.f;
-  for (int r = lane_id(); r < rows; r += kWave) s += partial[(static_cast<int64_t>(r) * 2 + which) * d + c];
+  for (int r = lane_id(); r < rows; r += kWave)
+    s += partial[(static_cast<int64_t>(r) * nsum + which) * d + c];
   s = wave_sum(s);
-  if (lane_id() == 0) (which == 0 ? out0 : out1)[c] = s;
+  if (lane_id() == 0) (which == 0 ? out0 : (which == 1 ? out1 : out2))[c] = s;
 }
 
 int epi_grid(int64_t n) {
@@ -172,15 +181,16 @@ int epi_grid(int64_t n) {
 using namespace fa;
 
 extern "C" int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, int64_t ld1,
-                                        const float* r2, int64_t ld2, const float* gamma,
-                                        const float* beta, float eps, uint64_t drop_seed,
-                                        float drop_p, float* out, float* y, float* stats,
-                                        hipStream_t stream) {
+                                        const float* r2, int64_t ld2, const float* bias,
+                                        const float* gamma, const float* beta, float eps,
+                                        uint64_t drop_seed, float drop_p, float* out, float* y,
+                                        float* stats, hipStream_t stream) {
   if (n < 0 || d <= 0 || d > kMaxPer * kWave || !(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
   if (n == 0) return FA_OK;
   if (!r1 || ld1 < d || (r2 && ld2 < d) || !gamma || !beta || !out || !y || !stats) return FA_EINVAL;
   EpiParams P;
-  P.n = n; P.d = d; P.r1 = r1; P.ld1 = ld1; P.r2 = r2; P.ld2 = ld2; P.gamma = gamma; P.beta = beta;
+  P.n = n; P.d = d; P.r1 = r1; P.ld1 = ld1; P.r2 = r2; P.ld2 = ld2; P.bias = bias;
+  P.gamma = gamma; P.beta = beta;
   P.eps = eps; P.drop = drop_p > 0.f; P.seed = drop_seed; P.p = drop_p;
   P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
   P.out = out; P.y = y; P.stats = stats;
@@ -196,18 +206,20 @@ extern "C" int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, i
 
 extern "C" size_t fa_tgat_epilogue_bwd_scratch_bytes(int64_t n, int32_t d) {
   if (n <= 0 || d <= 0) return 0;
-  return static_cast<size_t>(epi_grid(n)) * 2 * static_cast<size_t>(d) * sizeof(float);
+  return static_cast<size_t>(epi_grid(n)) * 3 * static_cast<size_t>(d) * sizeof(float);
 }
 
 extern "C" int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const float* y,
                                         const float* stats, const float* gamma, float drop_p,
-                                        float* du, float* dgamma, float* dbeta, void* scratch,
-                                        size_t scratch_bytes, hipStream_t stream) {
+                                        float* du, float* dgamma, float* dbeta, float* dbias,
+                                        void* scratch, size_t scratch_bytes, hipStream_t stream) {
   if (n < 0 || d <= 0 || d > kMaxPer * kWave || !(drop_p >= 0.f && drop_p < 1.f)) return FA_EINVAL;
   if (!dgamma || !dbeta || !gamma) return FA_EINVAL;
+  const int nsum = dbias ? 3 : 2;
   if (n == 0) {
-    hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(2 * d, kWavesPerBlock))),
-                       dim3(kBlock), 0, stream, static_cast<const float*>(nullptr), 0, d, dgamma, dbeta);
+    hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(nsum * d, kWavesPerBlock))),
+                       dim3(kBlock), 0, stream, static_cast<const float*>(nullptr), 0, d, nsum,
+                       dgamma, dbeta, dbias);
     return launch_status();
   }
   if (!dout || !y || !stats || !du) return FA_EINVAL;
@@ -215,7 +227,7 @@ extern "C" int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout,
   EpiBwdParams P;
   P.n = n; P.d = d; P.dout = dout; P.y = y; P.stats = stats; P.gamma = gamma;
   P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
-  P.du = du; P.partial = static_cast<float*>(scratch);
+  P.du = du; P.nsum = nsum; P.partial = static_cast<float*>(scratch);
   const int grid = epi_grid(n);
   switch (static_cast<int>(ceil_div(d, kWave))) {
     case 1: hipLaunchKernelGGL(epilogue_bwd<1>, dim3(grid), dim3(kBlock), 0, stream, P); break;
@@ -223,8 +235,8 @@ extern "C" int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout,
     case 3: hipLaunchKernelGGL(epilogue_bwd<3>, dim3(grid), dim3(kBlock), 0, stream, P); break;
     default: hipLaunchKernelGGL(epilogue_bwd<4>, dim3(grid), dim3(kBlock), 0, stream, P); break;
   }
-  hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(2 * d, kWavesPerBlock))),
-                     dim3(kBlock), 0, stream, static_cast<const float*>(P.partial), grid, d, dgamma,
-                     dbeta);
+  hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(nsum * d, kWavesPerBlock))),
+                     dim3(kBlock), 0, stream, static_cast<const float*>(P.partial), grid, d, nsum,
+                     dgamma, dbeta, dbias);
   return launch_status();
 }

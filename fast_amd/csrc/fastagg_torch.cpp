@@ -724,8 +724,9 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
 
 // -> [out [n, d], y [n, d], stats [n, 2]]
 std::vector<at::Tensor> tgat_epilogue_fwd(at::Tensor r1, std::optional<at::Tensor> r2,
-                                          at::Tensor gamma, at::Tensor beta, double eps,
-                                          uint64_t drop_seed, double drop_p) {
+                                          std::optional<at::Tensor> bias, at::Tensor gamma,
+                                          at::Tensor beta, double eps, uint64_t drop_seed,
+                                          double drop_p) {
   CHECK_CUDA(r1);
   CHECK_DTYPE(r1, at::kFloat);
   TORCH_CHECK(r1.dim() == 2 && r1.stride(1) == 1, "r1 must be a row-major [n, d] matrix");
@@ -743,12 +744,19 @@ std::vector<at::Tensor> tgat_epilogue_fwd(at::Tensor r1, std::optional<at::Tenso
   CHECK_INPUT(gamma);
   CHECK_INPUT(beta);
   TORCH_CHECK(gamma.numel() == d && beta.numel() == d, "gamma / beta must have d entries");
+  const float* bp = nullptr;
+  if (bias.has_value()) {
+    CHECK_INPUT((*bias));
+    CHECK_DTYPE((*bias), at::kFloat);
+    TORCH_CHECK(bias->numel() == d, "bias must have d entries");
+    bp = bias->data_ptr<float>();
+  }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(r1.device());
   auto out = at::empty({n, d}, r1.options());
   auto y = at::empty({n, d}, r1.options());
   auto stats = at::empty({n, 2}, r1.options());
   const int st = fa_tgat_epilogue_fwd_f32(n, static_cast<int32_t>(d), r1.data_ptr<float>(),
-                                          r1.stride(0), r2p, ld2, gamma.data_ptr<float>(),
+                                          r1.stride(0), r2p, ld2, bp, gamma.data_ptr<float>(),
                                           beta.data_ptr<float>(), static_cast<float>(eps),
                                           drop_seed, static_cast<float>(drop_p),
                                           out.data_ptr<float>(), y.data_ptr<float>(),
@@ -757,9 +765,9 @@ std::vector<at::Tensor> tgat_epilogue_fwd(at::Tensor r1, std::optional<at::Tenso
   return {out, y, stats};
 }
 
-// -> [du [n, d], dgamma [d], dbeta [d]]
+// -> [du [n, d], dgamma [d], dbeta [d], dbias [d] (empty unless need_dbias)]
 std::vector<at::Tensor> tgat_epilogue_bwd(at::Tensor dout, at::Tensor y, at::Tensor stats,
-                                          at::Tensor gamma, double drop_p) {
+                                          at::Tensor gamma, double drop_p, bool need_dbias) {
   CHECK_INPUT(dout);
   CHECK_INPUT(y);
   CHECK_INPUT(stats);
@@ -771,16 +779,19 @@ std::vector<at::Tensor> tgat_epilogue_bwd(at::Tensor dout, at::Tensor y, at::Ten
   auto du = at::empty({n, d}, y.options());
   auto dgamma = at::empty({d}, y.options());
   auto dbeta = at::empty({d}, y.options());
+  at::Tensor dbias;
+  if (need_dbias) dbias = at::empty({d}, y.options());
   const size_t sb = fa_tgat_epilogue_bwd_scratch_bytes(n, static_cast<int32_t>(d));
   auto scratch = at::empty({static_cast<int64_t>(sb > 0 ? sb : 1)}, y.options().dtype(at::kByte));
   const int st = fa_tgat_epilogue_bwd_f32(n, static_cast<int32_t>(d), dout.data_ptr<float>(),
                                           y.data_ptr<float>(), stats.data_ptr<float>(),
                                           gamma.data_ptr<float>(), static_cast<float>(drop_p),
                                           du.data_ptr<float>(), dgamma.data_ptr<float>(),
-                                          dbeta.data_ptr<float>(), scratch.data_ptr(), sb,
-                                          stream_of(y));
+                                          dbeta.data_ptr<float>(),
+                                          need_dbias ? dbias.data_ptr<float>() : nullptr,
+                                          scratch.data_ptr(), sb, stream_of(y));
   check_status(st, "tgat_epilogue_bwd");
-  return {du, dgamma, dbeta};
+  return {du, dgamma, dbeta, dbias};
 }
 
 // ----- per-head projections --------------------------------------------------------
@@ -950,10 +961,11 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("y"), py::arg("w"));
   m.def("head_wgrad", &head_wgrad, "per-head weight gradient x[:, g-block]^T @ y[g]",
         py::arg("x"), py::arg("y"), py::arg("groups"), py::arg("ones") = false);
-  m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2)))",
-        py::arg("r1"), py::arg("r2"), py::arg("gamma"), py::arg("beta"), py::arg("eps"),
-        py::arg("drop_seed"), py::arg("drop_p"));
+  m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2 + bias)))",
+        py::arg("r1"), py::arg("r2"), py::arg("bias"), py::arg("gamma"), py::arg("beta"),
+        py::arg("eps"), py::arg("drop_seed"), py::arg("drop_p"));
   m.def("tgat_epilogue_bwd", &tgat_epilogue_bwd, "backward of tgat_epilogue_fwd", py::arg("dout"),
-        py::arg("y"), py::arg("stats"), py::arg("gamma"), py::arg("drop_p"));
+        py::arg("y"), py::arg("stats"), py::arg("gamma"), py::arg("drop_p"),
+        py::arg("need_dbias") = false);
   m.attr("abi_version") = fa_abi_version();
 }

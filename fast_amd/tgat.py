@@ -322,40 +322,6 @@ class TgatAttention(torch.autograd.Function):
         return dqt, d_tw, d_tb, d_src, None, None, None, None, None
 
 
-def _rows_t_mm(a: torch.Tensor, b: torch.Tensor, chunk: int = 2048) -> torch.Tensor:
-    """a^T b for tall a [n, p], b [n, q], split over row chunks (one batched product
-    plus a sum) so that the reduction over n spreads over many workgroups."""
-    n = a.shape[0]
-    s = n // chunk
-    if s < 2:
-        return a.t() @ b
-    m = s * chunk
-    out = torch.bmm(a[:m].reshape(s, chunk, a.shape[1]).transpose(1, 2),
-                    b[:m].reshape(s, chunk, b.shape[1])).sum(0)
-    if m < n:
-        out = out + a[m:].t() @ b[m:]
-    return out
-
-
-class RowLinear(torch.autograd.Function):
-    """y = x W^T + b for x with many rows; the weight gradient is a split-row reduction."""
-
-    @staticmethod
-    def forward(ctx, x, W, b):
-        ctx.save_for_backward(x, W)
-        ctx.has_b = b is not None
-        return F.linear(x, W, b)
-
-    @staticmethod
-    def backward(ctx, dy):
-        x, W = ctx.saved_tensors
-        dy = dy.contiguous()
-        dx = dy @ W if ctx.needs_input_grad[0] else None
-        dW = _rows_t_mm(dy, x) if ctx.needs_input_grad[1] else None
-        db = dy.sum(0) if ctx.has_b and ctx.needs_input_grad[2] else None
-        return dx, dW, db
-
-
 class HeadProj(torch.autograd.Function):
     """y[g] = x[:, g*J:(g+1)*J] @ w[g] (+ bias[g]) for x [N, G*J], w [G, J, C] -> [G, N, C]."""
 
@@ -396,23 +362,80 @@ class HeadReduce(torch.autograd.Function):
 
 
 class TgatEpilogue(torch.autograd.Function):
-    """LayerNorm(ReLU(dropout(r1 + r2))) in one kernel each way (layers.py:235-236); the
-    dropout is the counter hash of (seed, row*d + col), as fastAgg.dropout_mask."""
+    """LayerNorm(ReLU(dropout(r1 + r2 + bias))) in one kernel each way (layers.py:235-236);
+    the dropout is the counter hash of (seed, row*d + col), as fastAgg.dropout_mask."""
 
     @staticmethod
-    def forward(ctx, r1, r2, gamma, beta, eps: float, seed: int, p: float):
-        out, y, stats = fastAgg.tgat_epilogue_fwd(r1, r2, gamma, beta, float(eps), int(seed),
-                                                  float(p))
+    def forward(ctx, r1, r2, bias, gamma, beta, eps: float, seed: int, p: float):
+        out, y, stats = fastAgg.tgat_epilogue_fwd(r1, r2, bias, gamma, beta, float(eps),
+                                                  int(seed), float(p))
         ctx.save_for_backward(y, stats, gamma)
         ctx.p = float(p)
         ctx.has_r2 = r2 is not None
+        ctx.has_bias = bias is not None
         return out
 
     @staticmethod
     def backward(ctx, dout):
         y, stats, gamma = ctx.saved_tensors
-        du, dgamma, dbeta = fastAgg.tgat_epilogue_bwd(dout.contiguous(), y, stats, gamma, ctx.p)
-        return du, (du if ctx.has_r2 else None), dgamma, dbeta, None, None, None
+        du, dgamma, dbeta, dbias = fastAgg.tgat_epilogue_bwd(dout.contiguous(), y, stats, gamma,
+                                                             ctx.p, ctx.has_bias)
+        return (du, (du if ctx.has_r2 else None), (dbias if ctx.has_bias else None), dgamma,
+                dbeta, None, None, None)
+
+
+class RowsMM(torch.autograd.Function):
+    """y = x W^T for x [N, K] with many rows and a small W [M, K] (no bias). The weight
+    gradient x^T dy is the split-row reduction of fastAgg.head_wgrad (deterministic)."""
+
+    @staticmethod
+    def forward(ctx, x, W):
+        ctx.save_for_backward(x, W)
+        return x @ W.t()
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, W = ctx.saved_tensors
+        dy = dy.contiguous()
+        dx = dy @ W if ctx.needs_input_grad[0] else None
+        dW = None
+        if ctx.needs_input_grad[1]:
+            dW = fastAgg.head_wgrad(x, dy.unsqueeze(0), 1, False)[0].t()
+        return dx, dW
+
+
+class DstProj(torch.autograd.Function):
+    """The two products of the destination features in one GEMM:
+    [q | r] = h [Wq | Wr]^T for h [N, K], Wq [Mq, K], Wr [Mr, K] (the query projection and
+    the h_dst half of w_out), returned as two column blocks of one [N, Mq+Mr] array."""
+
+    @staticmethod
+    def forward(ctx, h, Wq, Wr):
+        ctx.save_for_backward(h, Wq, Wr)
+        t = h @ torch.cat([Wq, Wr], 0).t()
+        mq = Wq.shape[0]
+        return t[:, :mq], t[:, mq:]
+
+    @staticmethod
+    def backward(ctx, dq, dr):
+        h, Wq, Wr = ctx.saved_tensors
+        dh = dWq = dWr = None
+        if dq is not None:
+            dq = dq.contiguous()
+        if dr is not None:
+            dr = dr.contiguous()
+        if ctx.needs_input_grad[0]:
+            if dq is not None:
+                dh = dq @ Wq
+                if dr is not None:
+                    dh.addmm_(dr, Wr)
+            elif dr is not None:
+                dh = dr @ Wr
+        if ctx.needs_input_grad[1] and dq is not None:
+            dWq = fastAgg.head_wgrad(h, dq.unsqueeze(0), 1, False)[0].t()
+        if ctx.needs_input_grad[2] and dr is not None:
+            dWr = fastAgg.head_wgrad(h, dr.unsqueeze(0), 1, False)[0].t()
+        return dh, dWq, dWr
 
 
 # ---------------------------------------------------------------------------------------
@@ -488,9 +511,14 @@ class TransfomerAttentionLayer(torch.nn.Module):
         kp = kspace_width(Dn, De, Dt)
         # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h].
         wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
+        Wo = self.w_out.weight
+        r2 = None
         if Dn > 0:
-            q = RowLinear.apply(hdst, self.w_q.weight[:, :Dn], self._query_bias())
-            qt = HeadProj.apply(q, wk, None)
+            # q = hdst W_q[:, :Dn]^T (its bias folded into qt's: qb[h] W_k,aug[h]) and the
+            # h_dst half of w_out, from one product
+            q, r2 = DstProj.apply(hdst, self.w_q.weight[:, :Dn], Wo[:, D:])
+            qbk = torch.bmm(self._query_bias().view(H, 1, dh), wk).view(H, kp)
+            qt = HeadProj.apply(q, wk, qbk)
         else:  # one query for every destination: the time part alone (or 1, layers.py:137-140)
             q1 = self._query_bias() if Dt > 0 else torch.ones(D, device=dev)
             qt = HeadProj.apply(q1.view(1, D), wk, None).expand(H, N, kp)
@@ -515,18 +543,14 @@ class TransfomerAttentionLayer(torch.nn.Module):
                                    drop_p)
 
         # Absorbed values, head by head: agg[v, h, :] = W_v,aug[h] xbar[h, v, :], then
-        # rst = w_out([agg | hdst]) as agg W_o[:, :D]^T + hdst W_o[:, D:]^T + b_o.
+        # rst = w_out([agg | hdst]) as agg W_o[:, :D]^T + hdst W_o[:, D:]^T + b_o (the
+        # bias and the sum in the epilogue kernel).
         wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
         agg = HeadReduce.apply(xbar, wv)
-        Wo = self.w_out.weight
-        if Dn > 0:
-            r1 = RowLinear.apply(agg, Wo[:, :D], None)
-            r2 = RowLinear.apply(hdst, Wo[:, D:], self.w_out.bias)
-        else:
-            r1 = RowLinear.apply(agg, Wo, self.w_out.bias)
-            r2 = None
+        r1 = RowsMM.apply(agg, Wo[:, :D])
         ln = self.layer_norm
-        return TgatEpilogue.apply(r1, r2, ln.weight, ln.bias, ln.eps, out_drop_seed, out_drop_p)
+        return TgatEpilogue.apply(r1, r2, self.w_out.bias, ln.weight, ln.bias, ln.eps,
+                                  out_drop_seed, out_drop_p)
 
 
 class TGATEncoder(torch.nn.Module):

@@ -284,23 +284,25 @@ int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const flo
  * ------------------------------------------------------------------------------- */
 
 /* For each row r < n of width d (d <= 256):
- *   u = r1[r] + r2[r] (r2 may be NULL), y = relu(u * m), m = the hashed dropout
- *   multiplier of entry r*d + c (1/(1-p) or 0, as fa_dropout_mask_f32 with drop_seed;
- *   m = 1 when drop_p = 0), out = (y - mean) * rstd * gamma + beta with
+ *   u = r1[r] + r2[r] + bias (r2, bias may be NULL), y = relu(u * m), m = the hashed
+ *   dropout multiplier of entry r*d + c (1/(1-p) or 0, as fa_dropout_mask_f32 with
+ *   drop_seed; m = 1 when drop_p = 0), out = (y - mean) * rstd * gamma + beta with
  *   rstd = 1/sqrt(var + eps) (biased variance over the row).
  * Saves y [n][d] and stats [n][2] = (mean, rstd) for the backward. */
 int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, int64_t ld1,
-                             const float* r2, int64_t ld2, const float* gamma,
-                             const float* beta, float eps, uint64_t drop_seed, float drop_p,
-                             float* out, float* y, float* stats, hipStream_t stream);
-/* Gradients of fa_tgat_epilogue_fwd_f32 from dout [n][d]: du [n][d] (the gradient of both r1
- * and r2), dgamma [d], dbeta [d] (deterministic two-pass sums).
+                             const float* r2, int64_t ld2, const float* bias,
+                             const float* gamma, const float* beta, float eps,
+                             uint64_t drop_seed, float drop_p, float* out, float* y,
+                             float* stats, hipStream_t stream);
+/* Gradients of fa_tgat_epilogue_fwd_f32 from dout [n][d]: du [n][d] (the gradient of r1, r2
+ * and each row of bias), dgamma [d], dbeta [d] and, when dbias is not NULL,
+ * dbias [d] = sum over rows of du (deterministic two-pass sums).
  * scratch: fa_tgat_epilogue_bwd_scratch_bytes(n, d). */
 size_t fa_tgat_epilogue_bwd_scratch_bytes(int64_t n, int32_t d);
 int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const float* y,
                              const float* stats, const float* gamma, float drop_p, float* du,
-                             float* dgamma, float* dbeta, void* scratch, size_t scratch_bytes,
-                             hipStream_t stream);
+                             float* dgamma, float* dbeta, float* dbias, void* scratch,
+                             size_t scratch_bytes, hipStream_t stream);
 
 /* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
 int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,

@@ -75,12 +75,12 @@ def test_layer_time_bias_and_dropout(dev):
                  p_out=0.1)
 
 
-@pytest.mark.parametrize("n,d,p,two", [(1000, 100, 0.0, True), (777, 100, 0.3, True),
-                                       (300, 256, 0.1, False), (5, 7, 0.0, True), (0, 100, 0.1, True),
-                                       (4096, 64, 0.2, False)])
-def test_epilogue_matches_torch(dev, n, d, p, two):
-    """LayerNorm(ReLU(dropout(r1 + r2))) fused kernel vs float64 torch with the same hashed
-    multipliers, forward and all gradients."""
+@pytest.mark.parametrize("n,d,p,two,bias", [(1000, 100, 0.0, True, True), (777, 100, 0.3, True, False),
+                                            (300, 256, 0.1, False, True), (5, 7, 0.0, True, True),
+                                            (0, 100, 0.1, True, True), (4096, 64, 0.2, False, False)])
+def test_epilogue_matches_torch(dev, n, d, p, two, bias):
+    """LayerNorm(ReLU(dropout(r1 + r2 + bias))) fused kernel vs float64 torch with the same
+    hashed multipliers, forward and all gradients."""
     import fast_amd
     from fast_amd.tgat import TgatEpilogue
     from oracle.ref_cpu import C
@@ -88,25 +88,30 @@ def test_epilogue_matches_torch(dev, n, d, p, two):
     g = torch.Generator().manual_seed(n + d)
     r1 = torch.randn(n, d, generator=g)
     r2 = torch.randn(n, d, generator=g) if two else None
+    b = torch.randn(d, generator=g) if bias else None
     gamma = 1 + 0.1 * torch.randn(d, generator=g)
     beta = 0.1 * torch.randn(d, generator=g)
     dout = torch.randn(n, d, generator=g)
     seed, eps = 4242, 1e-5
-    leaves = [t.to(dev).requires_grad_(True) if t is not None else None for t in (r1, r2, gamma, beta)]
-    out = TgatEpilogue.apply(leaves[0], leaves[1], leaves[2], leaves[3], eps, seed, p)
+    leaves = [t.to(dev).requires_grad_(True) if t is not None else None
+              for t in (r1, r2, b, gamma, beta)]
+    out = TgatEpilogue.apply(leaves[0], leaves[1], leaves[2], leaves[3], leaves[4], eps, seed, p)
     out.backward(dout.to(dev))
-    ref_leaves = [t.double().requires_grad_(True) if t is not None else None for t in (r1, r2, gamma, beta)]
-    u = ref_leaves[0] + (ref_leaves[1] if two else 0)
+    ref_leaves = [t.double().requires_grad_(True) if t is not None else None
+                  for t in (r1, r2, b, gamma, beta)]
+    u = ref_leaves[0] + (ref_leaves[1] if two else 0) + (ref_leaves[2] if bias else 0)
     if p > 0:
         u = u * torch.from_numpy(C.dropout_mask(n, d, seed, p)).double()
-    ref = torch.nn.functional.layer_norm(torch.relu(u), (d,), ref_leaves[2], ref_leaves[3], eps)
+    ref = torch.nn.functional.layer_norm(torch.relu(u), (d,), ref_leaves[3], ref_leaves[4], eps)
     ref.backward(dout.double())
     if n == 0:
         assert out.shape == (0, d)
-        assert torch.count_nonzero(leaves[2].grad) == 0
+        assert torch.count_nonzero(leaves[3].grad) == 0
+        if bias:
+            assert torch.count_nonzero(leaves[2].grad) == 0
         return
     assert_rel(out, ref, FP32_TOL, "epilogue out")
-    for got, want, name in zip(leaves, ref_leaves, ("r1", "r2", "gamma", "beta")):
+    for got, want, name in zip(leaves, ref_leaves, ("r1", "r2", "bias", "gamma", "beta")):
         if got is not None:
             assert_rel(got.grad, want.grad, FP32_TOL, f"epilogue grad {name}")
     assert fast_amd.fastAgg is not None

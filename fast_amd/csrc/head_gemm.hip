@@ -350,12 +350,13 @@ constexpr int kWgradStage = FA_WGRAD_STAGE;  // 16-row blocks per LDS stage
 // t of the wave stands for the columns cw + 4m + t (m < 16), so the four B values of a
 // lane in a k-step are one float4, Y[row][cw + 4*(l%16) .. +3]. The next block's X and Y
 // are loaded while the current one is multiplied.
-template <int NJT, bool VEC>
-__global__ __launch_bounds__(kBlock) void head_wgrad(WgradParams P) {
+template <int NJT, bool VEC, int NW>
+__global__ __launch_bounds__(NW * kWave) void head_wgrad(WgradParams P) {
   constexpr int XW = 65;
+  constexpr int NT = NW * kWave;               // threads of the workgroup
   constexpr int SR = 16 * kWgradStage;         // rows per stage
   constexpr int KK = SR / 4;                   // k-steps per stage
-  constexpr int XE = SR * 64 / kBlock;         // X elements per thread and stage
+  constexpr int XE = (SR * 64 + NT - 1) / NT;  // X elements per thread and stage
   __shared__ float xs[2][SR][XW];
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(kBlock) void head_wgrad(WgradParams P) {
   const int g = blockIdx.y / per_g;
   const int rem = blockIdx.y - g * per_g;
   const int jg = rem / P.ncw4;
-  const int cw = ((rem - jg * P.ncw4) * kWavesPerBlock + wave) * kWcols;
+  const int cw = ((rem - jg * P.ncw4) * NW + wave) * kWcols;
   const bool active = cw < P.c;
   const int j0 = jg * 64;
   const int li = lane & 15, lk = lane >> 4;
@@ -372,15 +373,16 @@ __global__ __launch_bounds__(kBlock) void head_wgrad(WgradParams P) {
   const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
   const float* xbase = P.x + g * P.xg;
   const float* ybase = P.y + g * P.yg;
-  // X elements of this thread: e = tid + kBlock*i of the SR x 64 stage (row e/64, col e%64)
+  // X elements of this thread: e = tid + NT*i of the SR x 64 stage (row e/64, col e%64)
   int xr[XE], xj[XE];
   uint32_t xo[XE];
 #pragma unroll
   for (int i = 0; i < XE; ++i) {
-    const int e = tid + kBlock * i;
-    xr[i] = e >> 6;
+    const int e = tid + NT * i;
+    const bool ok = e < SR * 64;
+    xr[i] = ok ? e >> 6 : SR;                  // row SR: no element
     xj[i] = j0 + (e & 63);
-    xo[i] = xj[i] < P.j ? 4u * static_cast<uint32_t>(xr[i] * P.ldx + xj[i]) : kOob;
+    xo[i] = (ok && xj[i] < P.j) ? 4u * static_cast<uint32_t>(xr[i] * P.ldx + xj[i]) : kOob;
   }
   const int cl = cw + 4 * li;                  // first of this lane's four B columns
   const uint32_t yo = (active && cl < P.c) ? 4u * static_cast<uint32_t>(lk * P.ldy + cl) : kOob;
@@ -399,6 +401,7 @@ __global__ __launch_bounds__(kBlock) void head_wgrad(WgradParams P) {
   auto xstore = [&](int b, int64_t nb) {
 #pragma unroll
     for (int i = 0; i < XE; ++i) {
+      if (xr[i] >= SR) continue;
       float v = xv[i];
       if (xj[i] >= P.j) v = (xj[i] < P.jr && nb + xr[i] < r1) ? 1.f : 0.f;
       xs[b][xr[i]][xj[i] - j0] = v;
@@ -515,19 +518,28 @@ int row_grid(int64_t n, int per_tile_groups, const void* kernel) {
   return static_cast<int>(g < 1 ? 1 : g);
 }
 
-// Chunks of the wgrad reduction: about kGemmBlocks workgroups in all, at least 64 rows each.
-int64_t wgrad_chunks(int64_t n, int groups) {
-  int64_t chunks = kGemmBlocks / (groups > 0 ? groups : 1);
+constexpr int kWgradWaves = 3072;  // waves of a wgrad launch (about 3 per SIMD)
+
+// Chunks of the wgrad reduction: about kWgradWaves waves in all, at least 64 rows each.
+int64_t wgrad_chunks(int64_t n, int groups, int waves_per_group) {
+  int64_t chunks = kWgradWaves / ((groups > 0 ? groups : 1) * waves_per_group);
   if (chunks < 1) chunks = 1;
   const int64_t by_rows = ceil_div(n, 64);
   return chunks < by_rows ? chunks : (by_rows < 1 ? 1 : by_rows);
 }
 
-// Workgroup rows of a wgrad launch: groups x 64-row j groups x column quads.
+// Waves per wgrad workgroup: the 64-column waves a head needs, shared out evenly over at
+// most 4 per workgroup (no idle waves for C = 100, 376, 708, ...).
+int wgrad_waves(int c) {
+  const int ncw = static_cast<int>(ceil_div(c, kWcols));
+  return static_cast<int>(ceil_div(ncw, ceil_div(ncw, kWavesPerBlock)));
+}
+
+// Workgroup rows of a wgrad launch: groups x 64-row j groups x column workgroups.
 int wgrad_groups(int j, int c, int groups, int ones) {
   const int jr = j + (ones ? 1 : 0);
-  const int ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), kWavesPerBlock));
-  return groups * static_cast<int>(ceil_div(jr, 64)) * ncw4;
+  const int ncwg = static_cast<int>(ceil_div(ceil_div(c, kWcols), wgrad_waves(c)));
+  return groups * static_cast<int>(ceil_div(jr, 64)) * ncwg;
 }
 
 void launch_proj(void (*k)(ProjParams), int64_t n, int gy, const ProjParams& P,
@@ -622,7 +634,7 @@ extern "C" size_t fa_head_wgrad_scratch_bytes(int64_t n, int32_t j, int32_t c, i
   if (n <= 0 || j <= 0 || c <= 0 || groups <= 0) return 0;
   const int jr = j + (ones ? 1 : 0);
   const int gy = wgrad_groups(j, c, groups, ones);
-  return static_cast<size_t>(wgrad_chunks(n, gy)) * groups * jr * c * sizeof(float);
+  return static_cast<size_t>(wgrad_chunks(n, gy, wgrad_waves(c))) * groups * jr * c * sizeof(float);
 }
 
 extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
@@ -642,10 +654,11 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.n = n; P.j = j; P.c = c; P.g = groups; P.jr = jr;
   P.x = x; P.ldx = ldx; P.xg = xg; P.y = y; P.yg = yg; P.ldy = ldy;
   P.vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
-  P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), kWavesPerBlock));
+  const int nw = wgrad_waves(c);
+  P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), nw));
   P.njg = static_cast<int>(ceil_div(jr, 64));
   const int gy = wgrad_groups(j, c, groups, ones);
-  const int64_t chunks = wgrad_chunks(n, gy);
+  const int64_t chunks = wgrad_chunks(n, gy, nw);
   P.rows = round_up(ceil_div(n, chunks), 16 * kWgradStage);
   // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
   if ((P.rows + 64) * (ldx > ldy ? ldx : ldy) * 4 >= static_cast<int64_t>(kOob)) return FA_EUNSUPPORTED;
@@ -655,13 +668,15 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.part = static_cast<float*>(scratch);
   const dim3 grid(static_cast<unsigned>(used), static_cast<unsigned>(gy));
   void (*k)(WgradParams) = nullptr;
-  switch (P.njg > 1 ? 4 : static_cast<int>(ceil_div(jr, 16))) {
-    case 1: k = P.vec ? head_wgrad<1, true> : head_wgrad<1, false>; break;
-    case 2: k = P.vec ? head_wgrad<2, true> : head_wgrad<2, false>; break;
-    case 3: k = P.vec ? head_wgrad<3, true> : head_wgrad<3, false>; break;
-    default: k = P.vec ? head_wgrad<4, true> : head_wgrad<4, false>; break;
-  }
-  hipLaunchKernelGGL(k, grid, dim3(kBlock), 0, stream, P);
+  const int njt = P.njg > 1 ? 4 : static_cast<int>(ceil_div(jr, 16));
+#define FA_WG_NW(NJ, NWV)                                                                \
+  if (njt == NJ && nw == NWV) k = P.vec ? head_wgrad<NJ, true, NWV> : head_wgrad<NJ, false, NWV>;
+#define FA_WG(NJ) FA_WG_NW(NJ, 1) FA_WG_NW(NJ, 2) FA_WG_NW(NJ, 3) FA_WG_NW(NJ, 4)
+  FA_WG(1) FA_WG(2) FA_WG(3) FA_WG(4)
+#undef FA_WG
+#undef FA_WG_NW
+  if (!k) return FA_EUNSUPPORTED;
+  hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(nw * kWave)), 0, stream, P);
   hipLaunchKernelGGL(chunk_sums, dim3(static_cast<unsigned>(ceil_div(out, 32))), dim3(kBlock), 0,
                      stream, static_cast<const float*>(P.part), static_cast<int>(used), out, dw);
   return launch_status();

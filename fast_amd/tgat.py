@@ -164,21 +164,48 @@ def kspace_width(dn: int, de: int, dt: int) -> int:
     return int(fastAgg.tgat_kspace(dn, de, dt))
 
 
+_KSPACE_COLS: dict = {}
+
+
+def kspace_columns(dn: int, de: int, dt: int, device) -> torch.Tensor:
+    """Column of the K-space layout that holds each of the dn+de+dt input columns (node,
+    edge and time parts each padded to a multiple of 4); cached per shape and device."""
+    key = (dn, de, dt, str(device))
+    cols = _KSPACE_COLS.get(key)
+    if cols is None:
+        idx, off = [], 0
+        for d in (dn, de, dt):
+            idx.extend(range(off, off + d))
+            off += d + (-d) % 4
+        cols = torch.tensor(idx, dtype=torch.long, device=device)
+        _KSPACE_COLS[key] = cols
+    return cols
+
+
+class _ToKspace(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, W, b, dn, de, dt):
+        kp = kspace_width(dn, de, dt)
+        cols = kspace_columns(dn, de, dt, W.device)
+        kb = 4 * ((dn + 3) // 4 + (de + 3) // 4 + (dt + 3) // 4)
+        out = W.new_zeros(W.shape[0], kp)
+        out.index_copy_(1, cols, W)
+        out[:, kb] = b
+        ctx.cols, ctx.kb = cols, kb
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        dW = dout.index_select(1, ctx.cols) if ctx.needs_input_grad[0] else None
+        db = dout[:, ctx.kb].contiguous() if ctx.needs_input_grad[1] else None
+        return dW, db, None, None, None
+
+
 def to_kspace(W: torch.Tensor, b: torch.Tensor, dn: int, de: int, dt: int) -> torch.Tensor:
     """[D, dn+de+dt] weight and [D] bias -> [D, Kp] with each part padded to a multiple of
-    4 columns, the bias at column Kb and zeros after it (the layout the kernels use)."""
-    pieces = []
-    off = 0
-    for d in (dn, de, dt):
-        if d:
-            pieces.append(W[:, off:off + d])
-            off += d
-        pad = (-d) % 4
-        if pad:
-            pieces.append(W.new_zeros(W.shape[0], pad))
-    pieces.append(b[:, None])
-    pieces.append(W.new_zeros(W.shape[0], 3))
-    return torch.cat(pieces, dim=1)
+    4 columns, the bias at column Kb and zeros after it (the layout the kernels use). One
+    scatter forward and one gather backward."""
+    return _ToKspace.apply(W, b, dn, de, dt)
 
 
 def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, heads: int,
@@ -299,7 +326,8 @@ class TgatAttention(torch.autograd.Function):
         drop = saved[7] if ctx.has_drop else None
         g = ctx.g
         need_node = ctx.needs_input_grad[3] and node_src.shape[1] > 0
-        dxbar = dxbar.contiguous()
+        if dxbar.stride(2) != 1:   # the kernel takes any row / head strides
+            dxbar = dxbar.contiguous()
         t0 = timer.begin() if timer is not None else None
         dqt, d_node, d_tw, d_tb = fastAgg.tgat_attn_bwd(g.rowptr, node_src, g.node_idx,
                                                         g.edge_tab, g.edge_idx, g.dt, time_w,

@@ -86,6 +86,16 @@ def test_kspace_absorbs_the_projection():
         torch.testing.assert_close(x_aug @ Wk.T, x @ W.T + b, rtol=1e-12, atol=1e-12)
 
 
+def test_kspace_gradients():
+    """to_kspace is a scatter of the weight columns and the bias: its gradient is the
+    matching gather (float64 finite differences)."""
+    g = torch.Generator().manual_seed(3)
+    for dn, de, dt in ((7, 5, 3), (0, 12, 9), (13, 6, 0)):
+        W = torch.randn(4, dn + de + dt, generator=g, dtype=torch.float64, requires_grad=True)
+        b = torch.randn(4, generator=g, dtype=torch.float64, requires_grad=True)
+        assert torch.autograd.gradcheck(lambda w, bb: tgat.to_kspace(w, bb, dn, de, dt), (W, b))
+
+
 def test_absorbed_attention_equals_per_edge_attention():
     """The fused kernels score q_h . (W_k x + b_k)_h as (Q_h W_k,h) . x_aug and aggregate
     V through xbar = sum_e a_e x_aug,e, out_h = W_v,h xbar_h; with a softmax over one

@@ -65,6 +65,7 @@ struct TgatParams {
   // the width zeroed; 2 = element loads (unaligned rows).
   int node_tail, edge_tail;
   uint32_t node_row_bytes, edge_row_bytes;  // descriptor range of a valid row
+  uint64_t node_stride, edge_stride;        // bytes between rows
   int dnode_dwords;                   // node-gradient rows stored dword by dword
   const float* dt; const float* time_w; const float* time_b; int dt_dim;
   int cn, ce, ct, cp;                 // chunk counts; cp = cn+ce+ct+1
@@ -234,9 +235,11 @@ __device__ __forceinline__ void init_tiles(const TgatParams& P, float* tile, int
 // ----- per-edge metadata ---------------------------------------------------------------
 // Per-lane metadata of up to 64 consecutive edges c0 + lane: row ids (split in 32-bit
 // halves for readlane), dt, dropout multipliers and (backward) scores.
+constexpr uint32_t kNoRow = 0xffffffffu;  // staged row id of a missing / out-of-range row
+
 template <int H, bool SCORES>
 struct EdgeMeta {
-  int nlo, nhi, elo, ehi;
+  uint32_t nid, eid;                        // row ids, kNoRow when outside the table
   float t;
   float dr[H];
   float sc[H];
@@ -249,10 +252,9 @@ __device__ __forceinline__ void stage_meta(const TgatParams& P, int64_t c0, int 
   const int64_t e = c0 + (lane < cnt ? lane : 0);
   const int64_t nr = P.node_idx ? P.node_idx[e] : e;
   const int64_t er = P.edge_idx ? P.edge_idx[e] : e;
-  M.nlo = static_cast<int>(nr & 0xffffffff);
-  M.nhi = static_cast<int>(nr >> 32);
-  M.elo = static_cast<int>(er & 0xffffffff);
-  M.ehi = static_cast<int>(er >> 32);
+  // range-checked here, once per edge, so that one 32-bit value per row reaches the loads
+  M.nid = (nr >= 0 && nr < P.n_node) ? static_cast<uint32_t>(nr) : kNoRow;
+  M.eid = (er >= 0 && er < P.n_erow) ? static_cast<uint32_t>(er) : kNoRow;
   M.t = P.dt_dim > 0 ? P.dt[e] : 0.f;
 #pragma unroll
   for (int h = 0; h < H; ++h) {
@@ -265,15 +267,13 @@ __device__ __forceinline__ void stage_meta(const TgatParams& P, int64_t c0, int 
 }
 
 template <int H, bool SCORES>
-__device__ __forceinline__ int64_t meta_node(const EdgeMeta<H, SCORES>& M, int j) {
-  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_int(M.nhi, j))) << 32) |
-                              static_cast<uint32_t>(lane_int(M.nlo, j)));
+__device__ __forceinline__ uint32_t meta_node(const EdgeMeta<H, SCORES>& M, int j) {
+  return static_cast<uint32_t>(lane_int(static_cast<int>(M.nid), j));
 }
 
 template <int H, bool SCORES>
-__device__ __forceinline__ int64_t meta_edge(const EdgeMeta<H, SCORES>& M, int j) {
-  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(lane_int(M.ehi, j))) << 32) |
-                              static_cast<uint32_t>(lane_int(M.elo, j)));
+__device__ __forceinline__ uint32_t meta_edge(const EdgeMeta<H, SCORES>& M, int j) {
+  return static_cast<uint32_t>(lane_int(static_cast<int>(M.eid), j));
 }
 
 // Issues the row-chunk loads of batch entries [jb, jb+nb): the lanes of node chunks load
@@ -287,14 +287,12 @@ __device__ __forceinline__ void issue_rows(const TgatParams& P, const LaneCtx<NS
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b < nb) {
-      const int64_t nrow = meta_node(M, jb + b);
-      const int64_t erow = meta_edge(M, jb + b);
-      const bool nok = nrow >= 0 && nrow < P.n_node;
-      const bool eok = erow >= 0 && erow < P.n_erow;
-      const int64_t nes = P.node_bf16 ? 2 : 4, ees = P.edge_bf16 ? 2 : 4;  // element bytes
-      const rsrc_t nr = make_rsrc(P.node_tab + (nok ? nrow : 0) * P.ld_node * nes,
+      const uint32_t nrow = meta_node(M, jb + b);
+      const uint32_t erow = meta_edge(M, jb + b);
+      const bool nok = nrow != kNoRow, eok = erow != kNoRow;
+      const rsrc_t nr = make_rsrc(P.node_tab + static_cast<uint64_t>(nok ? nrow : 0u) * P.node_stride,
                                   nok ? P.node_row_bytes : 0u);
-      const rsrc_t er = make_rsrc(P.edge_tab + (eok ? erow : 0) * P.ld_edge * ees,
+      const rsrc_t er = make_rsrc(P.edge_tab + static_cast<uint64_t>(eok ? erow : 0u) * P.edge_stride,
                                   eok ? P.edge_row_bytes : 0u);
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
@@ -793,11 +791,16 @@ int fill_params(const fa_tgat_graph* g, int heads, const float* qt, int64_t qt_r
   P.edge_tail = g->de <= 0 ? 0 : (!eal ? 2 : ((g->de & 3) ? 1 : 0));
   const int64_t nes = P.node_bf16 ? 2 : 4, ees = P.edge_bf16 ? 2 : 4;
   // mode 1 reads up to the padded width (ld rounded down to whole chunks >= dn)
+  P.node_stride = static_cast<uint64_t>(nes * g->ld_node);
+  P.edge_stride = static_cast<uint64_t>(ees * g->ld_edge);
   P.node_row_bytes = static_cast<uint32_t>(nes * (P.node_tail == 1 ? round_up(g->dn, 4) : g->dn));
   P.edge_row_bytes = static_cast<uint32_t>(ees * (P.edge_tail == 1 ? round_up(g->de, 4) : g->de));
   P.dnode_dwords = (g->dn & 3) != 0;
   if (g->n_edges > 0 && ((g->dn > 0 && g->n_node <= 0) || (g->de > 0 && g->n_edge_rows <= 0)))
     return FA_EINVAL;
+  // row ids travel as 32 bits (kNoRow marks a missing row)
+  if (g->n_node >= static_cast<int64_t>(kNoRow) || g->n_edge_rows >= static_cast<int64_t>(kNoRow))
+    return FA_EUNSUPPORTED;
   P.dt = g->dt; P.time_w = g->time_w; P.time_b = g->time_b; P.dt_dim = g->dt_dim;
   P.cn = static_cast<int>(ceil_div(g->dn, 4));
   P.ce = static_cast<int>(ceil_div(g->de, 4));

@@ -542,6 +542,286 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
 }
 
 // ---------------------------------------------------------------------------------
+// Forward, two edges at a time: the halves of the wave (lanes 0-31 and 32-63) take the
+// alternate edges c0 + 2p + half of the wave's destination. Each half holds a whole
+// K-space row in its 32 lanes (lane hl owns chunks hl + 32k, k < NS), so the dot products
+// reduce over 32 lanes, the softmax update runs for two edges per instruction and the
+// slots are fuller (94 chunks in 96 slots at C3, against 128). The halves keep separate
+// online-softmax states, merged once per destination. Rows are read with per-lane 64-bit
+// addresses (the two halves read different rows), so rows must be whole chunks (row mode
+// 0). Dynamic LDS: the time weights [dt_dim] (w, b), then per wave two time-tile rows
+// [2][tvs].
+// ---------------------------------------------------------------------------------
+constexpr int kHalf = 32;
+
+template <int NS>
+struct PairCtx {
+  // byte offset of the lane's chunk in its node / edge row, or float offset of its chunk in
+  // the time-tile row (time, bias or zero chunk)
+  uint32_t off[NS];
+  bool is_node[NS], is_edge[NS], live[NS];   // live: chunk < cp (stored)
+};
+
+template <int NS>
+__device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L) {
+  const int hl = lane_id() & (kHalf - 1);
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const int c = hl + k * kHalf;
+    L.is_node[k] = c < P.cn;
+    L.is_edge[k] = c >= P.cn && c < P.cn + P.ce;
+    L.live[k] = c < P.cp;
+    uint32_t off = 4u * static_cast<uint32_t>(P.ct + 1);
+    if (L.is_node[k]) off = (P.node_bf16 ? 8u : 16u) * static_cast<uint32_t>(c);
+    else if (L.is_edge[k]) off = (P.edge_bf16 ? 8u : 16u) * static_cast<uint32_t>(c - P.cn);
+    else if (c < P.cn + P.ce + P.ct) off = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
+    else if (c == P.cn + P.ce + P.ct) off = 4u * static_cast<uint32_t>(P.ct);
+    L.off[k] = off;
+  }
+}
+
+// Floats before the tiles in LDS: the time weights, rounded up to a whole chunk.
+__host__ __device__ __forceinline__ int pair_tile_base(int dt_dim) { return (2 * dt_dim + 3) & ~3; }
+
+// Floats of LDS per wave: two time-tile rows and the q~ rows.
+__host__ __device__ __forceinline__ int pair_wave_floats(int tvs, int heads, int ns) {
+  return 2 * tvs + 4 * heads * ns * kHalf;
+}
+
+// The time weights and phases, interleaved (w, b) per dimension, into `twb` (all waves of the
+// workgroup).
+__device__ __forceinline__ void stage_time_weights(const TgatParams& P, float2* twb) {
+  for (int d = threadIdx.x; d < P.dt_dim; d += blockDim.x) twb[d] = make_float2(P.time_w[d], P.time_b[d]);
+  __syncthreads();
+}
+
+__device__ __forceinline__ void pair_time(float t, float2 wb, float* row, int d, bool ok) {
+  float sv, cv;
+  const float a = time_arg(t, wb.x, wb.y);
+  sincos_hw(a, sv, cv);
+  if (fabsf(a) > trig::kMaxArg) cv = cosf(a);  // outside the reduction's range
+  if (ok) row[d] = cv;
+}
+
+// The value lane j holds, for every lane (j may differ per lane).
+__device__ __forceinline__ int pick_int(int v, int j) { return __builtin_amdgcn_ds_bpermute(j << 2, v); }
+__device__ __forceinline__ float pick_flt(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(j << 2, __float_as_int(v)));
+}
+
+// Sum over each half: every lane of rows 1 / 3 ends with its half's total; lanes 31 and 63
+// are read back, so the result is uniform per half.
+__device__ __forceinline__ float half_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_bcast<kRowBcast15, 0xA>(v);
+  const float s0 = lane_read(v, 31), s1 = lane_read(v, 63);
+  return lane_id() < kHalf ? s0 : s1;
+}
+
+// One chunk of a table row at `row + off` (float32, or bf16 widened).
+__device__ __forceinline__ float4 pair_chunk(const char* row, uint32_t off, int bf16) {
+  if (bf16) {
+    const uint2 w = *reinterpret_cast<const uint2*>(row + off);
+    return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+  }
+  return *reinterpret_cast<const float4*>(row + off);
+}
+
+// Row chunks of this lane's edge of pair p (edge index 2p + half among the staged ones);
+// lanes whose edge is past cnt, or whose row is missing, get zeros.
+template <int NS, int H>
+__device__ __forceinline__ void pair_rows(const TgatParams& P, const PairCtx<NS>& L,
+                                          const EdgeMeta<H, false>& M, int p, int cnt,
+                                          float4 (&x)[NS]) {
+  const int j = 2 * p + (lane_id() >= kHalf ? 1 : 0);
+  const int jj = j < cnt ? j : 0;
+  const uint32_t nid = static_cast<uint32_t>(pick_int(static_cast<int>(M.nid), jj));
+  const uint32_t eid = static_cast<uint32_t>(pick_int(static_cast<int>(M.eid), jj));
+  const bool nok = j < cnt && nid != kNoRow, eok = j < cnt && eid != kNoRow;
+  const char* nrow = P.node_tab + static_cast<uint64_t>(nok ? nid : 0u) * P.node_stride;
+  const char* erow = P.edge_tab + static_cast<uint64_t>(eok ? eid : 0u) * P.edge_stride;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    float4 v = f4_zero();
+    if (L.is_node[k] && nok) v = pair_chunk(nrow, L.off[k], P.node_bf16);
+    else if (L.is_edge[k] && eok) v = pair_chunk(erow, L.off[k], P.edge_bf16);
+    x[k] = v;
+  }
+}
+
+template <int H, int NS>
+struct PairState {
+  const float4* q;    // the destination's q~ rows in LDS: [H][32 * NS] chunks
+  float4 acc[H][NS];
+  float m[H], l[H];
+};
+
+// Pair p: time encoding of both edges into the halves' tile rows, the other chunks from
+// the tiles, scores, and the two online-softmax updates.
+template <int H, int NS>
+__device__ __forceinline__ void pair_step(const TgatParams& P, const PairCtx<NS>& L,
+                                          const EdgeMeta<H, false>& M, int64_t c0, int p,
+                                          int cnt, const float2* twb, float* tile,
+                                          float4 (&x)[NS], PairState<H, NS>& S) {
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int j = 2 * p + half;
+  const bool valid = j < cnt;
+  const int jj = valid ? j : 0;
+  float* row = tile + half * P.tvs;
+  if (P.dt_dim > 0) {
+    lds_sync();
+    const float t = pick_flt(M.t, jj);
+    for (int d = hl; d < P.dt_dim; d += kHalf) pair_time(t, twb[d], row, d, true);
+    lds_sync();
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    if (!(L.is_node[k] || L.is_edge[k])) x[k] = *reinterpret_cast<const float4*>(row + L.off[k]);
+  float sc[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    float d = 0.f;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) d += dot4(S.q[h * NS * kHalf + hl + k * kHalf], x[k]);
+    sc[h] = leaky(half_sum(d), P.slope);
+  }
+  // scores: lane hl == h of each valid half writes s[c0 + j, h]
+  {
+    float mine = 0.f;
+#pragma unroll
+    for (int h = 0; h < H; ++h) mine = hl == h ? sc[h] : mine;
+    if (valid && hl < H) P.scores[(c0 + j) * H + hl] = mine;
+  }
+  float dr[H];  // picked with every lane active (bpermute reads nothing from idle lanes)
+#pragma unroll
+  for (int h = 0; h < H; ++h) dr[h] = pick_flt(M.dr[h], jj);
+  if (valid) {
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float s = sc[h];
+      if (s > S.m[h]) {  // uniform within a half
+        const float r = exp_fast(S.m[h] - s);
+        S.l[h] *= r;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) scale4(S.acc[h][k], r);
+        S.m[h] = s;
+      }
+      const float pe = exp_fast(s - S.m[h]);
+      S.l[h] += pe;
+      const float w = pe * dr[h];
+#pragma unroll
+      for (int k = 0; k < NS; ++k) fma4(S.acc[h][k], w, x[k]);
+    }
+  }
+}
+
+template <int H, int NS>
+__global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
+  extern __shared__ float lds[];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  float2* twb = reinterpret_cast<float2*>(lds);
+  float* tile = lds + pair_tile_base(P.dt_dim) + wave * pair_wave_floats(P.tvs, H, NS);
+  float4* qs = reinterpret_cast<float4*>(tile + 2 * P.tvs);
+  PairCtx<NS> L;
+  setup_pair<NS>(P, L);
+  stage_time_weights(P, twb);
+  init_tiles(P, tile, 2, 2);
+  // chunks past cp stay zero (their x chunks are zero too)
+  for (int i = lane; i < H * NS * kHalf; i += kWave) qs[i] = f4_zero();
+
+  const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; v < P.n_dst;
+       v += total_waves) {
+    const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
+    const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
+    PairState<H, NS> S;
+    S.q = qs;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      S.m[h] = -INFINITY;
+      S.l[h] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) S.acc[h][k] = f4_zero();
+    }
+    if (e1 <= e0) {  // zero-degree destination: xbar = 0
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float* dst = P.xbar + v * P.xbar_rs + h * P.xbar_hs;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+          if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = f4_zero();
+      }
+      if (lane < H) {
+        P.stats[(v * H + lane) * 2 + 0] = -INFINITY;
+        P.stats[(v * H + lane) * 2 + 1] = 0.f;
+      }
+      continue;
+    }
+    int64_t c0 = e0;
+    int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+    EdgeMeta<H, false> M;
+    stage_meta<H, false>(P, c0, cnt, M);
+    lds_sync();  // the previous destination's reads of qs are done
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float4* src = reinterpret_cast<const float4*>(P.qt + v * P.qt_rs + h * P.qt_hs);
+      for (int c = lane; c < P.cp; c += kWave) qs[h * NS * kHalf + c] = src[c];
+    }
+    lds_sync();
+    float4 xa[NS], xb[NS];
+    pair_rows<NS, H>(P, L, M, 0, cnt, xa);
+    for (;;) {
+      const int np = (cnt + 1) >> 1;
+      for (int p = 0; p < np; p += 2) {
+        if (p + 1 < np) pair_rows<NS, H>(P, L, M, p + 1, cnt, xb);
+        pair_step<H, NS>(P, L, M, c0, p, cnt, twb, tile, xa, S);
+        if (p + 1 < np) {
+          if (p + 2 < np) pair_rows<NS, H>(P, L, M, p + 2, cnt, xa);
+          pair_step<H, NS>(P, L, M, c0, p + 1, cnt, twb, tile, xb, S);
+        }
+      }
+      c0 += kWave;
+      if (c0 >= e1) break;
+      cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      stage_meta<H, false>(P, c0, cnt, M);
+      pair_rows<NS, H>(P, L, M, 0, cnt, xa);
+    }
+    // merge the halves: M = max(m0, m1), weights exp(m - M) (0 for a half without edges)
+    const int other = lane ^ kHalf;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float mo = pick_flt(S.m[h], other), lo = pick_flt(S.l[h], other);
+      const float mx = S.m[h] > mo ? S.m[h] : mo;
+      const float r = S.m[h] == -INFINITY ? 0.f : exp_fast(S.m[h] - mx);
+      const float ro = mo == -INFINITY ? 0.f : exp_fast(mo - mx);
+      const float lt = S.l[h] * r + lo * ro;
+      const float inv = 1.f / lt;
+      float* dst = P.xbar + v * P.xbar_rs + h * P.xbar_hs;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        float4 a = S.acc[h][k], b;
+        b.x = pick_flt(a.x, other);
+        b.y = pick_flt(a.y, other);
+        b.z = pick_flt(a.z, other);
+        b.w = pick_flt(a.w, other);
+        a.x = (a.x * r + b.x * ro) * inv;
+        a.y = (a.y * r + b.y * ro) * inv;
+        a.z = (a.z * r + b.z * ro) * inv;
+        a.w = (a.w * r + b.w * ro) * inv;
+        if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = a;
+      }
+      if (lane == h) {
+        P.stats[(v * H + h) * 2 + 0] = mx;
+        P.stats[(v * H + h) * 2 + 1] = lt;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Backward: one wave per destination (grid-stride), one pass over the edges.
 // Dynamic LDS: per wave [kBatch][tvs] cos and -sin tiles, then the workgroup's time-grad
 // reduction buffer [kWavesPerBlock][2][tvs].
@@ -857,11 +1137,36 @@ int persistent_grid(int64_t n_dst, const void* kernel, size_t lds) {
   return want < res ? want : res;
 }
 
+// The two-edge forward: whole-chunk rows (mode 0), up to 2 heads, up to 128 chunks for one
+// head and 96 for two (beyond that its registers spill).
+bool pair_fwd_fits(const TgatParams& P, int heads) {
+  return heads <= 2 && P.node_tail == 0 && P.edge_tail == 0 &&
+         P.cp <= (heads == 1 ? 4 : 3) * kHalf;
+}
+
+size_t pair_lds_bytes(const TgatParams& P, int heads) {
+  return sizeof(float) * (static_cast<size_t>(pair_tile_base(P.dt_dim)) +
+                          static_cast<size_t>(kWavesPerBlock) *
+                              pair_wave_floats(P.tvs, heads, static_cast<int>(ceil_div(P.cp, kHalf))));
+}
+
 template <int H>
 int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
-  const size_t lds = fwd_lds_bytes(P);
+  size_t lds = fwd_lds_bytes(P);
   void (*k)(TgatParams) = nullptr;
+  if constexpr (H <= 2) if (pair_fwd_fits(P, H)) {
+    lds = pair_lds_bytes(P, H);
+    switch (ceil_div(P.cp, kHalf)) {
+      case 1: k = tgat_fwd_pair<H, 1>; break;
+      case 2: k = tgat_fwd_pair<H, 2>; break;
+      case 3: k = tgat_fwd_pair<H, 3>; break;
+      default: k = tgat_fwd_pair<H, (H == 1 ? 4 : 3)>; break;
+    }
+    const dim3 grid(static_cast<unsigned>(persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds)));
+    hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, stream, P);
+    return launch_status();
+  }
   switch (ns) {
     case 1: k = tgat_fwd<H, 1>; break;
     case 2: k = tgat_fwd<H, 2>; break;

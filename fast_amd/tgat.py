@@ -350,6 +350,29 @@ class TgatAttention(torch.autograd.Function):
         return dqt, d_tw, d_tb, d_src, None, None, None, None, None
 
 
+# Widest head (J) the per-head product kernels take (fastAgg.head_proj / head_reduce hold a
+# head's J x C weight fragments in registers); wider heads use batched float32 GEMMs.
+HEAD_KERNEL_MAX_J = 64
+
+
+def _proj(x, w, bias):
+    """[N, G*J] x [G, J, C] (+ [G, C]) -> [G, N, C]."""
+    G, J, _ = w.shape
+    if J <= HEAD_KERNEL_MAX_J:
+        return fastAgg.head_proj(x, w, bias)
+    y = torch.matmul(x.view(-1, G, J).transpose(0, 1), w)
+    return y if bias is None else y + bias[:, None, :]
+
+
+def _reduce(y, w):
+    """[G, N, C] x [G, J, C]^T -> [N, G*J]."""
+    G, J, _ = w.shape
+    if J <= HEAD_KERNEL_MAX_J:
+        return fastAgg.head_reduce(y, w)
+    z = torch.matmul(y, w.transpose(1, 2).contiguous())
+    return z.transpose(0, 1).reshape(y.shape[1], G * J)
+
+
 class HeadProj(torch.autograd.Function):
     """y[g] = x[:, g*J:(g+1)*J] @ w[g] (+ bias[g]) for x [N, G*J], w [G, J, C] -> [G, N, C]."""
 
@@ -357,14 +380,14 @@ class HeadProj(torch.autograd.Function):
     def forward(ctx, x, w, bias):
         ctx.save_for_backward(x, w)
         ctx.has_bias = bias is not None
-        return fastAgg.head_proj(x, w, bias)
+        return _proj(x, w, bias)
 
     @staticmethod
     def backward(ctx, dy):
         x, w = ctx.saved_tensors
         dx = dw = db = None
         if ctx.needs_input_grad[0]:
-            dx = fastAgg.head_reduce(dy, w)
+            dx = _reduce(dy, w)
         if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
             gw = fastAgg.head_wgrad(x, dy, w.shape[0], ctx.has_bias)
             dw = gw[:, :w.shape[1]]
@@ -378,13 +401,13 @@ class HeadReduce(torch.autograd.Function):
     @staticmethod
     def forward(ctx, y, w):
         ctx.save_for_backward(y, w)
-        return fastAgg.head_reduce(y, w)
+        return _reduce(y, w)
 
     @staticmethod
     def backward(ctx, dz):
         y, w = ctx.saved_tensors
         dz = dz.contiguous()
-        dy = fastAgg.head_proj(dz, w, None) if ctx.needs_input_grad[0] else None
+        dy = _proj(dz, w, None) if ctx.needs_input_grad[0] else None
         dw = fastAgg.head_wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
         return dy, dw
 

@@ -97,12 +97,14 @@ def test_head_ops_empty(dev):
     assert dw.shape == (2, 51, 376) and not bool(dw.any())
 
 
-def test_head_autograd_matches_float64(dev):
+@pytest.mark.parametrize("g,j", [(2, 50), (1, 100)])
+def test_head_autograd_matches_float64(dev, g, j):
     """The autograd wrappers of the layer (HeadProj, HeadReduce) against torch autograd in
-    float64 on the CPU, through a chain proj -> reduce like the layer's."""
+    float64 on the CPU, through a chain proj -> reduce like the layer's; heads wider than
+    the kernels' limit (j = 100) take the batched-GEMM path."""
     from fast_amd.tgat import HeadProj, HeadReduce
 
-    n, g, j, c = 500, 2, 50, 376
+    n, c = 500, 376
     gen = torch.Generator().manual_seed(4)
     x = torch.randn(n, g * j, generator=gen)
     wk = torch.randn(g, j, c, generator=gen) * 0.1

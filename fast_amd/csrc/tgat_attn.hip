@@ -560,11 +560,17 @@ struct PairCtx {
   // the time-tile row (time, bias or zero chunk)
   uint32_t off[NS];
   bool is_node[NS], is_edge[NS], live[NS];   // live: chunk < cp (stored)
+  // The lane's time chunk (at most one per lane while ct <= 32): its K-space chunk index,
+  // else `zero_chunk`, and its offset in a tile row, else the tile's zero chunk.
+  int tci;
+  uint32_t ttoff;
 };
 
 template <int NS>
-__device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L) {
+__device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L, int zero_chunk = 0) {
   const int hl = lane_id() & (kHalf - 1);
+  L.tci = zero_chunk;
+  L.ttoff = 4u * static_cast<uint32_t>(P.ct + 1);
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
     const int c = hl + k * kHalf;
@@ -574,8 +580,13 @@ __device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L) 
     uint32_t off = 4u * static_cast<uint32_t>(P.ct + 1);
     if (L.is_node[k]) off = (P.node_bf16 ? 8u : 16u) * static_cast<uint32_t>(c);
     else if (L.is_edge[k]) off = (P.edge_bf16 ? 8u : 16u) * static_cast<uint32_t>(c - P.cn);
-    else if (c < P.cn + P.ce + P.ct) off = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
-    else if (c == P.cn + P.ce + P.ct) off = 4u * static_cast<uint32_t>(P.ct);
+    else if (c < P.cn + P.ce + P.ct) {
+      off = 4u * static_cast<uint32_t>(c - P.cn - P.ce);
+      L.tci = c;
+      L.ttoff = off;
+    } else if (c == P.cn + P.ce + P.ct) {
+      off = 4u * static_cast<uint32_t>(P.ct);
+    }
     L.off[k] = off;
   }
 }
@@ -629,9 +640,9 @@ __device__ __forceinline__ float4 pair_chunk(const char* row, uint32_t off, int 
 
 // Row chunks of this lane's edge of pair p (edge index 2p + half among the staged ones);
 // lanes whose edge is past cnt, or whose row is missing, get zeros.
-template <int NS, int H>
+template <int NS, int H, bool SC>
 __device__ __forceinline__ void pair_rows(const TgatParams& P, const PairCtx<NS>& L,
-                                          const EdgeMeta<H, false>& M, int p, int cnt,
+                                          const EdgeMeta<H, SC>& M, int p, int cnt,
                                           float4 (&x)[NS]) {
   const int j = 2 * p + (lane_id() >= kHalf ? 1 : 0);
   const int jj = j < cnt ? j : 0;
@@ -772,14 +783,14 @@ __global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
     }
     lds_sync();
     float4 xa[NS], xb[NS];
-    pair_rows<NS, H>(P, L, M, 0, cnt, xa);
+    pair_rows<NS, H, false>(P, L, M, 0, cnt, xa);
     for (;;) {
       const int np = (cnt + 1) >> 1;
       for (int p = 0; p < np; p += 2) {
-        if (p + 1 < np) pair_rows<NS, H>(P, L, M, p + 1, cnt, xb);
+        if (p + 1 < np) pair_rows<NS, H, false>(P, L, M, p + 1, cnt, xb);
         pair_step<H, NS>(P, L, M, c0, p, cnt, twb, tile, xa, S);
         if (p + 1 < np) {
-          if (p + 2 < np) pair_rows<NS, H>(P, L, M, p + 2, cnt, xa);
+          if (p + 2 < np) pair_rows<NS, H, false>(P, L, M, p + 2, cnt, xa);
           pair_step<H, NS>(P, L, M, c0, p + 1, cnt, twb, tile, xb, S);
         }
       }
@@ -787,7 +798,7 @@ __global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
       if (c0 >= e1) break;
       cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
       stage_meta<H, false>(P, c0, cnt, M);
-      pair_rows<NS, H>(P, L, M, 0, cnt, xa);
+      pair_rows<NS, H, false>(P, L, M, 0, cnt, xa);
     }
     // merge the halves: M = max(m0, m1), weights exp(m - M) (0 for a half without edges)
     const int other = lane ^ kHalf;
@@ -993,6 +1004,242 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Backward, two edges at a time, in the layout of the two-edge forward: the halves take
+// alternate edges, each holds a whole K-space row in its 32 lanes. The destination's q~ and
+// dxbar rows sit in LDS ([H][32 * NS + 1] chunks each, the last chunk zero), read per pair;
+// dq~ accumulates per half in registers and the halves are added once per destination.
+// Each lane owns at most one time chunk (ct <= 32) and accumulates its time gradients.
+// Dynamic LDS: the time weights, then per wave the cos rows [2][tvs], the -sin rows
+// [2][tvs], q~ and dxbar; then the workgroup's time-grad buffer [kWavesPerBlock][2][tvs].
+// ---------------------------------------------------------------------------------
+__host__ __device__ __forceinline__ int pair_row_chunks(int ns) { return ns * kHalf + 1; }
+
+__host__ __device__ __forceinline__ int pair_bwd_wave_floats(int tvs, int heads, int ns) {
+  return 4 * tvs + 2 * 4 * heads * pair_row_chunks(ns);
+}
+
+template <int H, int NS>
+struct PairBwd {
+  float4 dq[H][NS];
+  float4 gw, gb;              // time-grad accumulators of this lane's time chunk
+  float mh[H], il[H], T[H];   // row max, 1 / softmax denominator, dxbar . xbar
+};
+
+template <int H, int NS>
+__device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx<NS>& L,
+                                              const EdgeMeta<H, true>& M, int64_t c0, int p,
+                                              int cnt, const float2* twb, float* tc, float* ts,
+                                              const float4* qs, const float4* gs,
+                                              float4 (&x)[NS], PairBwd<H, NS>& S) {
+  constexpr int QS = NS * kHalf + 1;
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int j = 2 * p + half;
+  const bool valid = j < cnt;
+  const int jj = valid ? j : 0;
+  float* rc = tc + half * P.tvs;
+  float* rs = ts + half * P.tvs;
+  const float t = pick_flt(M.t, jj);
+  if (P.dt_dim > 0) {
+    lds_sync();
+    for (int d = hl; d < P.dt_dim; d += kHalf) {
+      const float2 wb = twb[d];
+      const float a = time_arg(t, wb.x, wb.y);
+      float sv, cv;
+      sincos_hw(a, sv, cv);
+      if (fabsf(a) > trig::kMaxArg) sincosf(a, &sv, &cv);  // outside the reduction's range
+      rc[d] = cv;
+      rs[d] = -sv;
+    }
+    lds_sync();
+  }
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    if (!(L.is_node[k] || L.is_edge[k])) x[k] = *reinterpret_cast<const float4*>(rc + L.off[k]);
+  float dap[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    float d = 0.f;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) d += dot4(gs[h * QS + hl + k * kHalf], x[k]);
+    dap[h] = half_sum(d);
+  }
+  // per-edge factors; an idle half (odd edge count) gets zeros and contributes nothing
+  float ad[H], dz[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const float sc = pick_flt(M.sc[h], jj);
+    const float dr = pick_flt(M.dr[h], jj);
+    const float a = valid ? exp_fast(sc - S.mh[h]) * S.il[h] : 0.f;
+    ad[h] = a * dr;
+    dz[h] = a * (dr * dap[h] - S.T[h]) * (sc > 0.f ? 1.f : P.slope);
+#pragma unroll
+    for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[k]);
+  }
+  // node-row gradient of this half's edge: dx = sum_h ad_h dxbar_h + dz_h q~_h
+  if (P.d_node) {
+    float* drow = P.d_node + (c0 + jj) * P.ld_dnode;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      if (k * kHalf >= P.cn) continue;  // no node chunk in this slot (wave-uniform)
+      float4 dx = f4_zero();
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        fma4(dx, ad[h], gs[h * QS + hl + k * kHalf]);
+        fma4(dx, dz[h], qs[h * QS + hl + k * kHalf]);
+      }
+      if (valid && L.is_node[k]) *reinterpret_cast<float4*>(drow + 4 * (hl + k * kHalf)) = dx;
+    }
+  }
+  // d cos(w t + b) = -sin(w t + b) * (t dw + db), on this lane's time chunk
+  if (P.dt_dim > 0) {
+    float4 dx = f4_zero();
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      fma4(dx, ad[h], gs[h * QS + L.tci]);
+      fma4(dx, dz[h], qs[h * QS + L.tci]);
+    }
+    const float4 sn = *reinterpret_cast<const float4*>(rs + L.ttoff);
+    const float4 pr = make_float4(sn.x * dx.x, sn.y * dx.y, sn.z * dx.z, sn.w * dx.w);
+    S.gb.x += pr.x;
+    S.gb.y += pr.y;
+    S.gb.z += pr.z;
+    S.gb.w += pr.w;
+    fma4(S.gw, t, pr);
+  }
+}
+
+__device__ __forceinline__ float4 pick_f4(const float4& v, int j) {
+  return make_float4(pick_flt(v.x, j), pick_flt(v.y, j), pick_flt(v.z, j), pick_flt(v.w, j));
+}
+
+// Waves per SIMD the register budget is sized for (three leave 168 registers for the widest).
+constexpr int pair_bwd_min_waves(int H, int NS) { return H * NS >= 6 ? 3 : 4; }
+
+template <int H, int NS>
+__global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pair(TgatParams P) {
+  constexpr int QS = NS * kHalf + 1;
+  extern __shared__ float lds[];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int other = lane ^ kHalf;
+  float2* twb = reinterpret_cast<float2*>(lds);
+  float* tc = lds + pair_tile_base(P.dt_dim) + wave * pair_bwd_wave_floats(P.tvs, H, NS);
+  float* ts = tc + 2 * P.tvs;
+  float4* qs = reinterpret_cast<float4*>(ts + 2 * P.tvs);
+  float4* gs = qs + H * QS;
+  float* red = lds + pair_tile_base(P.dt_dim) + kWavesPerBlock * pair_bwd_wave_floats(P.tvs, H, NS);
+
+  PairCtx<NS> L;
+  setup_pair<NS>(P, L, NS * kHalf);
+  stage_time_weights(P, twb);
+  init_tiles(P, tc, 4, 2);
+  // chunks past cp (and the extra zero chunk) stay zero
+  for (int i = lane; i < 2 * H * QS; i += kWave) qs[i] = f4_zero();
+  PairBwd<H, NS> S;
+  S.gw = f4_zero();
+  S.gb = f4_zero();
+
+  const int64_t total_waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave; v < P.n_dst;
+       v += total_waves) {
+    const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
+    const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+      for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
+    if (e1 <= e0) {
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float* dst = P.dqt + v * P.dqt_rs + h * P.dqt_hs;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+          if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = f4_zero();
+      }
+      continue;
+    }
+    int64_t c0 = e0;
+    int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+    EdgeMeta<H, true> M;
+    stage_meta<H, true>(P, c0, cnt, M);
+    float4 xa[NS], xb[NS];
+    pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
+    // the destination's rows: q~ and dxbar into LDS, T = dxbar . xbar per head
+    lds_sync();  // the previous destination's reads of qs / gs are done
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const float4* qr = reinterpret_cast<const float4*>(P.qt + v * P.qt_rs + h * P.qt_hs);
+      const float4* gr = reinterpret_cast<const float4*>(P.dxbar + v * P.dxbar_rs + h * P.dxbar_hs);
+      const float4* xr = reinterpret_cast<const float4*>(P.xbar + v * P.xbar_rs + h * P.xbar_hs);
+      float d = 0.f;
+      for (int c = lane; c < P.cp; c += kWave) {
+        const float4 g = gr[c];
+        qs[h * QS + c] = qr[c];
+        gs[h * QS + c] = g;
+        d += dot4(g, xr[c]);
+      }
+      S.T[h] = wave_sum(d);
+      S.mh[h] = P.stats[(v * H + h) * 2 + 0];
+      S.il[h] = 1.f / P.stats[(v * H + h) * 2 + 1];
+    }
+    lds_sync();
+    for (;;) {
+      const int np = (cnt + 1) >> 1;
+      for (int p = 0; p < np; p += 2) {
+        if (p + 1 < np) pair_rows<NS, H, true>(P, L, M, p + 1, cnt, xb);
+        pair_bwd_step<H, NS>(P, L, M, c0, p, cnt, twb, tc, ts, qs, gs, xa, S);
+        if (p + 1 < np) {
+          if (p + 2 < np) pair_rows<NS, H, true>(P, L, M, p + 2, cnt, xa);
+          pair_bwd_step<H, NS>(P, L, M, c0, p + 1, cnt, twb, tc, ts, qs, gs, xb, S);
+        }
+      }
+      c0 += kWave;
+      if (c0 >= e1) break;
+      cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
+      stage_meta<H, true>(P, c0, cnt, M);
+      pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
+    }
+    // dq~ = the two halves' sums
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      float* dst = P.dqt + v * P.dqt_rs + h * P.dqt_hs;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        const float4 o = pick_f4(S.dq[h][k], other);
+        const float4 a = S.dq[h][k];
+        const float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+        if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = sum;
+      }
+    }
+  }
+
+  // Time-grad partials of this workgroup: the halves added, then the waves in a fixed order.
+  // Each time dim is owned by one lane of each half; lanes without a time chunk write zeros
+  // to the zero chunk, which the sum below does not read.
+  if (P.dt_dim <= 0) return;
+  {
+    const float4 ow = pick_f4(S.gw, other), ob = pick_f4(S.gb, other);
+    if (half == 0) {
+      float* rw = red + (wave * 2 + 0) * P.tvs + L.ttoff;
+      float* rb = red + (wave * 2 + 1) * P.tvs + L.ttoff;
+      rw[0] = S.gw.x + ow.x; rw[1] = S.gw.y + ow.y; rw[2] = S.gw.z + ow.z; rw[3] = S.gw.w + ow.w;
+      rb[0] = S.gb.x + ob.x; rb[1] = S.gb.y + ob.y; rb[2] = S.gb.z + ob.z; rb[3] = S.gb.w + ob.w;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 2 * P.dt_dim; idx += kBlock) {
+    const int which = idx / P.dt_dim;
+    const int jd = idx - which * P.dt_dim;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) sum += red[(w * 2 + which) * P.tvs + jd];
+    P.partial[(static_cast<int64_t>(blockIdx.x) * 2 + which) * P.dt_dim + jd] = sum;
+  }
+}
+
 // Sums the per-workgroup partials: one wave per output value, fixed lane assignment.
 __global__ __launch_bounds__(kBlock) void time_grad_reduce(const float* partial, int rows, int dt_dim,
                                                           float* d_w, float* d_b) {
@@ -1181,13 +1428,27 @@ int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
 
 constexpr size_t kMaxLds = 64 * 1024;  // dynamic LDS per workgroup used by the fused kernels
 
+// The two-edge backward: the forward's conditions, at most 96 chunks, at most 32 time
+// chunks (one per lane), and 16-byte node-gradient rows.
+bool pair_bwd_fits(const TgatParams& P, int heads) {
+  return pair_fwd_fits(P, heads) && P.cp <= 3 * kHalf && P.ct <= kHalf &&
+         (!P.d_node || !P.dnode_dwords);
+}
+
+size_t pair_bwd_lds_bytes(const TgatParams& P, int heads) {
+  const int ns = static_cast<int>(ceil_div(P.cp, kHalf));
+  return sizeof(float) * (static_cast<size_t>(pair_tile_base(P.dt_dim)) +
+                          static_cast<size_t>(kWavesPerBlock) * pair_bwd_wave_floats(P.tvs, heads, ns) +
+                          static_cast<size_t>(kWavesPerBlock) * 2 * P.tvs);
+}
+
 int bwd_grid(int64_t n_dst) { return stride_grid(n_dst); }
 
 // `grid` returns the workgroups launched (rows of the time-gradient partials).
 template <int H>
 int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
-  const size_t lds = bwd_lds_bytes(P);
+  size_t lds = bwd_lds_bytes(P);
   void (*k)(TgatParams) = nullptr;
   switch (ns) {
     case 1: k = tgat_bwd<H, 1>; break;
@@ -1195,6 +1456,15 @@ int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
     case 3: k = tgat_bwd<H, 3>; break;
     case 4: k = tgat_bwd<H, 4>; break;
     default: return FA_EUNSUPPORTED;
+  }
+  if constexpr (H <= 2) if (pair_bwd_fits(P, H)) {
+    const int pns = static_cast<int>(ceil_div(P.cp, kHalf));
+    lds = pair_bwd_lds_bytes(P, H);
+    switch (pns) {
+      case 1: k = tgat_bwd_pair<H, 1>; break;
+      case 2: k = tgat_bwd_pair<H, 2>; break;
+      default: k = tgat_bwd_pair<H, 3>; break;
+    }
   }
   grid = persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds);
   hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(kBlock), lds, stream, P);

@@ -175,6 +175,25 @@ int epi_grid(int64_t n) {
   return static_cast<int>(want < kEpiMaxBlocks ? (want < 1 ? 1 : want) : kEpiMaxBlocks);
 }
 
+// out[r][g] = sum_j a[r][g*width + j] * b[r][g*width + j]: one wave per row (grid-stride),
+// a fixed-order wave sum per group.
+__global__ __launch_bounds__(kBlock) void row_group_dots(int64_t n, int groups, int width,
+                                                        const float* a, int64_t lda,
+                                                        const float* b, int64_t ldb, float* out) {
+  const int lane = lane_id();
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       r < n; r += total) {
+    for (int g = 0; g < groups; ++g) {
+      float p = 0.f;
+      for (int j = lane; j < width; j += kWave)
+        p = fmaf(a[r * lda + g * width + j], b[r * ldb + g * width + j], p);
+      p = wave_sum(p);
+      if (lane == 0) out[r * groups + g] = p;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace fa
 
@@ -201,6 +220,18 @@ extern "C" int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, i
     case 3: hipLaunchKernelGGL(epilogue_fwd<3>, grid, dim3(kBlock), 0, stream, P); break;
     default: hipLaunchKernelGGL(epilogue_fwd<4>, grid, dim3(kBlock), 0, stream, P); break;
   }
+  return launch_status();
+}
+
+extern "C" int fa_row_group_dots_f32(int64_t n, int32_t groups, int32_t width, const float* a,
+                                     int64_t lda, const float* b, int64_t ldb, float* out,
+                                     hipStream_t stream) {
+  if (n < 0 || groups <= 0 || width <= 0) return FA_EINVAL;
+  if (n == 0) return FA_OK;
+  const int64_t cols = static_cast<int64_t>(groups) * width;
+  if (!a || !b || !out || lda < cols || ldb < cols) return FA_EINVAL;
+  hipLaunchKernelGGL(row_group_dots, dim3(static_cast<unsigned>(epi_grid(n))), dim3(kBlock), 0,
+                     stream, n, groups, width, a, lda, b, ldb, out);
   return launch_status();
 }
 

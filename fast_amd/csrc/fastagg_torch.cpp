@@ -624,14 +624,30 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       std::optional<at::Tensor> edge_idx, at::Tensor dt,
                                       at::Tensor time_w, at::Tensor time_b, at::Tensor qt,
                                       double slope, std::optional<at::Tensor> drop,
-                                      uint64_t drop_seed, double drop_p, at::Tensor xbar,
-                                      at::Tensor scores, at::Tensor stats, at::Tensor dxbar,
-                                      bool need_d_node) {
+                                      uint64_t drop_seed, double drop_p,
+                                      std::optional<at::Tensor> xbar, at::Tensor scores,
+                                      at::Tensor stats, at::Tensor dxbar, bool need_d_node,
+                                      std::optional<at::Tensor> tdot) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
   TORCH_CHECK(qt.dim() == 3, "qt must be [heads, n_dst, Kp]");
   const int64_t H = qt.size(0);
   check_kspace(qt, g, H, "qt");
-  check_kspace(xbar, g, H, "xbar");
+  TORCH_CHECK(xbar.has_value() || tdot.has_value(), "tgat_attn_bwd needs xbar or tdot");
+  const float* xptr = nullptr;
+  int64_t x_rs = 0, x_hs = 0;
+  if (xbar.has_value()) {
+    check_kspace(*xbar, g, H, "xbar");
+    xptr = xbar->data_ptr<float>();
+    x_rs = xbar->stride(1);
+    x_hs = xbar->stride(0);
+  }
+  const float* tptr = nullptr;
+  if (tdot.has_value()) {
+    CHECK_INPUT((*tdot));
+    CHECK_DTYPE((*tdot), at::kFloat);
+    TORCH_CHECK(tdot->numel() == g.n_dst * H, "tdot must be [n_dst, heads]");
+    tptr = tdot->data_ptr<float>();
+  }
   check_kspace(dxbar, g, H, "dxbar");
   CHECK_INPUT(scores);
   CHECK_INPUT(stats);
@@ -655,7 +671,7 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
   const int st = fa_tgat_attn_bwd_f32(
       &g, static_cast<int32_t>(H), qt.data_ptr<float>(), qt.stride(1), qt.stride(0),
       static_cast<float>(slope), dptr, drop_seed, static_cast<float>(drop_p),
-      xbar.data_ptr<float>(), xbar.stride(1), xbar.stride(0), scores.data_ptr<float>(),
+      xptr, x_rs, x_hs, tptr, scores.data_ptr<float>(),
       stats.data_ptr<float>(), dxbar.data_ptr<float>(), dxbar.stride(1), dxbar.stride(0),
       dqt.data_ptr<float>(), dqt.stride(1), dqt.stride(0),
       need_d_node && g.n_edges > 0 && g.dn > 0 ? d_node.data_ptr<float>() : nullptr,
@@ -719,6 +735,24 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
                      : fa_gather_rows_f32(tab.data_ptr<float>(), ld, tab.size(0), ip, n, dim,
                                           out.data_ptr<float>(), dim, stream_of(tab));
   check_status(st, "gather_rows");
+  return out;
+}
+
+// [n, groups]: dot products of a's and b's column groups of `width` per row.
+at::Tensor row_group_dots(at::Tensor a, at::Tensor b, int64_t groups) {
+  CHECK_INPUT(a);
+  CHECK_INPUT(b);
+  CHECK_DTYPE(a, at::kFloat);
+  CHECK_DTYPE(b, at::kFloat);
+  TORCH_CHECK(a.dim() == 2 && a.sizes() == b.sizes(), "a and b must be the same [n, cols]");
+  TORCH_CHECK(groups > 0 && a.size(1) % groups == 0, "cols must split into groups");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+  auto out = at::empty({a.size(0), groups}, a.options());
+  const int st = fa_row_group_dots_f32(a.size(0), static_cast<int32_t>(groups),
+                                       static_cast<int32_t>(a.size(1) / groups), a.data_ptr<float>(),
+                                       a.size(1), b.data_ptr<float>(), b.size(1),
+                                       out.data_ptr<float>(), stream_of(a));
+  check_status(st, "row_group_dots");
   return out;
 }
 
@@ -948,7 +982,8 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("node_tab"), py::arg("node_idx"), py::arg("edge_tab"), py::arg("edge_idx"),
         py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"), py::arg("slope"),
         py::arg("drop"), py::arg("drop_seed"), py::arg("drop_p"), py::arg("xbar"),
-        py::arg("scores"), py::arg("stats"), py::arg("dxbar"), py::arg("need_d_node"));
+        py::arg("scores"), py::arg("stats"), py::arg("dxbar"), py::arg("need_d_node"),
+        py::arg("tdot") = py::none());
   m.def("dropout_mask", &dropout_mask, "multipliers of the hashed attention dropout",
         py::arg("n_edges"), py::arg("heads"), py::arg("seed"), py::arg("p"), py::arg("device"));
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
@@ -964,6 +999,8 @@ PYBIND11_MODULE(fastAgg, m) {
   m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2 + bias)))",
         py::arg("r1"), py::arg("r2"), py::arg("bias"), py::arg("gamma"), py::arg("beta"),
         py::arg("eps"), py::arg("drop_seed"), py::arg("drop_p"));
+  m.def("row_group_dots", &row_group_dots, "per-row dot products of column groups",
+        py::arg("a"), py::arg("b"), py::arg("groups"));
   m.def("tgat_epilogue_bwd", &tgat_epilogue_bwd, "backward of tgat_epilogue_fwd", py::arg("dout"),
         py::arg("y"), py::arg("stats"), py::arg("gamma"), py::arg("drop_p"),
         py::arg("need_dbias") = false);

@@ -34,6 +34,7 @@
 #include <float.h>
 
 #include "fa_common.hpp"
+#include <type_traits>
 
 namespace fa {
 namespace {
@@ -80,6 +81,7 @@ struct TgatParams {
   float* scores; float* stats;
   // backward
   const float* dxbar; int64_t dxbar_rs, dxbar_hs;
+  const float* tdot;                  // [n_dst][H] dxbar . xbar when given (xbar then unread)
   float* dqt; int64_t dqt_rs, dqt_hs;
   float* d_node; int64_t ld_dnode;
   float* partial;                     // [gridDim.x][2][dt_dim]
@@ -950,7 +952,7 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     load_rows<H, NS>(P.qt, P.qt_rs, P.qt_hs, v, P.kp, S.q);
     load_rows<H, NS>(P.dxbar, P.dxbar_rs, P.dxbar_hs, v, P.kp, S.g);
     float4 xr[H][NS];
-    load_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, xr);
+    if (!P.tdot) load_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, xr);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
@@ -959,7 +961,8 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     float4 xa[kBatch][NS], xb[kBatch][NS];
     issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
 #pragma unroll
-    for (int h = 0; h < H; ++h) S.T[h] = wave_sum(row_dot<NS>(S.g[h], xr[h]));
+    for (int h = 0; h < H; ++h)
+      S.T[h] = P.tdot ? P.tdot[v * H + h] : wave_sum(row_dot<NS>(S.g[h], xr[h]));
     for (;;) {
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;
@@ -1173,15 +1176,23 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     for (int h = 0; h < H; ++h) {
       const float4* qr = reinterpret_cast<const float4*>(P.qt + v * P.qt_rs + h * P.qt_hs);
       const float4* gr = reinterpret_cast<const float4*>(P.dxbar + v * P.dxbar_rs + h * P.dxbar_hs);
-      const float4* xr = reinterpret_cast<const float4*>(P.xbar + v * P.xbar_rs + h * P.xbar_hs);
       float d = 0.f;
-      for (int c = lane; c < P.cp; c += kWave) {
-        const float4 g = gr[c];
-        qs[h * QS + c] = qr[c];
-        gs[h * QS + c] = g;
-        d += dot4(g, xr[c]);
+      if (P.tdot) {
+        for (int c = lane; c < P.cp; c += kWave) {
+          qs[h * QS + c] = qr[c];
+          gs[h * QS + c] = gr[c];
+        }
+        S.T[h] = P.tdot[v * H + h];
+      } else {
+        const float4* xr = reinterpret_cast<const float4*>(P.xbar + v * P.xbar_rs + h * P.xbar_hs);
+        for (int c = lane; c < P.cp; c += kWave) {
+          const float4 g = gr[c];
+          qs[h * QS + c] = qr[c];
+          gs[h * QS + c] = g;
+          d += dot4(g, xr[c]);
+        }
+        S.T[h] = wave_sum(d);
       }
-      S.T[h] = wave_sum(d);
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
       S.il[h] = 1.f / P.stats[(v * H + h) * 2 + 1];
     }
@@ -1279,6 +1290,20 @@ __global__ __launch_bounds__(kBlock) void gather_rows(const T* tab, int64_t ld_t
   const bool ok = src >= 0 && src < n_tab;
   for (int c = lane_id(); c < dim; c += kWave)
     out[r * ld_out + c] = ok ? to_float(tab[src * ld_tab + c]) : 0.f;
+}
+
+// Float32 rows whole chunks wide (aligned, dim and both row strides multiples of 4): a
+// half-wave per row, float4 loads and stores.
+__global__ __launch_bounds__(kBlock) void gather_rows4(const float* tab, int64_t ld_tab, int64_t n_tab,
+                                                      const int64_t* idx, int64_t n, int dim,
+                                                      float* out, int64_t ld_out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (2 * kWavesPerBlock) + threadIdx.x / kHalf;
+  if (r >= n) return;
+  const int64_t src = idx ? idx[r] : r;
+  const bool ok = src >= 0 && src < n_tab;
+  const float4* row = reinterpret_cast<const float4*>(tab + (ok ? src : 0) * ld_tab);
+  float4* dst = reinterpret_cast<float4*>(out + r * ld_out);
+  for (int c = threadIdx.x & (kHalf - 1); c < dim / 4; c += kHalf) dst[c] = ok ? row[c] : f4_zero();
 }
 
 // ---------------------------------------------------------------------------------
@@ -1524,7 +1549,8 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
 extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                                     int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
                                     uint64_t drop_seed, float drop_p, const float* xbar,
-                                    int64_t xbar_rs, int64_t xbar_hs, const float* scores,
+                                    int64_t xbar_rs, int64_t xbar_hs, const float* tdot,
+                                    const float* scores,
                                     const float* stats, const float* dxbar, int64_t dxbar_rs,
                                     int64_t dxbar_hs, float* dqt, int64_t dqt_rs, int64_t dqt_hs,
                                     float* d_node, int64_t ld_dnode,
@@ -1541,8 +1567,8 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
     return launch_status();
   }
   if (bwd_lds_bytes(P) > kMaxLds || P.ct > kWave) return FA_EUNSUPPORTED;
-  if (!xbar || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
-  if ((st = check_in_rows(xbar, xbar_rs, xbar_hs)) != FA_OK) return st;
+  if ((!xbar && !tdot) || !dxbar || !dqt || !stats || (P.n_edges > 0 && !scores)) return FA_EINVAL;
+  if (!tdot && (st = check_in_rows(xbar, xbar_rs, xbar_hs)) != FA_OK) return st;
   if ((st = check_in_rows(dxbar, dxbar_rs, dxbar_hs)) != FA_OK) return st;
   if ((st = check_out_rows(dqt, dqt_rs, dqt_hs, P.kp, heads, P.n_dst)) != FA_OK) return st;
   if (d_node && (P.dn <= 0 || ld_dnode < P.dn)) return FA_EINVAL;
@@ -1551,7 +1577,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   int grid = bwd_grid(P.n_dst);   // the most workgroups a launch uses (scratch rows)
   if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
-  P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs;
+  P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs; P.tdot = tdot;
   P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dxbar_hs = dxbar_hs;
   P.dqt = dqt; P.dqt_rs = dqt_rs; P.dqt_hs = dqt_hs;
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
@@ -1595,6 +1621,13 @@ int gather_rows_launch(const T* tab, int64_t ld_tab, int64_t n_tab, const int64_
   if (n < 0 || dim < 0 || n_tab < 0) return FA_EINVAL;
   if (n == 0 || dim == 0) return FA_OK;
   if (!tab || !out || ld_tab < dim || ld_out < dim) return FA_EINVAL;
+  if constexpr (std::is_same<T, float>::value) {
+    if (aligned16(tab) && aligned16(out) && !(dim & 3) && !(ld_tab & 3) && !(ld_out & 3)) {
+      hipLaunchKernelGGL(gather_rows4, dim3(static_cast<unsigned>(ceil_div(n, 2 * kWavesPerBlock))),
+                         dim3(kBlock), 0, stream, tab, ld_tab, n_tab, idx, n, dim, out, ld_out);
+      return launch_status();
+    }
+  }
   hipLaunchKernelGGL(gather_rows<T>, dim3(static_cast<unsigned>(ceil_div(n, kWavesPerBlock))), dim3(kBlock),
                      0, stream, tab, ld_tab, n_tab, idx, n, dim, out, ld_out);
   return launch_status();

@@ -210,7 +210,7 @@ def to_kspace(W: torch.Tensor, b: torch.Tensor, dn: int, de: int, dt: int) -> to
 
 def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, heads: int,
                        node_idx: bool, edge_idx: bool, d_node: bool = False,
-                       node_bytes: int = 4, edge_bytes: int = 4) -> dict:
+                       node_bytes: int = 4, edge_bytes: int = 4, tdot: bool = False) -> dict:
     """Algorithmic HBM bytes of one launch of the fused forward / backward kernel (float32):
     every byte the kernel must read or write once, gathered rows counted once per use.
 
@@ -219,14 +219,16 @@ def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, head
                + score (4*heads, written / read)
                [+ d_node row (4*dn) written in backward when requested]
     per dst  : forward  qt read + xbar written (2 * 4*heads*Kp) + stats written (8*heads)
-               backward qt, xbar, dxbar read + dqt written (4 * 4*heads*Kp) + stats read (8*heads)
+               backward qt, xbar, dxbar read + dqt written (4 * 4*heads*Kp) + stats read (8*heads);
+               with ``tdot`` the per-head dot products (4*heads) are read instead of xbar
     plus the row offsets 4*(n_dst+1) and the time parameters 8*dt."""
     kp = kspace_width(dn, de, dt)
     edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + node_bytes * dn + edge_bytes * de
     common = 4 * (n_dst + 1) + 8 * dt
     fwd = common + n_edges * (edge_in + 4 * heads) + n_dst * (2 * 4 * heads * kp + 8 * heads)
+    dst_rows = (3 * 4 * heads * kp + 4 * heads) if tdot else 4 * 4 * heads * kp
     bwd = (common + n_edges * (edge_in + 4 * heads + (4 * dn if d_node else 0))
-           + n_dst * (4 * 4 * heads * kp + 8 * heads))
+           + n_dst * (dst_rows + 8 * heads))
     return {"fwd": fwd, "bwd": bwd}
 
 
@@ -295,7 +297,7 @@ class TgatAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, qt, time_w, time_b, node_src, g: _Graph, slope: float, drop,
-                drop_seed: int = 0, drop_p: float = 0.0):
+                drop_seed: int = 0, drop_p: float = 0.0, link: Optional["_TdotLink"] = None):
         t0 = timer.begin() if timer is not None else None
         xbar, scores, stats = fastAgg.tgat_attn_fwd(g.rowptr, node_src, g.node_idx, g.edge_tab,
                                                     g.edge_idx, g.dt, time_w, time_b, qt,
@@ -309,6 +311,7 @@ class TgatAttention(torch.autograd.Function):
                                     edge_bytes=g.edge_tab.element_size())["fwd"]
             timer.end("tgat_fwd", t0, nb)
         ctx.g = g
+        ctx.link = link
         ctx.slope = float(slope)
         ctx.has_drop = drop is not None
         ctx.drop_seed = int(drop_seed)
@@ -328,18 +331,22 @@ class TgatAttention(torch.autograd.Function):
         need_node = ctx.needs_input_grad[3] and node_src.shape[1] > 0
         if dxbar.stride(2) != 1:   # the kernel takes any row / head strides
             dxbar = dxbar.contiguous()
+        # dxbar . xbar per destination and head, when the consumer of xbar supplied it
+        tdot = ctx.link.take() if ctx.link is not None else None
         t0 = timer.begin() if timer is not None else None
         dqt, d_node, d_tw, d_tb = fastAgg.tgat_attn_bwd(g.rowptr, node_src, g.node_idx,
                                                         g.edge_tab, g.edge_idx, g.dt, time_w,
                                                         time_b, qt, ctx.slope, drop,
-                                                        ctx.drop_seed, ctx.drop_p, xbar,
-                                                        scores, stats, dxbar, need_node)
+                                                        ctx.drop_seed, ctx.drop_p,
+                                                        None if tdot is not None else xbar,
+                                                        scores, stats, dxbar, need_node, tdot)
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
                                     g.node_idx is not None, g.edge_idx is not None,
                                     need_node, node_bytes=node_src.element_size(),
-                                    edge_bytes=g.edge_tab.element_size())["bwd"]
+                                    edge_bytes=g.edge_tab.element_size(),
+                                    tdot=tdot is not None)["bwd"]
             timer.end("tgat_bwd", t0, nb)
         d_src = None
         if need_node:
@@ -347,7 +354,20 @@ class TgatAttention(torch.autograd.Function):
                 d_src = d_node
             else:
                 d_src = torch.zeros_like(node_src).index_add_(0, g.node_idx, d_node)
-        return dqt, d_tw, d_tb, d_src, None, None, None, None, None
+        return dqt, d_tw, d_tb, d_src, None, None, None, None, None, None
+
+
+class _TdotLink:
+    """Carries T[v, h] = dxbar[h, v] . xbar[h, v] from the backward of the reduction that
+    consumes xbar (HeadReduce: with agg = W_v xbar, T = dagg . agg over D/H entries instead
+    of Kp) to the backward of TgatAttention, which runs right after it."""
+
+    def __init__(self):
+        self.tdot = None
+
+    def take(self):
+        t, self.tdot = self.tdot, None
+        return t
 
 
 # Widest head (J) the per-head product kernels take (fastAgg.head_proj / head_reduce hold a
@@ -373,6 +393,27 @@ def _reduce(y, w):
     return z.transpose(0, 1).reshape(y.shape[1], G * J)
 
 
+class _SplitRows(torch.autograd.Function):
+    """(h[:n], h[n:]): the destination rows and the rows feeding the edges of a dense
+    source-feature tensor. Its backward concatenates the two gradients into one tensor (two
+    plain slices would each zero-fill a full-size gradient and then add them)."""
+
+    @staticmethod
+    def forward(ctx, h, n: int):
+        ctx.n = int(n)
+        ctx.shape = h.shape
+        return h[:n], h[n:]
+
+    @staticmethod
+    def backward(ctx, g_dst, g_src):
+        n, (rows, dim) = ctx.n, ctx.shape
+        if g_dst is None:
+            g_dst = torch.zeros(n, dim, device=g_src.device, dtype=g_src.dtype)
+        if g_src is None:
+            g_src = torch.zeros(rows - n, dim, device=g_dst.device, dtype=g_dst.dtype)
+        return torch.cat([g_dst, g_src]), None
+
+
 class HeadProj(torch.autograd.Function):
     """y[g] = x[:, g*J:(g+1)*J] @ w[g] (+ bias[g]) for x [N, G*J], w [G, J, C] -> [G, N, C]."""
 
@@ -396,20 +437,26 @@ class HeadProj(torch.autograd.Function):
 
 
 class HeadReduce(torch.autograd.Function):
-    """z[:, g*J:(g+1)*J] = y[g] @ w[g]^T for y [G, N, C], w [G, J, C] -> [N, G*J]."""
+    """z[:, g*J:(g+1)*J] = y[g] @ w[g]^T for y [G, N, C], w [G, J, C] -> [N, G*J]. With a
+    ``link``, its backward also leaves T[n, g] = dy[g, n] . y[g, n] = dz[n, g-block] .
+    z[n, g-block] there (for TgatAttention's backward)."""
 
     @staticmethod
-    def forward(ctx, y, w):
-        ctx.save_for_backward(y, w)
-        return _reduce(y, w)
+    def forward(ctx, y, w, link: Optional[_TdotLink] = None):
+        z = _reduce(y, w)
+        ctx.link = link
+        ctx.save_for_backward(y, w, z)
+        return z
 
     @staticmethod
     def backward(ctx, dz):
-        y, w = ctx.saved_tensors
+        y, w, z = ctx.saved_tensors
         dz = dz.contiguous()
         dy = _proj(dz, w, None) if ctx.needs_input_grad[0] else None
         dw = fastAgg.head_wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
-        return dy, dw
+        if ctx.link is not None and dy is not None:
+            ctx.link.tdot = fastAgg.row_group_dots(dz, z, w.shape[0])
+        return dy, dw, None
 
 
 class TgatEpilogue(torch.autograd.Function):
@@ -558,7 +605,13 @@ class TransfomerAttentionLayer(torch.nn.Module):
         dev = b.device
         if E == 0:  # layers.py:101-102
             return torch.zeros((N, D), device=dev)
-        hdst = b.dst_node_feats() if Dn > 0 else None
+        node_src = node_idx = None
+        if Dn > 0 and "h" in b.srcdata:
+            hdst, node_src = _SplitRows.apply(b.srcdata["h"], N)
+        else:
+            hdst = b.dst_node_feats() if Dn > 0 else None
+            if Dn > 0:
+                node_src, node_idx = b.src_node_source()
         kp = kspace_width(Dn, De, Dt)
         # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h].
         wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
@@ -574,7 +627,6 @@ class TransfomerAttentionLayer(torch.nn.Module):
             q1 = self._query_bias() if Dt > 0 else torch.ones(D, device=dev)
             qt = HeadProj.apply(q1.view(1, D), wk, None).expand(H, N, kp)
 
-        node_src, node_idx = b.src_node_source() if Dn > 0 else (None, None)
         edge_tab, edge_idx = b.edge_source() if De > 0 else (None, None)
         if node_src is None:
             node_src = torch.empty(E, 0, device=dev)
@@ -590,14 +642,15 @@ class TransfomerAttentionLayer(torch.nn.Module):
             tw = tb = torch.empty(0, device=dev)
             dt = torch.zeros(E, device=dev)
         g = _Graph(b.rowptr(), node_idx, edge_tab, edge_idx, dt)
+        link = _TdotLink()
         xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop, drop_seed,
-                                   drop_p)
+                                   drop_p, link)
 
         # Absorbed values, head by head: agg[v, h, :] = W_v,aug[h] xbar[h, v, :], then
         # rst = w_out([agg | hdst]) as agg W_o[:, :D]^T + hdst W_o[:, D:]^T + b_o (the
         # bias and the sum in the epilogue kernel).
         wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
-        agg = HeadReduce.apply(xbar, wv)
+        agg = HeadReduce.apply(xbar, wv, link)
         r1 = RowsMM.apply(agg, Wo[:, :D])
         ln = self.layer_norm
         return TgatEpilogue.apply(r1, r2, self.w_out.bias, ln.weight, ln.bias, ln.eps,

@@ -233,7 +233,9 @@ int fa_tgat_attn_weights_f32(const int64_t* dst, int64_t n_edges, int64_t n_dst,
                              hipStream_t stream);
 
 /* Backward, one pass over the edges. xbar: the forward output (its dot product with dxbar
- * gives each destination's softmax correction); dxbar: gradient of xbar. Outputs: dqt
+ * gives each destination's softmax correction); tdot: that dot product itself, [n_dst][heads]
+ * (may be NULL; when given, xbar is not read and may be NULL; a caller holding
+ * agg = W_v xbar and its gradient has it as dagg . agg); dxbar: gradient of xbar. Outputs: dqt
  * (strides dqt_rs, dqt_hs); d_node [n_edges][ld_dnode] gradient of the
  * node-feature part of every x_e (may be NULL); d_time_w/d_time_b [dt_dim] (may be NULL
  * when dt_dim == 0). scratch: fa_tgat_attn_bwd_scratch_bytes(g->n_dst, dt_dim).
@@ -242,7 +244,7 @@ size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim);
 int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                          int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
                          uint64_t drop_seed, float drop_p, const float* xbar, int64_t xbar_rs,
-                         int64_t xbar_hs, const float* scores, const float* stats,
+                         int64_t xbar_hs, const float* tdot, const float* scores, const float* stats,
                          const float* dxbar, int64_t dxbar_rs, int64_t dxbar_hs, float* dqt,
                          int64_t dqt_rs, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
                          float* d_time_w, float* d_time_b, void* scratch,
@@ -303,6 +305,12 @@ int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const floa
                              const float* stats, const float* gamma, float drop_p, float* du,
                              float* dgamma, float* dbeta, float* dbias, void* scratch,
                              size_t scratch_bytes, hipStream_t stream);
+
+/* Per-row, per-group dot products (new op, no reference counterpart: it gives the fused
+ * backward its per-destination correction in D-space, dagg . agg, instead of reading xbar):
+ * out[r*groups + g] = sum_{j < width} a[r*lda + g*width + j] * b[r*ldb + g*width + j]. */
+int fa_row_group_dots_f32(int64_t n, int32_t groups, int32_t width, const float* a, int64_t lda,
+                          const float* b, int64_t ldb, float* out, hipStream_t stream);
 
 /* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
 int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,

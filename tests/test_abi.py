@@ -37,7 +37,8 @@ def test_header_declares_the_path():
                  "fa_edge_softmax_bwd_f32", "fa_edge_scatter_sum_f32", "fa_segment_sum_f32",
                  "fa_exclusive_sum_i32", "fa_degree_count_i32", "fa_balance_mask_i32",
                  "fa_fused_attn_fwd_f32", "fa_fused_attn_bwd_f32", "fa_group_softmax_fwd_f32",
-                 "fa_head_proj_f32", "fa_head_reduce_f32", "fa_head_wgrad_f32"):
+                 "fa_head_proj_f32", "fa_head_reduce_f32", "fa_head_wgrad_f32",
+                 "fa_row_group_dots_f32"):
         assert must in names
 
 
@@ -62,7 +63,7 @@ def test_status_strings_and_version(lib):
         assert lib.fa_status_string(st)
     assert lib.fa_status_string(FA_OK) == b"success"
     assert lib.fa_status_string(-99) == b"unknown status"
-    assert lib.fa_abi_version() // 100 == 3
+    assert lib.fa_abi_version() // 100 == 4
 
 
 def test_kspace_width(lib):

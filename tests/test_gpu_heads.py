@@ -123,3 +123,18 @@ def test_head_autograd_matches_float64(dev, g, j):
     assert_rel(z, zr, 1e-5, "chain output")
     for a, b, name in zip(xs, rs, ("dx", "dwk", "dwv")):
         assert_rel(a.grad, b.grad, 1e-5, name)
+
+
+@pytest.mark.parametrize("n,g,j", [(1000, 2, 50), (77, 8, 32), (5, 1, 100), (300, 3, 7), (0, 2, 50)])
+def test_row_group_dots(dev, n, g, j):
+    """out[r, h] = a[r, h-block] . b[r, h-block] against float64, entrywise error bound."""
+    from fast_amd import fastAgg
+
+    gen = torch.Generator().manual_seed(n + g + j)
+    a = torch.randn(n, g * j, generator=gen)
+    b = torch.randn(n, g * j, generator=gen)
+    got = fastAgg.row_group_dots(a.to(dev), b.to(dev), g)
+    assert got.shape == (n, g)
+    ref = (a.double().view(n, g, j) * b.double().view(n, g, j)).sum(-1)
+    mag = (a.double().abs().view(n, g, j) * b.double().abs().view(n, g, j)).sum(-1)
+    _bound_check(got, ref, mag, j, "row_group_dots")

@@ -399,3 +399,36 @@ def test_hashed_dropout_equals_explicit_mask(dev):
     ref = tgat_layer(P, cpu.srcdata["h"].double(), cpu.edata["f"], cpu.edata["dt"], src, dst,
                      len(degrees), att_drop=mask)
     assert_rel(outs[0], ref, FP32_TOL, "hashed dropout vs restatement")
+
+
+@pytest.mark.parametrize("heads", [2, 4])
+def test_backward_with_tdot_matches_xbar(dev, heads):
+    """The backward given T = dxbar . xbar per destination (tdot) equals the backward that
+    reads xbar and forms T itself (both kernel variants: 2 heads take the two-edge kernels)."""
+    from fast_amd import fastAgg
+    from fast_amd.tgat import kspace_width
+
+    g = torch.Generator().manual_seed(21 + heads)
+    N, dn, de, dtd = 300, 100, 172, 100
+    deg = torch.randint(0, 30, (N,), generator=g)
+    rowptr = torch.zeros(N + 1, dtype=torch.int32)
+    rowptr[1:] = torch.cumsum(deg, 0).to(torch.int32)
+    E = int(rowptr[-1])
+    ntab = torch.randn(500, dn, generator=g)
+    etab = torch.randn(900, de, generator=g)
+    nid = torch.randint(0, 500, (E,), generator=g)
+    eid = torch.randint(0, 900, (E,), generator=g)
+    dt = torch.empty(E).exponential_(1e-4, generator=g)
+    tw = torch.randn(dtd, generator=g) * 0.1
+    tb = torch.randn(dtd, generator=g)
+    kp = kspace_width(dn, de, dtd)
+    qt = torch.randn(heads, N, kp, generator=g) * 0.05
+    dxbar = torch.randn(heads, N, kp, generator=g)
+    args = [t.to(dev) for t in (rowptr, ntab, nid, etab, eid, dt, tw, tb, qt)]
+    xbar, sc, st = fastAgg.tgat_attn_fwd(*args, 0.2, None)
+    dxb = dxbar.to(dev)
+    tdot = (dxb * xbar).sum(-1).t().contiguous()       # [N, heads]
+    ra = fastAgg.tgat_attn_bwd(*args, 0.2, None, 0, 0.0, xbar, sc, st, dxb, True)
+    rb = fastAgg.tgat_attn_bwd(*args, 0.2, None, 0, 0.0, None, sc, st, dxb, True, tdot)
+    for x, y, name in zip(ra, rb, ("dqt", "d_node", "d_time_w", "d_time_b")):
+        assert_rel(y, x.double(), FP32_TOL, f"tdot backward {name}")

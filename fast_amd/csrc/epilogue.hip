@@ -14,6 +14,7 @@ namespace {
 
 constexpr int kMaxPer = 4;          // columns per lane: rows up to 256 wide
 constexpr int kEpiMaxBlocks = 1024;  // grid cap (rows of the weight-gradient partials)
+constexpr int kEpiRowBlocks = 2048;  // grid cap of the forward's half-wave form (8 waves per SIMD)
 
 struct EpiParams {
   int64_t n;
@@ -75,6 +76,74 @@ __global__ __launch_bounds__(kBlock) void epilogue_fwd(EpiParams P) {
     if (lane == 0) {
       P.stats[2 * r] = mean;
       P.stats[2 * r + 1] = rstd;
+    }
+  }
+}
+
+// Rows of whole chunks (d % 4 == 0, d <= 128, 16-byte aligned rows): a half-wave per row,
+// lane l holding columns 4l .. 4l+3 as one float4; two rows per half-wave and iteration, so
+// four rows' loads are in flight per wave.
+constexpr int kEpiRows = 2;   // rows per half-wave and iteration
+
+__device__ __forceinline__ float4 f4_load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+__global__ __launch_bounds__(kBlock) void epilogue_fwd_h(EpiParams P) {
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int c = 4 * hl;
+  const bool on = c < P.d;
+  const float inv_d = 1.f / static_cast<float>(P.d);
+  const float4 gm = on ? f4_load(P.gamma + c) : f4_zero();
+  const float4 bt = on ? f4_load(P.beta + c) : f4_zero();
+  const float4 bs = (on && P.bias) ? f4_load(P.bias + c) : f4_zero();
+  const int64_t slots = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * 2;  // half-waves
+  const int64_t first = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave)) * 2 + half;
+  // the loop runs on the wave's first row, so both halves take every iteration (the
+  // half-wave sums need the whole wave)
+  for (int64_t rb = first - half; rb < P.n; rb += kEpiRows * slots) {
+    const int64_t r0 = rb + half;
+    float4 u[kEpiRows];
+#pragma unroll
+    for (int i = 0; i < kEpiRows; ++i) {
+      const int64_t r = r0 + i * slots;
+      float4 a = f4_zero();
+      if (on && r < P.n) {
+        a = f4_load(P.r1 + r * P.ld1 + c);
+        if (P.r2) {
+          const float4 b = f4_load(P.r2 + r * P.ld2 + c);
+          a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+        }
+      }
+      u[i] = a;
+    }
+#pragma unroll
+    for (int i = 0; i < kEpiRows; ++i) {
+      const int64_t r = r0 + i * slots;
+      float4 a = u[i];
+      a.x += bs.x; a.y += bs.y; a.z += bs.z; a.w += bs.w;
+      if (P.drop) {
+        const uint64_t e = static_cast<uint64_t>(r * P.d + c);
+        a.x *= drop_mult(P.seed, e, P.p, P.scale);
+        a.y *= drop_mult(P.seed, e + 1, P.p, P.scale);
+        a.z *= drop_mult(P.seed, e + 2, P.p, P.scale);
+        a.w *= drop_mult(P.seed, e + 3, P.p, P.scale);
+      }
+      a = make_float4(a.x > 0.f ? a.x : 0.f, a.y > 0.f ? a.y : 0.f, a.z > 0.f ? a.z : 0.f,
+                      a.w > 0.f ? a.w : 0.f);
+      if (!on) a = f4_zero();
+      const float mean = half_sum(a.x + a.y + a.z + a.w) * inv_d;
+      const float4 dv = on ? make_float4(a.x - mean, a.y - mean, a.z - mean, a.w - mean) : f4_zero();
+      const float rstd = 1.f / sqrtf(half_sum(dv.x * dv.x + dv.y * dv.y + dv.z * dv.z + dv.w * dv.w) * inv_d + P.eps);
+      if (on && r < P.n) {
+        *reinterpret_cast<float4*>(P.y + r * P.d + c) = a;
+        *reinterpret_cast<float4*>(P.out + r * P.d + c) =
+            make_float4(dv.x * rstd * gm.x + bt.x, dv.y * rstd * gm.y + bt.y,
+                        dv.z * rstd * gm.z + bt.z, dv.w * rstd * gm.w + bt.w);
+      }
+      if (hl == 0 && r < P.n) {
+        P.stats[2 * r] = mean;
+        P.stats[2 * r + 1] = rstd;
+      }
     }
   }
 }
@@ -175,6 +244,43 @@ int epi_grid(int64_t n) {
   return static_cast<int>(want < kEpiMaxBlocks ? (want < 1 ? 1 : want) : kEpiMaxBlocks);
 }
 
+// The same for rows of whole chunks up to 128 wide (cols % 4 == 0, 16-byte aligned rows): a
+// half-wave per row, lane l multiplying columns 4l .. 4l+3; each group's products are
+// summed over the half-wave in a fixed order.
+__global__ __launch_bounds__(kBlock) void row_group_dots_h(int64_t n, int groups, int width,
+                                                          const float* a, int64_t lda,
+                                                          const float* b, int64_t ldb, float* out) {
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int cols = groups * width;
+  const int c = 4 * hl;
+  const bool on = c < cols;
+  int gi[4];  // group of each of the lane's four columns
+#pragma unroll
+  for (int i = 0; i < 4; ++i) gi[i] = (c + i) / width;
+  const int64_t slots = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * 2;
+  // the loop runs on the wave's first row, so both halves take every iteration
+  for (int64_t r = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave)) * 2 + half;
+       r - half < n; r += slots) {
+    float p[4] = {0.f, 0.f, 0.f, 0.f};
+    if (on && r < n) {
+      const float4 x = *reinterpret_cast<const float4*>(a + r * lda + c);
+      const float4 y = *reinterpret_cast<const float4*>(b + r * ldb + c);
+      p[0] = x.x * y.x;
+      p[1] = x.y * y.y;
+      p[2] = x.z * y.z;
+      p[3] = x.w * y.w;
+    }
+    for (int g = 0; g < groups; ++g) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s += gi[i] == g ? p[i] : 0.f;
+      s = half_sum(s);
+      if (hl == 0 && r < n) out[r * groups + g] = s;
+    }
+  }
+}
+
 // out[r][g] = sum_j a[r][g*width + j] * b[r][g*width + j]: one wave per row (grid-stride),
 // a fixed-order wave sum per group.
 __global__ __launch_bounds__(kBlock) void row_group_dots(int64_t n, int groups, int width,
@@ -213,6 +319,15 @@ extern "C" int fa_tgat_epilogue_fwd_f32(int64_t n, int32_t d, const float* r1, i
   P.eps = eps; P.drop = drop_p > 0.f; P.seed = drop_seed; P.p = drop_p;
   P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
   P.out = out; P.y = y; P.stats = stats;
+  const bool rows4 = !(d & 3) && d <= 4 * kHalf && aligned16(r1) && !(ld1 & 3) &&
+                     (!r2 || (aligned16(r2) && !(ld2 & 3))) && (!bias || aligned16(bias)) &&
+                     aligned16(gamma) && aligned16(beta) && aligned16(out) && aligned16(y);
+  if (rows4) {
+    const int64_t want = ceil_div(n, 2 * kWavesPerBlock * kEpiRows);
+    const int g = static_cast<int>(want < kEpiRowBlocks ? want : kEpiRowBlocks);
+    hipLaunchKernelGGL(epilogue_fwd_h, dim3(g), dim3(kBlock), 0, stream, P);
+    return launch_status();
+  }
   const dim3 grid(epi_grid(n));
   switch (static_cast<int>(ceil_div(d, kWave))) {
     case 1: hipLaunchKernelGGL(epilogue_fwd<1>, grid, dim3(kBlock), 0, stream, P); break;
@@ -230,6 +345,13 @@ extern "C" int fa_row_group_dots_f32(int64_t n, int32_t groups, int32_t width, c
   if (n == 0) return FA_OK;
   const int64_t cols = static_cast<int64_t>(groups) * width;
   if (!a || !b || !out || lda < cols || ldb < cols) return FA_EINVAL;
+  if (!(cols & 3) && cols <= 4 * kHalf && aligned16(a) && aligned16(b) && !(lda & 3) && !(ldb & 3)) {
+    const int64_t want = ceil_div(n, 2 * kWavesPerBlock);
+    const int g = static_cast<int>(want < kEpiRowBlocks ? want : kEpiRowBlocks);
+    hipLaunchKernelGGL(row_group_dots_h, dim3(static_cast<unsigned>(g)), dim3(kBlock), 0, stream, n,
+                       groups, width, a, lda, b, ldb, out);
+    return launch_status();
+  }
   hipLaunchKernelGGL(row_group_dots, dim3(static_cast<unsigned>(epi_grid(n))), dim3(kBlock), 0,
                      stream, n, groups, width, a, lda, b, ldb, out);
   return launch_status();

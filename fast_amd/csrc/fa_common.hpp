@@ -72,6 +72,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return lane_read(v, 63);
 }
 
+constexpr int kHalf = 32;  // lanes of a half-wave
+
+// Sum over each half-wave: every lane of rows 1 / 3 ends with its half's total; lanes 31
+// and 63 are read back, so the result is uniform per half.
+__device__ __forceinline__ float half_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_bcast<kRowBcast15, 0xA>(v);
+  const float s0 = lane_read(v, 31), s1 = lane_read(v, 63);
+  return (threadIdx.x & (kWave - 1)) < kHalf ? s0 : s1;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = row16_max(v);
   return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)),

@@ -554,7 +554,6 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
 // 0). Dynamic LDS: the time weights [dt_dim] (w, b), then per wave two time-tile rows
 // [2][tvs].
 // ---------------------------------------------------------------------------------
-constexpr int kHalf = 32;
 
 template <int NS>
 struct PairCtx {
@@ -620,15 +619,6 @@ __device__ __forceinline__ void pair_time(float t, float2 wb, float* row, int d,
 __device__ __forceinline__ int pick_int(int v, int j) { return __builtin_amdgcn_ds_bpermute(j << 2, v); }
 __device__ __forceinline__ float pick_flt(float v, int j) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(j << 2, __float_as_int(v)));
-}
-
-// Sum over each half: every lane of rows 1 / 3 ends with its half's total; lanes 31 and 63
-// are read back, so the result is uniform per half.
-__device__ __forceinline__ float half_sum(float v) {
-  v = row16_sum(v);
-  v += dpp_bcast<kRowBcast15, 0xA>(v);
-  const float s0 = lane_read(v, 31), s1 = lane_read(v, 63);
-  return lane_id() < kHalf ? s0 : s1;
 }
 
 // One chunk of a table row at `row + off` (float32, or bf16 widened).

@@ -738,6 +738,94 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
   return out;
 }
 
+static const float* opt_ptr(const std::optional<at::Tensor>& t, int64_t numel, const char* name) {
+  if (!t.has_value() || !t->defined()) return nullptr;
+  CHECK_INPUT((*t));
+  CHECK_DTYPE((*t), at::kFloat);
+  TORCH_CHECK(t->numel() == numel, name, ": wrong size");
+  return t->data_ptr<float>();
+}
+
+static void check_param(const at::Tensor& t, int64_t rows, int64_t cols, const char* name) {
+  CHECK_INPUT(t);
+  CHECK_DTYPE(t, at::kFloat);
+  TORCH_CHECK(t.numel() == rows * cols, name, ": wrong size");
+}
+
+// -> [wq_node, wk_aug, wv_aug, qbk, wo1, wo2]
+std::vector<at::Tensor> layer_params_fwd(at::Tensor wq, at::Tensor bq, at::Tensor wk,
+                                         at::Tensor bk, at::Tensor wv, at::Tensor bv,
+                                         std::optional<at::Tensor> bt, at::Tensor wo,
+                                         int64_t heads, int64_t dn, int64_t de, int64_t dt) {
+  const int64_t d = bq.numel();
+  const int64_t kp = fa_tgat_kspace(static_cast<int32_t>(dn), static_cast<int32_t>(de),
+                                    static_cast<int32_t>(dt));
+  check_param(wq, d, dn + dt, "wq");
+  check_param(bq, d, 1, "bq");
+  check_param(wk, d, dn + de + dt, "wk");
+  check_param(bk, d, 1, "bk");
+  check_param(wv, d, dn + de + dt, "wv");
+  check_param(bv, d, 1, "bv");
+  check_param(wo, d, d + dn, "wo");
+  const float* btp = opt_ptr(bt, dt, "bt");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(wq.device());
+  auto o = wq.options();
+  auto wq_node = at::empty({d, dn}, o), wk_aug = at::empty({d, kp}, o), wv_aug = at::empty({d, kp}, o);
+  auto qbk = at::empty({heads, kp}, o), wo1 = at::empty({d, d}, o), wo2 = at::empty({d, dn}, o);
+  const int st = fa_layer_params_fwd_f32(
+      static_cast<int32_t>(d), static_cast<int32_t>(heads), static_cast<int32_t>(dn),
+      static_cast<int32_t>(de), static_cast<int32_t>(dt), wq.data_ptr<float>(), dn + dt,
+      bq.data_ptr<float>(), wk.data_ptr<float>(), dn + de + dt, bk.data_ptr<float>(),
+      wv.data_ptr<float>(), dn + de + dt, bv.data_ptr<float>(), btp, wo.data_ptr<float>(), d + dn,
+      wq_node.data_ptr<float>(), wk_aug.data_ptr<float>(), wv_aug.data_ptr<float>(),
+      qbk.data_ptr<float>(), wo1.data_ptr<float>(), wo2.data_ptr<float>(),
+      at::empty({2 * d}, o).data_ptr<float>(), stream_of(wq));
+  check_status(st, "layer_params_fwd");
+  return {wq_node, wk_aug, wv_aug, qbk, wo1, wo2};
+}
+
+// -> [d_wq, d_bq, d_wk, d_bk, d_wv, d_bv, d_bt, d_wo]
+std::vector<at::Tensor> layer_params_bwd(at::Tensor wq, at::Tensor bq, at::Tensor wk,
+                                         at::Tensor bk, std::optional<at::Tensor> bt,
+                                         std::optional<at::Tensor> g_wq_node,
+                                         std::optional<at::Tensor> g_wk_aug,
+                                         std::optional<at::Tensor> g_wv_aug,
+                                         std::optional<at::Tensor> g_qbk,
+                                         std::optional<at::Tensor> g_wo1,
+                                         std::optional<at::Tensor> g_wo2, int64_t heads,
+                                         int64_t dn, int64_t de, int64_t dt) {
+  const int64_t d = bq.numel();
+  const int64_t kp = fa_tgat_kspace(static_cast<int32_t>(dn), static_cast<int32_t>(de),
+                                    static_cast<int32_t>(dt));
+  check_param(wq, d, dn + dt, "wq");
+  check_param(bq, d, 1, "bq");
+  check_param(wk, d, dn + de + dt, "wk");
+  check_param(bk, d, 1, "bk");
+  const float* btp = opt_ptr(bt, dt, "bt");
+  const float* p_wq = opt_ptr(g_wq_node, d * dn, "g_wq_node");
+  const float* p_wk = opt_ptr(g_wk_aug, d * kp, "g_wk_aug");
+  const float* p_wv = opt_ptr(g_wv_aug, d * kp, "g_wv_aug");
+  const float* p_qb = opt_ptr(g_qbk, heads * kp, "g_qbk");
+  const float* p_o1 = opt_ptr(g_wo1, d * d, "g_wo1");
+  const float* p_o2 = opt_ptr(g_wo2, d * dn, "g_wo2");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(wq.device());
+  auto o = wq.options();
+  auto d_wq = at::empty({d, dn + dt}, o), d_bq = at::empty({d}, o);
+  auto d_wk = at::empty({d, dn + de + dt}, o), d_bk = at::empty({d}, o);
+  auto d_wv = at::empty({d, dn + de + dt}, o), d_bv = at::empty({d}, o);
+  auto d_bt = at::empty({dt}, o), d_wo = at::empty({d, d + dn}, o);
+  const int st = fa_layer_params_bwd_f32(
+      static_cast<int32_t>(d), static_cast<int32_t>(heads), static_cast<int32_t>(dn),
+      static_cast<int32_t>(de), static_cast<int32_t>(dt), wq.data_ptr<float>(), dn + dt,
+      bq.data_ptr<float>(), wk.data_ptr<float>(), dn + de + dt, bk.data_ptr<float>(), btp, p_wq,
+      p_wk, p_wv, p_qb, p_o1, p_o2, d_wq.data_ptr<float>(), d_bq.data_ptr<float>(),
+      d_wk.data_ptr<float>(), d_bk.data_ptr<float>(), d_wv.data_ptr<float>(),
+      d_bv.data_ptr<float>(), dt > 0 ? d_bt.data_ptr<float>() : nullptr, d_wo.data_ptr<float>(),
+      at::empty({2 * d}, o).data_ptr<float>(), stream_of(wq));
+  check_status(st, "layer_params_bwd");
+  return {d_wq, d_bq, d_wk, d_bk, d_wv, d_bv, d_bt, d_wo};
+}
+
 // [n, groups]: dot products of a's and b's column groups of `width` per row.
 at::Tensor row_group_dots(at::Tensor a, at::Tensor b, int64_t groups) {
   CHECK_INPUT(a);
@@ -999,6 +1087,13 @@ PYBIND11_MODULE(fastAgg, m) {
   m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2 + bias)))",
         py::arg("r1"), py::arg("r2"), py::arg("bias"), py::arg("gamma"), py::arg("beta"),
         py::arg("eps"), py::arg("drop_seed"), py::arg("drop_p"));
+  m.def("layer_params_fwd", &layer_params_fwd, "per-step weight layouts of one layer",
+        py::arg("wq"), py::arg("bq"), py::arg("wk"), py::arg("bk"), py::arg("wv"), py::arg("bv"),
+        py::arg("bt"), py::arg("wo"), py::arg("heads"), py::arg("dn"), py::arg("de"), py::arg("dt"));
+  m.def("layer_params_bwd", &layer_params_bwd, "backward of layer_params_fwd", py::arg("wq"),
+        py::arg("bq"), py::arg("wk"), py::arg("bk"), py::arg("bt"), py::arg("g_wq_node"),
+        py::arg("g_wk_aug"), py::arg("g_wv_aug"), py::arg("g_qbk"), py::arg("g_wo1"),
+        py::arg("g_wo2"), py::arg("heads"), py::arg("dn"), py::arg("de"), py::arg("dt"));
   m.def("row_group_dots", &row_group_dots, "per-row dot products of column groups",
         py::arg("a"), py::arg("b"), py::arg("groups"));
   m.def("tgat_epilogue_bwd", &tgat_epilogue_bwd, "backward of tgat_epilogue_fwd", py::arg("dout"),

@@ -497,8 +497,8 @@ class RowsMM(torch.autograd.Function):
         dy = dy.contiguous()
         dx = dy @ W if ctx.needs_input_grad[0] else None
         dW = None
-        if ctx.needs_input_grad[1]:
-            dW = fastAgg.head_wgrad(x, dy.unsqueeze(0), 1, False)[0].t()
+        if ctx.needs_input_grad[1]:   # dy^T x, written [M, K] (no transposed view)
+            dW = fastAgg.head_wgrad(dy, x.unsqueeze(0), 1, False)[0]
         return dx, dW
 
 
@@ -529,11 +529,36 @@ class DstProj(torch.autograd.Function):
                     dh.addmm_(dr, Wr)
             elif dr is not None:
                 dh = dr @ Wr
+        hc = h.contiguous() if (ctx.needs_input_grad[1] or ctx.needs_input_grad[2]) else h
         if ctx.needs_input_grad[1] and dq is not None:
-            dWq = fastAgg.head_wgrad(h, dq.unsqueeze(0), 1, False)[0].t()
+            dWq = fastAgg.head_wgrad(dq, hc.unsqueeze(0), 1, False)[0]
         if ctx.needs_input_grad[2] and dr is not None:
-            dWr = fastAgg.head_wgrad(h, dr.unsqueeze(0), 1, False)[0].t()
+            dWr = fastAgg.head_wgrad(dr, hc.unsqueeze(0), 1, False)[0]
         return dh, dWq, dWr
+
+
+class LayerParams(torch.autograd.Function):
+    """The layer's weights in the forms the step uses, one kernel each way
+    (fastAgg.layer_params_fwd / _bwd): W_q[:, :Dn]; W_k and W_v with their biases in the
+    K-space layout; qbk[h] = qb[h-block] W_k,aug[h-block] with the query bias
+    qb = b_q + W_q[:, Dn:] cos(b_t) (layers.py:109-110); W_o[:, :D] and W_o[:, D:]."""
+
+    @staticmethod
+    def forward(ctx, wq, bq, wk, bk, wv, bv, bt, wo, dims):
+        heads, dn, de, dt = dims
+        ctx.dims = dims
+        ctx.save_for_backward(wq, bq, wk, bk, bt if bt is not None else wq.new_empty(0))
+        return tuple(fastAgg.layer_params_fwd(wq, bq, wk, bk, wv, bv, bt, wo, heads, dn, de, dt))
+
+    @staticmethod
+    def backward(ctx, g_wq, g_wk, g_wv, g_qbk, g_wo1, g_wo2):
+        heads, dn, de, dt = ctx.dims
+        wq, bq, wk, bk, bt = ctx.saved_tensors
+        c = lambda t: t.contiguous() if t is not None else None
+        d_wq, d_bq, d_wk, d_bk, d_wv, d_bv, d_bt, d_wo = fastAgg.layer_params_bwd(
+            wq, bq, wk, bk, bt if dt > 0 else None, c(g_wq), c(g_wk), c(g_wv), c(g_qbk),
+            c(g_wo1), c(g_wo2), heads, dn, de, dt)
+        return d_wq, d_bq, d_wk, d_bk, d_wv, d_bv, (d_bt if dt > 0 else None), d_wo, None
 
 
 # ---------------------------------------------------------------------------------------
@@ -613,17 +638,23 @@ class TransfomerAttentionLayer(torch.nn.Module):
             if Dn > 0:
                 node_src, node_idx = b.src_node_source()
         kp = kspace_width(Dn, De, Dt)
-        # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h].
-        wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
         Wo = self.w_out.weight
         r2 = None
         if Dn > 0:
-            # q = hdst W_q[:, :Dn]^T (its bias folded into qt's: qb[h] W_k,aug[h]) and the
-            # h_dst half of w_out, from one product
-            q, r2 = DstProj.apply(hdst, self.w_q.weight[:, :Dn], Wo[:, D:])
-            qbk = torch.bmm(self._query_bias().view(H, 1, dh), wk).view(H, kp)
+            # the weights in K-space form, the query bias folded into qt's (qbk), w_out's
+            # halves; one kernel each way
+            wq_node, wk, wv, qbk, wo1, wo2 = LayerParams.apply(
+                self.w_q.weight, self.w_q.bias, self.w_k.weight, self.w_k.bias, self.w_v.weight,
+                self.w_v.bias, self.time_enc.w.bias if Dt > 0 else None, Wo, (H, Dn, De, Dt))
+            wk, wv = wk.view(H, dh, kp), wv.view(H, dh, kp)
+            # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h], with
+            # q = hdst W_q[:, :Dn]^T and the h_dst half of w_out from one product
+            q, r2 = DstProj.apply(hdst, wq_node, wo2)
             qt = HeadProj.apply(q, wk, qbk)
         else:  # one query for every destination: the time part alone (or 1, layers.py:137-140)
+            wk = to_kspace(self.w_k.weight, self.w_k.bias, Dn, De, Dt).view(H, dh, kp)
+            wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
+            wo1 = Wo[:, :D]
             q1 = self._query_bias() if Dt > 0 else torch.ones(D, device=dev)
             qt = HeadProj.apply(q1.view(1, D), wk, None).expand(H, N, kp)
 
@@ -649,9 +680,8 @@ class TransfomerAttentionLayer(torch.nn.Module):
         # Absorbed values, head by head: agg[v, h, :] = W_v,aug[h] xbar[h, v, :], then
         # rst = w_out([agg | hdst]) as agg W_o[:, :D]^T + hdst W_o[:, D:]^T + b_o (the
         # bias and the sum in the epilogue kernel).
-        wv = to_kspace(self.w_v.weight, self.w_v.bias, Dn, De, Dt).view(H, dh, kp)
         agg = HeadReduce.apply(xbar, wv, link)
-        r1 = RowsMM.apply(agg, Wo[:, :D])
+        r1 = RowsMM.apply(agg, wo1)
         ln = self.layer_norm
         return TgatEpilogue.apply(r1, r2, self.w_out.bias, ln.weight, ln.bias, ln.eps,
                                   out_drop_seed, out_drop_p)

@@ -312,6 +312,31 @@ int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout, const floa
 int fa_row_group_dots_f32(int64_t n, int32_t groups, int32_t width, const float* a, int64_t lda,
                           const float* b, int64_t ldb, float* out, hipStream_t stream);
 
+/* Per-step parameter preparation of one layer (new op: the reference applies w_q, w_k, w_v,
+ * w_out and the time encoding directly, layers.py:105-169; here their weights enter the
+ * fused path in K-space form). d = dim_out, dn/de/dt the input widths, all row-major float32:
+ * W_q [d][dn+dt] (row stride ldq), W_k, W_v [d][dn+de+dt], W_o [d][d+dn], b_t [dt].
+ * Forward outputs: wq_node = W_q[:, :dn] [d][dn]; wk_aug, wv_aug [d][Kp] (= [heads][d/heads][Kp],
+ * fa_tgat_kspace layout, bias at column Kp-4); qbk [heads][Kp] = qb[h-block] wk_aug[h-block] with
+ * qb = b_q + W_q[:, dn:] cos(b_t); wo1 = W_o[:, :d] [d][d]; wo2 = W_o[:, d:] [d][dn].
+ * Backward: the gradients of the forward's inputs from those of its outputs (each g_* may be
+ * NULL for a zero gradient); d_* are written whole. dn > 0, d <= 512. scratch: 2*d floats
+ * (FA_ESCRATCH when NULL). */
+int fa_layer_params_fwd_f32(int32_t d, int32_t heads, int32_t dn, int32_t de, int32_t dt,
+                            const float* wq, int64_t ldq, const float* bq, const float* wk,
+                            int64_t ldk, const float* bk, const float* wv, int64_t ldv,
+                            const float* bv, const float* bt, const float* wo, int64_t ldo,
+                            float* wq_node, float* wk_aug, float* wv_aug, float* qbk, float* wo1,
+                            float* wo2, float* scratch, hipStream_t stream);
+int fa_layer_params_bwd_f32(int32_t d, int32_t heads, int32_t dn, int32_t de, int32_t dt,
+                            const float* wq, int64_t ldq, const float* bq, const float* wk,
+                            int64_t ldk, const float* bk, const float* bt,
+                            const float* g_wq_node, const float* g_wk_aug, const float* g_wv_aug,
+                            const float* g_qbk, const float* g_wo1, const float* g_wo2,
+                            float* d_wq, float* d_bq, float* d_wk, float* d_bk, float* d_wv,
+                            float* d_bv, float* d_bt, float* d_wo, float* scratch,
+                            hipStream_t stream);
+
 /* Row gather: out[i, :dim] = tab[idx[i], :dim] (idx NULL => i). */
 int fa_gather_rows_f32(const float* tab, int64_t ld_tab, int64_t n_tab, const int64_t* idx,
                        int64_t n, int32_t dim, float* out, int64_t ld_out, hipStream_t stream);

@@ -432,3 +432,44 @@ def test_backward_with_tdot_matches_xbar(dev, heads):
     rb = fastAgg.tgat_attn_bwd(*args, 0.2, None, 0, 0.0, None, sc, st, dxb, True, tdot)
     for x, y, name in zip(ra, rb, ("dqt", "d_node", "d_time_w", "d_time_b")):
         assert_rel(y, x.double(), FP32_TOL, f"tdot backward {name}")
+
+
+@pytest.mark.parametrize("dims", [(100, 172, 100, 2, 100), (13, 6, 0, 8, 64), (8, 0, 4, 2, 8),
+                                  (413, 186, 100, 8, 256)])
+def test_layer_params_match_torch(dev, dims):
+    """The per-step weight preparation (fastAgg.layer_params_fwd / _bwd through
+    tgat.LayerParams) against the same formulas in float64 torch autograd on the CPU:
+    K-space weights, the folded query bias product qbk, the w_q / w_out slices, and every
+    parameter gradient for random upstream gradients."""
+    from fast_amd.tgat import LayerParams, TransfomerAttentionLayer, to_kspace
+
+    dn, de, dt, H, D = dims
+    torch.manual_seed(7)
+    layer = TransfomerAttentionLayer(dn, de, dt, H, 0.0, 0.0, D)
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.add_(0.1 * torch.randn_like(p))   # non-zero biases everywhere
+    names = ["w_q.weight", "w_q.bias", "w_k.weight", "w_k.bias", "w_v.weight", "w_v.bias",
+             "time_enc.w.bias", "w_out.weight"]
+    pd = dict(layer.named_parameters())
+    cpu = [pd[n].detach() if n in pd else None for n in names]
+    gpu = [t.to(dev).requires_grad_(True) if t is not None else None for t in cpu]
+    ref = [t.double().requires_grad_(True) if t is not None else None for t in cpu]
+    outs = LayerParams.apply(*gpu, (H, dn, de, dt))
+    wq, bq, wk, bk, wv, bv, bt, wo = ref
+    qb = bq + (wq[:, dn:] @ torch.cos(bt) if dt > 0 else 0)
+    wk_aug = to_kspace(wk, bk, dn, de, dt)
+    kp = wk_aug.shape[1]
+    qbk = torch.bmm(qb.view(H, 1, D // H), wk_aug.view(H, D // H, kp)).view(H, kp)
+    routs = [wq[:, :dn], wk_aug, to_kspace(wv, bv, dn, de, dt), qbk, wo[:, :D], wo[:, D:]]
+    gen = torch.Generator().manual_seed(3)
+    ups = [torch.randn(r.shape, generator=gen, dtype=torch.float64) for r in routs]
+    for o, r, name in zip(outs, routs, ["wq_node", "wk_aug", "wv_aug", "qbk", "wo1", "wo2"]):
+        assert o.shape == r.shape, name
+        assert_rel(o, r, FP32_TOL, f"layer params {name}")
+    torch.autograd.backward(list(outs), [u.float().to(dev) for u in ups])
+    torch.autograd.backward(routs, ups)
+    for g, r, name in zip(gpu, ref, names):
+        if g is None:
+            continue
+        assert_rel(g.grad, r.grad, FP32_TOL, f"layer params grad {name}")

@@ -503,6 +503,35 @@ __global__ __launch_bounds__(kBlock) void chunk_sums(const float* part, int chun
   }
 }
 
+// The same, four consecutive outputs per thread (stride and out 16-byte aligned, stride a
+// multiple of 4): 32 outputs per workgroup (8 threads of float4), 32 threads per output
+// each summing every 32nd chunk, then the 32 partial sums in order through LDS.
+constexpr int kSumOut4 = 8;                  // float4 outputs per workgroup
+constexpr int kSumGroups = kBlock / kSumOut4;  // chunk groups
+
+__global__ __launch_bounds__(kBlock) void chunk_sums4(const float* part, int chunks, int64_t stride,
+                                                      float* out) {
+  __shared__ float4 red[kSumGroups][kSumOut4];
+  const int o = threadIdx.x % kSumOut4, kg = threadIdx.x / kSumOut4;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * kSumOut4 + o) * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i < stride)
+    for (int k = kg; k < chunks; k += kSumGroups) {
+      const float4 v = *reinterpret_cast<const float4*>(part + k * stride + i);
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+  red[kg][o] = s;
+  __syncthreads();
+  if (kg == 0 && i < stride) {
+    float4 t = red[0][o];
+    for (int q = 1; q < kSumGroups; ++q) {
+      const float4 v = red[q][o];
+      t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+    }
+    *reinterpret_cast<float4*>(out + i) = t;
+  }
+}
+
 constexpr int kGemmBlocks = 1024;  // workgroups of the row-tile launches
 constexpr size_t kMaxReduceLds = 160 * 1024;
 
@@ -677,6 +706,11 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
 #undef FA_WG_NW
   if (!k) return FA_EUNSUPPORTED;
   hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(nw * kWave)), 0, stream, P);
+  if (!(out & 3) && aligned16(dw) && aligned16(scratch)) {
+    hipLaunchKernelGGL(chunk_sums4, dim3(static_cast<unsigned>(ceil_div(out, 4 * kSumOut4))), dim3(kBlock), 0,
+                       stream, static_cast<const float*>(P.part), static_cast<int>(used), out, dw);
+    return launch_status();
+  }
   hipLaunchKernelGGL(chunk_sums, dim3(static_cast<unsigned>(ceil_div(out, 32))), dim3(kBlock), 0,
                      stream, static_cast<const float*>(P.part), static_cast<int>(used), out, dw);
   return launch_status();

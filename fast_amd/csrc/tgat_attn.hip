@@ -941,8 +941,6 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     stage_meta<H, true>(P, c0, cnt, M);
     load_rows<H, NS>(P.qt, P.qt_rs, P.qt_hs, v, P.kp, S.q);
     load_rows<H, NS>(P.dxbar, P.dxbar_rs, P.dxbar_hs, v, P.kp, S.g);
-    float4 xr[H][NS];
-    if (!P.tdot) load_rows<H, NS>(P.xbar, P.xbar_rs, P.xbar_hs, v, P.kp, xr);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       S.mh[h] = P.stats[(v * H + h) * 2 + 0];
@@ -950,9 +948,19 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     }
     float4 xa[kBatch][NS], xb[kBatch][NS];
     issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
+    if (P.tdot) {
 #pragma unroll
-    for (int h = 0; h < H; ++h)
-      S.T[h] = P.tdot ? P.tdot[v * H + h] : wave_sum(row_dot<NS>(S.g[h], xr[h]));
+      for (int h = 0; h < H; ++h) S.T[h] = P.tdot[v * H + h];
+    } else {  // head by head: one x-bar row in registers at a time
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const rsrc_t rr = make_rsrc(P.xbar + v * P.xbar_rs + h * P.xbar_hs, 4u * static_cast<uint32_t>(P.kp));
+        float d = 0.f;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) d += dot4(S.g[h][k], bload4(rr, 16u * static_cast<uint32_t>(lane_id() + k * kWave)));
+        S.T[h] = wave_sum(d);
+      }
+    }
     for (;;) {
       for (int jb = 0; jb < cnt; jb += 2 * kBatch) {
         const int na = cnt - jb < kBatch ? cnt - jb : kBatch;

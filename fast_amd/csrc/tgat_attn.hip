@@ -767,15 +767,30 @@ __global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
     int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
     EdgeMeta<H, false> M;
     stage_meta<H, false>(P, c0, cnt, M);
-    lds_sync();  // the previous destination's reads of qs are done
+    // the q~ rows' loads, then the first pair's row loads (which wait for the staged ids),
+    // are all in flight before the q~ rows go to LDS
+    constexpr int QR = (NS * kHalf + kWave - 1) / kWave;  // q~ chunks per lane and head
+    float4 qv[H][QR];
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       const float4* src = reinterpret_cast<const float4*>(P.qt + v * P.qt_rs + h * P.qt_hs);
-      for (int c = lane; c < P.cp; c += kWave) qs[h * NS * kHalf + c] = src[c];
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        const int c = lane + r * kWave;
+        qv[h][r] = c < P.cp ? src[c] : f4_zero();
+      }
     }
-    lds_sync();
     float4 xa[NS], xb[NS];
     pair_rows<NS, H, false>(P, L, M, 0, cnt, xa);
+    lds_sync();  // the previous destination's reads of qs are done
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+      for (int r = 0; r < QR; ++r) {
+        const int c = lane + r * kWave;
+        if (c < P.cp) qs[h * NS * kHalf + c] = qv[h][r];
+      }
+    lds_sync();
     for (;;) {
       const int np = (cnt + 1) >> 1;
       for (int p = 0; p < np; p += 2) {
@@ -1176,9 +1191,22 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
       const float4* gr = reinterpret_cast<const float4*>(P.dxbar + v * P.dxbar_rs + h * P.dxbar_hs);
       float d = 0.f;
       if (P.tdot) {
-        for (int c = lane; c < P.cp; c += kWave) {
-          qs[h * QS + c] = qr[c];
-          gs[h * QS + c] = gr[c];
+        // every load of the two rows first, then the LDS writes
+        constexpr int QR = (NS * kHalf + kWave - 1) / kWave;
+        float4 qv[QR], gv[QR];
+#pragma unroll
+        for (int r = 0; r < QR; ++r) {
+          const int c = lane + r * kWave;
+          qv[r] = c < P.cp ? qr[c] : f4_zero();
+          gv[r] = c < P.cp ? gr[c] : f4_zero();
+        }
+#pragma unroll
+        for (int r = 0; r < QR; ++r) {
+          const int c = lane + r * kWave;
+          if (c < P.cp) {
+            qs[h * QS + c] = qv[r];
+            gs[h * QS + c] = gv[r];
+          }
         }
         S.T[h] = P.tdot[v * H + h];
       } else {

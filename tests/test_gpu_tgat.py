@@ -473,3 +473,25 @@ def test_layer_params_match_torch(dev, dims):
         if g is None:
             continue
         assert_rel(g.grad, r.grad, FP32_TOL, f"layer params grad {name}")
+
+
+def test_to_blocks_on_device_match_host(dev):
+    """The pinned, packed transfer gives the same blocks on the GPU as on the host, for more
+    results than staging buffers (buffer reuse after its copy finished), and a layer runs
+    on them with the offsets derived on the device."""
+    from fast_amd.mfg import PinnedStager, to_blocks
+    from tests.test_host import _FakeSample
+
+    ret = [_FakeSample(40 + i, 3 + i, i) for i in range(5)]
+    cpu = to_blocks(ret, device="cpu")
+    gpu = to_blocks(ret, device=dev, stager=PinnedStager(buffers=2))
+    for gc, gg in zip(cpu, gpu):
+        for bc, bg in zip(gc, gg):
+            for a, b in zip(bc.edges(), bg.edges()):
+                assert torch.equal(a, b.cpu())
+            for k in ("ID", "ts"):
+                assert torch.equal(bc.srcdata[k], bg.srcdata[k].cpu())
+            for k in ("dt", "ID"):
+                assert torch.equal(bc.edata[k], bg.edata[k].cpu())
+            rp = bg.rowptr().cpu()
+            assert int(rp[-1]) == bc.num_edges() and bool((rp[1:] >= rp[:-1]).all())

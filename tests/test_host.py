@@ -197,3 +197,53 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+class _FakeSample:
+    """A sampler result with the FAST sampler's accessors (sampler_core.cpp): dim_out
+    destinations, `deg` edges each, edge e from source node dim_out + e."""
+
+    def __init__(self, dim_out, deg, seed):
+        rng = np.random.default_rng(seed)
+        E = dim_out * deg
+        self._row = np.repeat(np.arange(dim_out, dtype=np.int32), deg)
+        self._col = np.arange(dim_out, dim_out + E, dtype=np.int32)
+        self._nodes = rng.integers(0, 10 ** 6, dim_out + E).astype(np.int64)
+        self._ts = rng.random(dim_out + E).astype(np.float32)
+        self._dts = rng.random(dim_out + E).astype(np.float32)
+        self._eid = rng.integers(0, 10 ** 7, E).astype(np.int64)
+        self._n = (dim_out + E, dim_out)
+
+    def row(self): return self._row
+    def col(self): return self._col
+    def nodes(self): return self._nodes
+    def ts(self): return self._ts
+    def dts(self): return self._dts
+    def eid(self): return self._eid
+    def dim_in(self): return self._n[0]
+    def dim_out(self): return self._n[1]
+
+
+def test_to_blocks_mirrors_to_dgl_blocks():
+    """utils.py:67-87: edges col -> row, dt = dts[num_dst:], ids and ts on the sources, the
+    results grouped `hist` at a time and the groups reversed; reverse=True swaps the roles."""
+    from fast_amd.mfg import to_blocks
+
+    ret = [_FakeSample(5, 3, 0), _FakeSample(2, 4, 1), _FakeSample(3, 2, 2), _FakeSample(4, 1, 3)]
+    groups = to_blocks(ret, hist=2, device="cpu")
+    assert [len(g) for g in groups] == [2, 2]
+    assert groups[0][0].num_dst_nodes() == 3 and groups[1][0].num_dst_nodes() == 5
+    b, r = groups[1][0], ret[0]
+    src, dst = b.edges()
+    assert torch.equal(src, torch.from_numpy(r.col()).long())
+    assert torch.equal(dst, torch.from_numpy(r.row()).long())
+    assert b.num_src_nodes() == r.dim_in() and b.num_edges() == 15
+    assert torch.equal(b.srcdata["ID"], torch.from_numpy(r.nodes()))
+    assert torch.equal(b.srcdata["ts"], torch.from_numpy(r.ts()))
+    assert torch.equal(b.edata["dt"], torch.from_numpy(r.dts())[5:])
+    assert torch.equal(b.edata["ID"], torch.from_numpy(r.eid()))
+    rb = to_blocks(ret[:1], device="cpu", reverse=True)[0][0]
+    s2, d2 = rb.edges()
+    assert torch.equal(s2, torch.from_numpy(r.row()).long()) and rb.num_dst_nodes() == r.dim_in()
+    assert torch.equal(rb.dstdata["ID"], torch.from_numpy(r.nodes()))
+    assert torch.equal(rb.edata["dt"], torch.from_numpy(r.dts())[r.dim_out():])

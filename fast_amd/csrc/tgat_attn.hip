@@ -1277,6 +1277,202 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Head-split forward (4 or 8 heads): a workgroup takes one destination at a time; its four
+// waves gather each batch of kHsBatch edges' K-space rows once, together, into LDS (row
+// chunks by per-lane global loads, the time chunks evaluated in place, the bias chunk), and
+// wave w scores and accumulates heads [w*HG, (w+1)*HG) from LDS with its q~ rows in
+// registers. A lane owns chunks lane + 64k of a row (NS slots). Rows must be chunk loads
+// (modes 0 and 1). Dynamic LDS: the time table [ct + 1][2] float4, then the batch rows
+// [kHsBatch][64 NS] float4.
+// ---------------------------------------------------------------------------------
+constexpr int kHsBatch = 8;
+
+// Read (never written) by gather tasks of non-row chunks and for missing rows; no table row
+// chunk lies past 4 * 192 floats from its row start.
+__device__ __align__(16) float kZeroRow[4 * 3 * kWave];
+
+// Library cosine for arguments outside the fast reduction's range, kept out of line so
+// that its registers do not count against the callers' main path.
+__device__ __attribute__((noinline)) float cos_far(float a) { return cosf(a); }
+
+// The time weights and phases by chunk into LDS, `twt` [ct + 1][2] (w chunk, b chunk; the
+// last entry and the dims past dt_dim zero), for all waves of the workgroup.
+__device__ __forceinline__ void stage_time_table(const TgatParams& P, float* twt) {
+  const int n = 4 * (P.ct + 1);
+  for (int d = threadIdx.x; d < n; d += blockDim.x) {
+    const bool ok = d < P.dt_dim;
+    twt[8 * (d >> 2) + (d & 3)] = ok ? P.time_w[d] : 0.f;
+    twt[8 * (d >> 2) + 4 + (d & 3)] = ok ? P.time_b[d] : 0.f;
+  }
+  __syncthreads();
+}
+
+// Per-edge data of a batch, staged in LDS by one thread per edge: row ids (kNoRow when
+// missing or out of range) and dt.
+struct HsEdge {
+  uint32_t nid, eid;
+  float t;
+};
+
+__device__ __forceinline__ void hs_stage_edges(const TgatParams& P, int64_t c0, int nb, HsEdge* ed) {
+  const int b = threadIdx.x;
+  if (b < nb) {
+    const int64_t e = c0 + b;
+    const int64_t nr = P.node_idx ? P.node_idx[e] : e;
+    const int64_t er = P.edge_idx ? P.edge_idx[e] : e;
+    ed[b].nid = (nr >= 0 && nr < P.n_node) ? static_cast<uint32_t>(nr) : kNoRow;
+    ed[b].eid = (er >= 0 && er < P.n_erow) ? static_cast<uint32_t>(er) : kNoRow;
+    ed[b].t = P.dt_dim > 0 ? P.dt[e] : 0.f;
+  }
+}
+
+// The batch's K-space rows into LDS: every thread first issues the row-chunk loads of all
+// its tasks (chunk c of edge b; non-row chunks and missing rows read the static zero row),
+// then completes them (bf16 widening, the row end of padded rows, the time cosines, the
+// bias chunk) and stores them.
+template <int RS>
+__device__ __forceinline__ void hs_gather(const TgatParams& P, const float4* twt, const HsEdge* ed,
+                                          int nb, float4* xs) {
+  constexpr int G = (kHsBatch * RS + kBlock - 1) / kBlock;  // tasks per thread
+  const char* zero = reinterpret_cast<const char*>(kZeroRow);
+  const int tasks = nb * P.cp;
+  float4 val[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i = threadIdx.x + g * kBlock;
+    const int b = i < tasks ? i / P.cp : 0, c = i < tasks ? i - b * P.cp : P.cp;
+    const char* ptr = zero;
+    if (c < P.cn) {
+      const uint32_t r = ed[b].nid;
+      if (r != kNoRow) ptr = P.node_tab + static_cast<uint64_t>(r) * P.node_stride + (P.node_bf16 ? 8 : 16) * c;
+    } else if (c < P.cn + P.ce) {
+      const uint32_t r = ed[b].eid;
+      if (r != kNoRow) ptr = P.edge_tab + static_cast<uint64_t>(r) * P.edge_stride + (P.edge_bf16 ? 8 : 16) * (c - P.cn);
+    }
+    const bool bf = c < P.cn ? P.node_bf16 : P.edge_bf16;
+    if (bf) {
+      const uint2 w = *reinterpret_cast<const uint2*>(ptr);
+      val[g] = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+    } else {
+      val[g] = *reinterpret_cast<const float4*>(ptr);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int i = threadIdx.x + g * kBlock;
+    if (i >= tasks) continue;
+    const int b = i / P.cp, c = i - b * P.cp;
+    float4 v = val[g];
+    if (c < P.cn) {
+      if (P.node_tail == 1) v = keep_first(v, P.dn - 4 * c);
+    } else if (c < P.cn + P.ce) {
+      if (P.edge_tail == 1) v = keep_first(v, P.de - 4 * (c - P.cn));
+    } else if (c < P.cn + P.ce + P.ct) {
+      const int tj = c - P.cn - P.ce;
+      const float t = ed[b].t;
+      const float4 w = twt[2 * tj], bb = twt[2 * tj + 1];
+      const float a[4] = {time_arg(t, w.x, bb.x), time_arg(t, w.y, bb.y), time_arg(t, w.z, bb.z),
+                          time_arg(t, w.w, bb.w)};
+      float cv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float sv;
+        sincos_hw(a[q], sv, cv[q]);
+        if (fabsf(a[q]) > trig::kMaxArg) cv[q] = cos_far(a[q]);  // outside the reduction's range
+        if (4 * tj + q >= P.dt_dim) cv[q] = 0.f;
+      }
+      v = make_float4(cv[0], cv[1], cv[2], cv[3]);
+    } else {
+      v = c == P.cn + P.ce + P.ct ? make_float4(1.f, 0.f, 0.f, 0.f) : f4_zero();
+    }
+    xs[b * RS + c] = v;
+  }
+}
+
+template <int H, int NS>
+__global__ __launch_bounds__(kBlock) void tgat_fwd_hs(TgatParams P) {
+  constexpr int HG = H / kWavesPerBlock;   // heads per wave
+  constexpr int RS = NS * kWave;           // chunks per LDS row
+  extern __shared__ float lds[];
+  const int wave = uniform(threadIdx.x / kWave);
+  const int lane = lane_id();
+  float4* twt = reinterpret_cast<float4*>(lds);
+  float4* xs = twt + 2 * (P.ct + 1);
+  HsEdge* ed = reinterpret_cast<HsEdge*>(xs + kHsBatch * RS);
+  stage_time_table(P, lds);
+  for (int i = threadIdx.x; i < kHsBatch * RS; i += kBlock) xs[i] = f4_zero();
+  __syncthreads();
+
+  for (int64_t v = blockIdx.x; v < P.n_dst; v += gridDim.x) {
+    const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
+    const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
+    float4 q[HG][NS], acc[HG][NS];
+    float m[HG], l[HG];
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      const int h = wave * HG + g;
+      const rsrc_t rr = make_rsrc(P.qt + v * P.qt_rs + h * P.qt_hs, 4u * static_cast<uint32_t>(P.kp));
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        q[g][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+        acc[g][k] = f4_zero();
+      }
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+    }
+    for (int64_t c0 = e0; c0 < e1; c0 += kHsBatch) {
+      const int nb = static_cast<int>(e1 - c0 < kHsBatch ? e1 - c0 : kHsBatch);
+      __syncthreads();  // the previous batch's reads are done
+      hs_stage_edges(P, c0, nb, ed);
+      __syncthreads();
+      hs_gather<RS>(P, twt, ed, nb, xs);
+      __syncthreads();
+      for (int b = 0; b < nb; ++b) {
+        const int64_t e = c0 + b;
+        float4 x[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k) x[k] = xs[b * RS + lane + k * kWave];
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+          const int h = wave * HG + g;
+          const float s = leaky(wave_sum(row_dot<NS>(q[g], x)), P.slope);
+          if (lane == 0) P.scores[e * H + h] = s;
+          float dr = 1.f;
+          if (P.drop) dr = P.drop[e * H + h];
+          else if (P.drop_hash) dr = drop_mult(P.drop_seed, static_cast<uint64_t>(e * H + h), P.drop_p, P.drop_scale);
+          if (s > m[g]) {  // wave-uniform
+            const float r = exp_fast(m[g] - s);
+            l[g] *= r;
+#pragma unroll
+            for (int k = 0; k < NS; ++k) scale4(acc[g][k], r);
+            m[g] = s;
+          }
+          const float pe = exp_fast(s - m[g]);
+          l[g] += pe;
+#pragma unroll
+          for (int k = 0; k < NS; ++k) fma4(acc[g][k], pe * dr, x[k]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      const int h = wave * HG + g;
+      const float inv = e1 > e0 ? 1.f / l[g] : 0.f;
+      const rsrc_t rr = make_rsrc(P.xbar + v * P.xbar_rs + h * P.xbar_hs, 4u * static_cast<uint32_t>(P.kp));
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        scale4(acc[g][k], inv);
+        bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), acc[g][k]);
+      }
+      if (lane == 0) {
+        P.stats[(v * H + h) * 2 + 0] = m[g];
+        P.stats[(v * H + h) * 2 + 1] = l[g];
+      }
+    }
+  }
+}
+
 // Sums the per-workgroup partials: one wave per output value, fixed lane assignment.
 __global__ __launch_bounds__(kBlock) void time_grad_reduce(const float* partial, int rows, int dt_dim,
                                                           float* d_w, float* d_b) {
@@ -1448,11 +1644,37 @@ size_t pair_lds_bytes(const TgatParams& P, int heads) {
                               pair_wave_floats(P.tvs, heads, static_cast<int>(ceil_div(P.cp, kHalf))));
 }
 
+// The head-split forward: 4 or 8 heads, chunk loads (modes 0 and 1), at most 32 time chunks
+// (the time table) and 192 chunks.
+bool hs_fwd_fits(const TgatParams& P, int heads) {
+  return (heads == 4 || heads == 8) && P.node_tail != 2 && P.edge_tail != 2 && P.ct <= 64 &&
+         P.cp <= 3 * kWave;
+}
+
+size_t hs_lds_bytes(const TgatParams& P) {
+  return sizeof(float4) * (2 * static_cast<size_t>(P.ct + 1) +
+                           static_cast<size_t>(kHsBatch) * kWave * ceil_div(P.cp, kWave)) +
+         sizeof(HsEdge) * kHsBatch;
+}
+
 template <int H>
 int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   const int ns = static_cast<int>(ceil_div(P.cp, kWave));
   size_t lds = fwd_lds_bytes(P);
   void (*k)(TgatParams) = nullptr;
+  if constexpr (H == 4 || H == 8) if (hs_fwd_fits(P, H)) {
+    lds = hs_lds_bytes(P);
+    switch (ns) {
+      case 1: k = tgat_fwd_hs<H, 1>; break;
+      case 2: k = tgat_fwd_hs<H, 2>; break;
+      default: k = tgat_fwd_hs<H, 3>; break;
+    }
+    const void* kp = reinterpret_cast<const void*>(k);
+    const int64_t res = resident_blocks(kp, lds);
+    const dim3 grid(static_cast<unsigned>(P.n_dst < res ? (P.n_dst < 1 ? 1 : P.n_dst) : res));
+    hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, stream, P);
+    return launch_status();
+  }
   if constexpr (H <= 2) if (pair_fwd_fits(P, H)) {
     lds = pair_lds_bytes(P, H);
     switch (ceil_div(P.cp, kHalf)) {

@@ -223,6 +223,63 @@ __global__ __launch_bounds__(kBlock) void epilogue_bwd(EpiBwdParams P) {
   }
 }
 
+// The backward for rows of whole chunks up to 128 wide (aligned): a half-wave per row, lane
+// l holding columns 4l .. 4l+3; the column sums are kept per lane, combined over the
+// workgroup's eight half-waves in a fixed order.
+__global__ __launch_bounds__(kBlock) void epilogue_bwd_h(EpiBwdParams P) {
+  __shared__ float4 red[2 * kWavesPerBlock][3][kHalf];
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int c = 4 * hl;
+  const bool on = c < P.d;
+  const float inv_d = 1.f / static_cast<float>(P.d);
+  const float4 gm = on ? f4_load(P.gamma + c) : f4_zero();
+  float4 gg = f4_zero(), gb = f4_zero(), gu = f4_zero();
+  const int64_t slots = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * 2;
+  // the loop runs on the wave's first row, so both halves take every iteration
+  for (int64_t rb = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave) * 2; rb < P.n; rb += slots) {
+    const int64_t r = rb + half;
+    const bool ok = on && r < P.n;
+    const float mean = r < P.n ? P.stats[2 * r] : 0.f, rstd = r < P.n ? P.stats[2 * r + 1] : 0.f;
+    const float4 dy = ok ? f4_load(P.dout + r * P.d + c) : f4_zero();
+    const float4 yy = ok ? f4_load(P.y + r * P.d + c) : f4_zero();
+    const float4 yh = ok ? make_float4((yy.x - mean) * rstd, (yy.y - mean) * rstd, (yy.z - mean) * rstd,
+                                       (yy.w - mean) * rstd)
+                         : f4_zero();
+    const float4 g = make_float4(dy.x * gm.x, dy.y * gm.y, dy.z * gm.z, dy.w * gm.w);
+    gg.x = fmaf(dy.x, yh.x, gg.x); gg.y = fmaf(dy.y, yh.y, gg.y);
+    gg.z = fmaf(dy.z, yh.z, gg.z); gg.w = fmaf(dy.w, yh.w, gg.w);
+    gb.x += dy.x; gb.y += dy.y; gb.z += dy.z; gb.w += dy.w;
+    const float m1 = half_sum(g.x + g.y + g.z + g.w) * inv_d;
+    const float m2 = half_sum(g.x * yh.x + g.y * yh.y + g.z * yh.z + g.w * yh.w) * inv_d;
+    // y = relu(u * mult): dy/du = mult where y > 0, else 0
+    const float4 du = make_float4(yy.x > 0.f ? rstd * (g.x - m1 - yh.x * m2) * P.scale : 0.f,
+                                  yy.y > 0.f ? rstd * (g.y - m1 - yh.y * m2) * P.scale : 0.f,
+                                  yy.z > 0.f ? rstd * (g.z - m1 - yh.z * m2) * P.scale : 0.f,
+                                  yy.w > 0.f ? rstd * (g.w - m1 - yh.w * m2) * P.scale : 0.f);
+    if (ok) {
+      *reinterpret_cast<float4*>(P.du + r * P.d + c) = du;
+      gu.x += du.x; gu.y += du.y; gu.z += du.z; gu.w += du.w;
+    }
+  }
+  red[wave * 2 + half][0][hl] = gg;
+  red[wave * 2 + half][1][hl] = gb;
+  red[wave * 2 + half][2][hl] = gu;
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < P.nsum * P.d; idx += kBlock) {
+    const int which = idx / P.d;
+    const int col = idx - which * P.d;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 2 * kWavesPerBlock; ++w) {
+      const float4 v = red[w][which][col >> 2];
+      s += (col & 3) == 0 ? v.x : ((col & 3) == 1 ? v.y : ((col & 3) == 2 ? v.z : v.w));
+    }
+    P.partial[(static_cast<int64_t>(blockIdx.x) * P.nsum + which) * P.d + col] = s;
+  }
+}
+
 // out_which[c] = sum over rows r of partial[r][which][c] (which < nsum): one wave per
 // output, fixed order.
 __global__ __launch_bounds__(kBlock) void column_sums(const float* partial, int rows, int d,
@@ -382,11 +439,17 @@ extern "C" int fa_tgat_epilogue_bwd_f32(int64_t n, int32_t d, const float* dout,
   P.scale = static_cast<float>(1.0 / (1.0 - static_cast<double>(drop_p)));
   P.du = du; P.nsum = nsum; P.partial = static_cast<float*>(scratch);
   const int grid = epi_grid(n);
-  switch (static_cast<int>(ceil_div(d, kWave))) {
-    case 1: hipLaunchKernelGGL(epilogue_bwd<1>, dim3(grid), dim3(kBlock), 0, stream, P); break;
-    case 2: hipLaunchKernelGGL(epilogue_bwd<2>, dim3(grid), dim3(kBlock), 0, stream, P); break;
-    case 3: hipLaunchKernelGGL(epilogue_bwd<3>, dim3(grid), dim3(kBlock), 0, stream, P); break;
-    default: hipLaunchKernelGGL(epilogue_bwd<4>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+  const bool rows4 = !(d & 3) && d <= 4 * kHalf && aligned16(dout) && aligned16(y) &&
+                     aligned16(du) && aligned16(gamma);
+  if (rows4) {
+    hipLaunchKernelGGL(epilogue_bwd_h, dim3(grid), dim3(kBlock), 0, stream, P);
+  } else {
+    switch (static_cast<int>(ceil_div(d, kWave))) {
+      case 1: hipLaunchKernelGGL(epilogue_bwd<1>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+      case 2: hipLaunchKernelGGL(epilogue_bwd<2>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+      case 3: hipLaunchKernelGGL(epilogue_bwd<3>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+      default: hipLaunchKernelGGL(epilogue_bwd<4>, dim3(grid), dim3(kBlock), 0, stream, P); break;
+    }
   }
   hipLaunchKernelGGL(column_sums, dim3(static_cast<unsigned>(ceil_div(nsum * d, kWavesPerBlock))),
                      dim3(kBlock), 0, stream, static_cast<const float*>(P.partial), grid, d, nsum,

@@ -362,18 +362,20 @@ def test_dropout_mask_matches_restatement(dev):
     assert abs(keep - 0.9) < 0.003, keep
 
 
-def test_hashed_dropout_equals_explicit_mask(dev):
+@pytest.mark.parametrize("heads,dim", [(2, 100), (8, 128)])
+def test_hashed_dropout_equals_explicit_mask(dev, heads, dim):
     """The kernels' in-kernel dropout (seed, p) gives exactly the layer computed with the
     explicit multipliers fastAgg.dropout_mask(seed, p), forward and backward, and both match
-    the restatement with that mask."""
+    the restatement with that mask (2 heads: the two-edge kernels; 8: the head-split
+    forward and the one-edge backward)."""
     import fast_amd
     from fast_amd.tgat import TransfomerAttentionLayer
     from fast_amd.workloads import single_layer
 
     torch.manual_seed(0)
-    layer = TransfomerAttentionLayer(100, 172, 100, 2, 0.0, 0.3, 100).to(dev)
+    layer = TransfomerAttentionLayer(100, 172, 100, heads, 0.0, 0.3, dim).to(dev)
     degrees = np.array([10] * 100 + [0, 1, 25])
-    inp = single_layer(len(degrees), degrees=degrees, seed=3)
+    inp = single_layer(len(degrees), degrees=degrees, seed=3, heads=heads, dim_out=dim)
     seed, p = 99, 0.3
     outs, grads = [], []
     for explicit in (False, True):
@@ -381,7 +383,7 @@ def test_hashed_dropout_equals_explicit_mask(dev):
         blk.srcdata["h"].requires_grad_(True)
         layer.zero_grad()
         if explicit:
-            mask = fast_amd.fastAgg.dropout_mask(blk.num_edges(), 2, seed, p, dev)
+            mask = fast_amd.fastAgg.dropout_mask(blk.num_edges(), heads, seed, p, dev)
             out = layer.attend(blk, drop=mask)
         else:
             out = layer.attend(blk, drop_seed=seed, drop_p=p)
@@ -393,7 +395,7 @@ def test_hashed_dropout_equals_explicit_mask(dev):
         assert torch.equal(a, b)
     cpu = inp.block
     mask = torch.from_numpy(__import__("oracle.ref_cpu", fromlist=["C"]).C.dropout_mask(
-        cpu.num_edges(), 2, seed, p))
+        cpu.num_edges(), heads, seed, p))
     P = layer_params(layer)
     src, dst = cpu.edges()
     ref = tgat_layer(P, cpu.srcdata["h"].double(), cpu.edata["f"], cpu.edata["dt"], src, dst,

@@ -338,10 +338,12 @@ struct WgradParams {
 };
 
 constexpr int kWcols = 64;  // columns per wave in wgrad
-#ifndef FA_WGRAD_STAGE
-#define FA_WGRAD_STAGE 2
-#endif
-constexpr int kWgradStage = FA_WGRAD_STAGE;  // 16-row blocks per LDS stage
+// Waves per SIMD the register budget of wgrad is held to (nw waves per workgroup)
+constexpr int wgrad_min_waves(int nw, bool vec) { return nw >= 2 && vec ? 4 : 3; }
+// LDS row of the staged X block: 80 floats, so the four rows a k-step reads (one per lane
+// quarter) start 16 banks apart and the 64 lanes of a read hit distinct banks
+constexpr int kWgradLdsRow = 80;
+constexpr int kWgradStage = 16;  // rows per LDS stage (one k-block of four MFMA k-steps)
 
 // Workgroup (chunk, g, j group, column quad): each wave accumulates X^T Y over the chunk's
 // rows for 16*NJT rows j and 64 columns, 16 rows (4 k-steps, k-slot of lane l = row
@@ -350,14 +352,15 @@ constexpr int kWgradStage = FA_WGRAD_STAGE;  // 16-row blocks per LDS stage
 // t of the wave stands for the columns cw + 4m + t (m < 16), so the four B values of a
 // lane in a k-step are one float4, Y[row][cw + 4*(l%16) .. +3]. The next block's X and Y
 // are loaded while the current one is multiplied.
-template <int NJT, bool VEC, int NW>
-__global__ __launch_bounds__(NW * kWave) void head_wgrad(WgradParams P) {
-  constexpr int XW = 65;
-  constexpr int NT = NW * kWave;               // threads of the workgroup
-  constexpr int SR = 16 * kWgradStage;         // rows per stage
+template <int NJT, bool VEC, int NW, int XV>
+__global__ __launch_bounds__(NW * kWave, wgrad_min_waves(NW, VEC)) void head_wgrad(WgradParams P) {
+  constexpr int XW = kWgradLdsRow;
+  constexpr int SR = kWgradStage;              // rows per stage
   constexpr int KK = SR / 4;                   // k-steps per stage
-  constexpr int XE = (SR * 64 + NT - 1) / NT;  // X elements per thread and stage
-  __shared__ float xs[2][SR][XW];
+  constexpr int XL = kWave / XV;               // lanes per 64-column X row
+  constexpr int XR = NW * kWave / XL;          // stage rows covered by one pass of the threads
+  constexpr int XE = (SR + XR - 1) / XR;       // X vectors per thread and stage
+  __shared__ __align__(16) float xs[2][SR][XW];
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = uniform(tid / kWave);
@@ -373,17 +376,12 @@ __global__ __launch_bounds__(NW * kWave) void head_wgrad(WgradParams P) {
   const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
   const float* xbase = P.x + g * P.xg;
   const float* ybase = P.y + g * P.yg;
-  // X elements of this thread: e = tid + NT*i of the SR x 64 stage (row e/64, col e%64)
-  int xr[XE], xj[XE];
-  uint32_t xo[XE];
-#pragma unroll
-  for (int i = 0; i < XE; ++i) {
-    const int e = tid + NT * i;
-    const bool ok = e < SR * 64;
-    xr[i] = ok ? e >> 6 : SR;                  // row SR: no element
-    xj[i] = j0 + (e & 63);
-    xo[i] = (ok && xj[i] < P.j) ? 4u * static_cast<uint32_t>(xr[i] * P.ldx + xj[i]) : kOob;
-  }
+  // X vectors of this thread: columns xc .. xc+XV-1 (of the 64-column j group) of the stage
+  // rows xr + XR*i. j % XV == 0, so a vector lies wholly inside X or wholly past column j.
+  const int xr = tid / XL, xc = (tid % XL) * XV;
+  const int xj = j0 + xc;
+  const uint32_t xo = xj < P.j ? 4u * static_cast<uint32_t>(xr * P.ldx + xj) : kOob;
+  const uint32_t xstep = 4u * static_cast<uint32_t>(XR * P.ldx);
   const int cl = cw + 4 * li;                  // first of this lane's four B columns
   const uint32_t yo = (active && cl < P.c) ? 4u * static_cast<uint32_t>(lk * P.ldy + cl) : kOob;
   const uint32_t ystep = 16u * static_cast<uint32_t>(P.ldy);   // 4 rows
@@ -392,19 +390,46 @@ __global__ __launch_bounds__(NW * kWave) void head_wgrad(WgradParams P) {
     const int64_t rows = r1 - nb < SR ? r1 - nb : SR;
     return rsrc(base + nb * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
   };
-  float xv[XE];
+  float xv[XE][XV];
   auto xload = [&](int64_t nb) {
     const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
 #pragma unroll
-    for (int i = 0; i < XE; ++i) xv[i] = ld1(rx, xo[i]);
+    for (int i = 0; i < XE; ++i) {
+      const uint32_t off = (xo == kOob || xr + XR * i >= SR) ? kOob : xo + i * xstep;
+      if constexpr (XV == 4) {
+        const f4 v = ld4(rx, off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[i][e] = v[e];
+      } else if constexpr (XV == 2) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rx, static_cast<int>(off), 0, 0);
+        xv[i][0] = __uint_as_float(v[0]);
+        xv[i][1] = __uint_as_float(v[1]);
+      } else {
+        xv[i][0] = ld1(rx, off);
+      }
+    }
   };
   auto xstore = [&](int b, int64_t nb) {
+    const int64_t left = r1 - nb;              // rows of the stage inside the chunk
+    const int valid = left < SR ? static_cast<int>(left) : SR;
 #pragma unroll
     for (int i = 0; i < XE; ++i) {
-      if (xr[i] >= SR) continue;
-      float v = xv[i];
-      if (xj[i] >= P.j) v = (xj[i] < P.jr && nb + xr[i] < r1) ? 1.f : 0.f;
-      xs[b][xr[i]][xj[i] - j0] = v;
+      const int r = xr + XR * i;
+      if (XE * XR > SR && r >= SR) continue;
+      float v[XV];
+#pragma unroll
+      for (int e = 0; e < XV; ++e) {
+        // past column j: the ones row (with ones) over the rows inside the chunk, else 0
+        const float one = (xj + e >= P.j && xj + e < P.jr && r < valid) ? 1.f : 0.f;
+        v[e] = xo == kOob ? one : xv[i][e];
+      }
+      if constexpr (XV == 4) {
+        *reinterpret_cast<f4*>(&xs[b][r][xc]) = f4{v[0], v[1], v[2], v[3]};
+      } else if constexpr (XV == 2) {
+        *reinterpret_cast<float2*>(&xs[b][r][xc]) = make_float2(v[0], v[1]);
+      } else {
+        xs[b][r][xc] = v[0];
+      }
     }
   };
   auto yload = [&](int64_t nb, f4 (&bv)[KK]) {
@@ -426,17 +451,23 @@ __global__ __launch_bounds__(NW * kWave) void head_wgrad(WgradParams P) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[a][t] = f4{0.f, 0.f, 0.f, 0.f};
   auto stage = [&](int b, const f4 (&bv)[KK]) {
+    // the A values of k-step kk + 1 are read from LDS while k-step kk is multiplied
+    float av[2][NJT];
+#pragma unroll
+    for (int a = 0; a < NJT; ++a) av[0][a] = xs[b][lk][16 * a + li];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      // the k-step's A values first: one LDS wait per k-step, not per product
-      float av[NJT];
+      if (kk + 1 < KK) {
 #pragma unroll
-      for (int a = 0; a < NJT; ++a) av[a] = xs[b][4 * kk + lk][16 * a + li];
+        for (int a = 0; a < NJT; ++a) av[(kk + 1) & 1][a] = xs[b][4 * (kk + 1) + lk][16 * a + li];
+      }
+      pin();
 #pragma unroll
       for (int a = 0; a < NJT; ++a) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[a][t] = mfma4(av[a], bv[kk][t], acc[a][t]);
+        for (int t = 0; t < 4; ++t) acc[a][t] = mfma4(av[kk & 1][a], bv[kk][t], acc[a][t]);
       }
+      pin();
     }
   };
   f4 ba[KK], bb[KK];
@@ -547,13 +578,17 @@ int row_grid(int64_t n, int per_tile_groups, const void* kernel) {
   return static_cast<int>(g < 1 ? 1 : g);
 }
 
-constexpr int kWgradWaves = 3072;  // waves of a wgrad launch (about 3 per SIMD)
+#ifndef FA_WGRAD_MIN_ROWS
+#define FA_WGRAD_MIN_ROWS 64
+#endif
+constexpr int kWgradMinRows = FA_WGRAD_MIN_ROWS;  // rows of a wgrad chunk, at least
 
-// Chunks of the wgrad reduction: about kWgradWaves waves in all, at least 64 rows each.
-int64_t wgrad_chunks(int64_t n, int groups, int waves_per_group) {
-  int64_t chunks = kWgradWaves / ((groups > 0 ? groups : 1) * waves_per_group);
+// Chunks of the wgrad reduction: one per resident workgroup row (the launch runs in one
+// round, with no tail of late workgroups), at least kWgradMinRows rows each.
+int64_t wgrad_chunks(int64_t n, int groups, int64_t resident) {
+  int64_t chunks = resident / (groups > 0 ? groups : 1);
   if (chunks < 1) chunks = 1;
-  const int64_t by_rows = ceil_div(n, 64);
+  const int64_t by_rows = ceil_div(n, kWgradMinRows);
   return chunks < by_rows ? chunks : (by_rows < 1 ? 1 : by_rows);
 }
 
@@ -569,6 +604,39 @@ int wgrad_groups(int j, int c, int groups, int ones) {
   const int jr = j + (ones ? 1 : 0);
   const int ncwg = static_cast<int>(ceil_div(ceil_div(c, kWcols), wgrad_waves(c)));
   return groups * static_cast<int>(ceil_div(jr, 64)) * ncwg;
+}
+
+using WgradKernel = void (*)(WgradParams);
+
+// The wgrad kernel for njt 16-row j tiles, nw waves per workgroup and X read xv floats
+// at a time (1 with scalar-column Y).
+WgradKernel wgrad_kernel(int njt, int nw, bool vec, int xv) {
+#define FA_WG_NW(NJ, NWV)                                                                  \
+  if (njt == NJ && nw == NWV) {                                                            \
+    if (!vec) return head_wgrad<NJ, false, NWV, 1>;                                        \
+    return xv == 4 ? head_wgrad<NJ, true, NWV, 4>                                          \
+                   : (xv == 2 ? head_wgrad<NJ, true, NWV, 2> : head_wgrad<NJ, true, NWV, 1>); \
+  }
+#define FA_WG(NJ) FA_WG_NW(NJ, 1) FA_WG_NW(NJ, 2) FA_WG_NW(NJ, 3) FA_WG_NW(NJ, 4)
+  FA_WG(1) FA_WG(2) FA_WG(3) FA_WG(4)
+#undef FA_WG
+#undef FA_WG_NW
+  return nullptr;
+}
+
+int wgrad_njt(int jr) {
+  return jr > 64 ? 4 : static_cast<int>(ceil_div(jr, 16));
+}
+
+// Row chunks of a wgrad launch (the same for the scratch size and the launch): the
+// resident workgroups of the 16-byte kernel, shared out over the workgroup rows.
+int64_t wgrad_plan_chunks(int64_t n, int j, int c, int groups, int ones) {
+  const int jr = j + (ones ? 1 : 0);
+  const int nw = wgrad_waves(c);
+  const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, true, 1);
+  const int64_t resident =
+      k ? resident_blocks(reinterpret_cast<const void*>(k), 0, nw * kWave) : 1;
+  return wgrad_chunks(n, wgrad_groups(j, c, groups, ones), resident);
 }
 
 void launch_proj(void (*k)(ProjParams), int64_t n, int gy, const ProjParams& P,
@@ -662,8 +730,8 @@ extern "C" size_t fa_head_wgrad_scratch_bytes(int64_t n, int32_t j, int32_t c, i
                                               int32_t ones) {
   if (n <= 0 || j <= 0 || c <= 0 || groups <= 0) return 0;
   const int jr = j + (ones ? 1 : 0);
-  const int gy = wgrad_groups(j, c, groups, ones);
-  return static_cast<size_t>(wgrad_chunks(n, gy, wgrad_waves(c))) * groups * jr * c * sizeof(float);
+  return static_cast<size_t>(wgrad_plan_chunks(n, j, c, groups, ones)) * groups * jr * c *
+         sizeof(float);
 }
 
 extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
@@ -687,8 +755,8 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), nw));
   P.njg = static_cast<int>(ceil_div(jr, 64));
   const int gy = wgrad_groups(j, c, groups, ones);
-  const int64_t chunks = wgrad_chunks(n, gy, nw);
-  P.rows = round_up(ceil_div(n, chunks), 16 * kWgradStage);
+  const int64_t chunks = wgrad_plan_chunks(n, j, c, groups, ones);
+  P.rows = round_up(ceil_div(n, chunks), kWgradStage);
   // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
   if ((P.rows + 64) * (ldx > ldy ? ldx : ldy) * 4 >= static_cast<int64_t>(kOob)) return FA_EUNSUPPORTED;
   const int64_t used = ceil_div(n, P.rows);
@@ -696,14 +764,13 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
     return FA_ESCRATCH;
   P.part = static_cast<float*>(scratch);
   const dim3 grid(static_cast<unsigned>(used), static_cast<unsigned>(gy));
-  void (*k)(WgradParams) = nullptr;
-  const int njt = P.njg > 1 ? 4 : static_cast<int>(ceil_div(jr, 16));
-#define FA_WG_NW(NJ, NWV)                                                                \
-  if (njt == NJ && nw == NWV) k = P.vec ? head_wgrad<NJ, true, NWV> : head_wgrad<NJ, false, NWV>;
-#define FA_WG(NJ) FA_WG_NW(NJ, 1) FA_WG_NW(NJ, 2) FA_WG_NW(NJ, 3) FA_WG_NW(NJ, 4)
-  FA_WG(1) FA_WG(2) FA_WG(3) FA_WG(4)
-#undef FA_WG
-#undef FA_WG_NW
+  // X read 4 or 2 floats at a time where j, the strides and the base allow it
+  int xv = 1;
+  if (!(j & 3) && !(ldx & 3) && !(xg & 3) && aligned16(x))
+    xv = 4;
+  else if (!(j & 1) && !(ldx & 1) && !(xg & 1) && !(reinterpret_cast<uintptr_t>(x) & 7))
+    xv = 2;
+  const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, P.vec != 0, xv);
   if (!k) return FA_EUNSUPPORTED;
   hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(nw * kWave)), 0, stream, P);
   if (!(out & 3) && aligned16(dw) && aligned16(scratch)) {

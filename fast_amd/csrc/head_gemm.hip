@@ -513,6 +513,179 @@ __global__ __launch_bounds__(NW * kWave, wgrad_min_waves(NW, VEC)) void head_wgr
   }
 }
 
+// ----- wgrad on the bf16 matrix cores -----------------------------------------------------
+// The same product with every fp32 operand split into three bf16 parts whose sum is the
+// operand exactly (hi = bf16(x), mid = bf16(x - hi), lo = x - hi - mid: 8 + 8 + 8 bits of
+// the 24-bit significand), multiplied as the six part products whose order is at most
+// 2^-16 of the whole (hi.hi, hi.mid, mid.hi, hi.lo, lo.hi, mid.mid) on MFMA 16x16x32 bf16
+// with fp32 accumulation. The three products left out are below 2^-24 of |x y| together,
+// the size of the rounding of one fp32 product, and six bf16 products cost less than half
+// the matrix-core time of one fp32 product.
+//   MFMA 16x16x32 bf16, lane l: A[l%16][8*(l/16) + s], B[8*(l/16) + s][l%16] (s < 8, the
+//   same k for A and B), D[4*(l/16)+r][l%16].
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+typedef float fl2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(fl2_t{a, b}, bf2_t));
+}
+__device__ __forceinline__ float bf16_low(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_high(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Two floats as three bf16 pairs (hi, mid, lo) with x = hi + mid + lo per element.
+__device__ __forceinline__ void split3(float x0, float x1, uint32_t (&part)[3]) {
+  part[0] = pack_bf16(x0, x1);
+  const float r0 = x0 - bf16_low(part[0]), r1 = x1 - bf16_high(part[0]);
+  part[1] = pack_bf16(r0, r1);
+  part[2] = pack_bf16(r0 - bf16_low(part[1]), r1 - bf16_high(part[1]));
+}
+
+__device__ __forceinline__ f4 mfma_bf(const u4_t& a, const u4_t& b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, a),
+                                                 __builtin_bit_cast(bf8_t, b), c, 0, 0, 0);
+}
+
+constexpr int kBfStage = 32;  // rows per stage: one k-block of the bf16 product
+constexpr int kBfXp = 40;     // bf16 per LDS row of the transposed X parts (32 rows + 8)
+
+// Workgroup as head_wgrad. X staged in LDS already split and transposed, [part][j][row], so
+// a lane's A operand of a tile and part is one 16-byte LDS read; each lane's Y values of a
+// stage are eight float4 rows (rows 8*(l/16) + s, columns cw + 4*(l%16) .. +3), split in
+// registers into the B operands of its four column tiles. The next stage's X and Y are
+// loaded while the current one is multiplied.
+template <int NJT, int NW>
+__global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
+  constexpr int SR = kBfStage;
+  constexpr int XE = (SR + NW - 1) / NW;       // X elements per thread and stage
+  __shared__ __align__(16) uint16_t xp[2][3][64][kBfXp];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int per_g = P.njg * P.ncw4;
+  const int g = blockIdx.y / per_g;
+  const int rem = blockIdx.y - g * per_g;
+  const int jg = rem / P.ncw4;
+  const int cw = ((rem - jg * P.ncw4) * NW + wave) * kWcols;
+  const bool active = cw < P.c;
+  const int j0 = jg * 64;
+  const int li = lane & 15, lq = lane >> 4;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * P.rows;
+  const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
+  const float* xbase = P.x + g * P.xg;
+  const float* ybase = P.y + g * P.yg;
+  // X elements of this thread: column `lane` of the j group, stage rows wave + NW*i
+  const int xj = j0 + lane;
+  const uint32_t xo = xj < P.j ? 4u * static_cast<uint32_t>(wave * P.ldx + xj) : kOob;
+  const uint32_t xstep = 4u * static_cast<uint32_t>(NW * P.ldx);
+  const bool xones = xj >= P.j && xj < P.jr;   // this thread's column is the ones row
+  const int cl = cw + 4 * li;                  // first of this lane's four B columns
+  const uint32_t yo =
+      (active && cl < P.c) ? 4u * static_cast<uint32_t>(8 * lq * P.ldy + cl) : kOob;
+  const uint32_t ystep = 4u * static_cast<uint32_t>(P.ldy);   // one row
+  auto stage_rsrc = [&](const float* base, int64_t nb, int64_t ld, int64_t w) {
+    const int64_t rows = r1 - nb < SR ? r1 - nb : SR;
+    return rsrc(base + nb * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
+  };
+  float xv[XE];
+  auto xload = [&](int64_t nb) {
+    const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
+#pragma unroll
+    for (int i = 0; i < XE; ++i)
+      xv[i] = ld1(rx, (xo == kOob || wave + NW * i >= SR) ? kOob : xo + i * xstep);
+  };
+  auto xstore = [&](int b, int64_t nb) {
+    const int64_t left = r1 - nb;
+    const int valid = left < SR ? static_cast<int>(left) : SR;
+#pragma unroll
+    for (int i = 0; i < XE; i += 2) {
+      const int ra = wave + NW * i, rb = wave + NW * (i + 1);
+      const float va = xo == kOob ? ((xones && ra < valid) ? 1.f : 0.f) : xv[i];
+      const float vb = i + 1 < XE ? (xo == kOob ? ((xones && rb < valid) ? 1.f : 0.f) : xv[i + 1]) : 0.f;
+      uint32_t part[3];
+      split3(va, vb, part);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        if (ra < SR) xp[b][q][lane][ra] = static_cast<uint16_t>(part[q] & 0xffffu);
+        if (i + 1 < XE && rb < SR) xp[b][q][lane][rb] = static_cast<uint16_t>(part[q] >> 16);
+      }
+    }
+  };
+  f4 raw[8];
+  auto yload = [&](int64_t nb) {
+    const rsrc_t ry = stage_rsrc(ybase, nb, P.ldy, P.c);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) raw[s] = ld4(ry, yo == kOob ? kOob : yo + s * ystep);
+  };
+  f4 acc[NJT][4];
+#pragma unroll
+  for (int a = 0; a < NJT; ++a)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[a][t] = f4{0.f, 0.f, 0.f, 0.f};
+  int64_t nb = r0;
+  xload(nb);
+  yload(nb);
+  xstore(0, nb);
+  __syncthreads();
+  int b = 0;
+  for (; nb < r1; nb += SR) {
+    // this stage's B operands: tile t, part q, k-slots s = rows 8*(l/16) + s
+    u4_t bp[3][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int s = 0; s < 8; s += 2) {
+        uint32_t part[3];
+        split3(raw[s][t], raw[s + 1][t], part);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) bp[q][t][s / 2] = part[q];
+      }
+    }
+    xload(nb + SR);
+    yload(nb + SR);
+    pin();
+    if (active) {
+      u4_t ap[3][NJT];
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int a = 0; a < NJT; ++a)
+          ap[q][a] = *reinterpret_cast<const u4_t*>(&xp[b][q][16 * a + li][8 * lq]);
+      // the six part products, each over every (a, t): consecutive products go to
+      // different accumulators
+      constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
+      constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
+#pragma unroll
+      for (int pr = 0; pr < 6; ++pr) {
+#pragma unroll
+        for (int a = 0; a < NJT; ++a) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[a][t] = mfma_bf(ap[kPa[pr]][a], bp[kPb[pr]][t], acc[a][t]);
+        }
+      }
+    }
+    xstore(b ^ 1, nb + SR);
+    __syncthreads();
+    b ^= 1;
+  }
+  if (!active) return;
+  // D[i][m] of tile t: row j0 + 16a + 4lq + r, column cw + 4*li + t
+  float* part = P.part + (static_cast<int64_t>(blockIdx.x) * P.g + g) * P.jr * P.c;
+#pragma unroll
+  for (int a = 0; a < NJT; ++a) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int jj = j0 + 16 * a + 4 * lq + r;
+      if (jj < P.jr) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (cl + t < P.c) part[static_cast<int64_t>(jj) * P.c + cl + t] = acc[a][t][r];
+      }
+    }
+  }
+}
+
 // out[i] = sum over chunks k of part[k*stride + i], in chunk order: 32 outputs per
 // workgroup, 8 threads per output each summing every 8th chunk, then the 8 partial sums
 // in order through LDS.
@@ -624,16 +797,35 @@ WgradKernel wgrad_kernel(int njt, int nw, bool vec, int xv) {
   return nullptr;
 }
 
+// The split-bf16 wgrad kernel for njt 16-row j tiles and nw waves per workgroup.
+WgradKernel wgrad_bf_kernel(int njt, int nw) {
+#define FA_WGB_NW(NJ, NWV) \
+  if (njt == NJ && nw == NWV) return head_wgrad_bf<NJ, NWV>;
+#define FA_WGB(NJ) FA_WGB_NW(NJ, 1) FA_WGB_NW(NJ, 2) FA_WGB_NW(NJ, 3) FA_WGB_NW(NJ, 4)
+  FA_WGB(1) FA_WGB(2) FA_WGB(3) FA_WGB(4)
+#undef FA_WGB
+#undef FA_WGB_NW
+  return nullptr;
+}
+
 int wgrad_njt(int jr) {
   return jr > 64 ? 4 : static_cast<int>(ceil_div(jr, 16));
 }
 
-// Row chunks of a wgrad launch (the same for the scratch size and the launch): the
-// resident workgroups of the 16-byte kernel, shared out over the workgroup rows.
-int64_t wgrad_plan_chunks(int64_t n, int j, int c, int groups, int ones) {
+#ifndef FA_WGRAD_BF
+#define FA_WGRAD_BF 1
+#endif
+// Y blocks with 16-byte rows go to the split-bf16 kernel
+constexpr bool kWgradBf = FA_WGRAD_BF != 0;
+
+// Row chunks of a wgrad launch: the resident workgroups of its kernel (the fp32 kernel with
+// 16-byte Y rows and single X loads, or the split-bf16 one), shared out over the workgroup
+// rows.
+int64_t wgrad_plan_chunks(int64_t n, int j, int c, int groups, int ones, bool bf) {
   const int jr = j + (ones ? 1 : 0);
   const int nw = wgrad_waves(c);
-  const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, true, 1);
+  const WgradKernel k = bf ? wgrad_bf_kernel(wgrad_njt(jr), nw)
+                           : wgrad_kernel(wgrad_njt(jr), nw, true, 1);
   const int64_t resident =
       k ? resident_blocks(reinterpret_cast<const void*>(k), 0, nw * kWave) : 1;
   return wgrad_chunks(n, wgrad_groups(j, c, groups, ones), resident);
@@ -730,8 +922,13 @@ extern "C" size_t fa_head_wgrad_scratch_bytes(int64_t n, int32_t j, int32_t c, i
                                               int32_t ones) {
   if (n <= 0 || j <= 0 || c <= 0 || groups <= 0) return 0;
   const int jr = j + (ones ? 1 : 0);
-  return static_cast<size_t>(wgrad_plan_chunks(n, j, c, groups, ones)) * groups * jr * c *
-         sizeof(float);
+  // enough for either kernel (which one runs depends on the alignment of Y)
+  int64_t chunks = wgrad_plan_chunks(n, j, c, groups, ones, false);
+  if (kWgradBf && !(c & 3) && wgrad_waves(c) >= 2) {
+    const int64_t bf = wgrad_plan_chunks(n, j, c, groups, ones, true);
+    chunks = bf > chunks ? bf : chunks;
+  }
+  return static_cast<size_t>(chunks) * groups * jr * c * sizeof(float);
 }
 
 extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
@@ -755,8 +952,9 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), nw));
   P.njg = static_cast<int>(ceil_div(jr, 64));
   const int gy = wgrad_groups(j, c, groups, ones);
-  const int64_t chunks = wgrad_plan_chunks(n, j, c, groups, ones);
-  P.rows = round_up(ceil_div(n, chunks), kWgradStage);
+  const bool bf = kWgradBf && P.vec && nw >= 2;   // one-wave shapes (c <= 64) stay fp32
+  const int64_t chunks = wgrad_plan_chunks(n, j, c, groups, ones, bf);
+  P.rows = round_up(ceil_div(n, chunks), bf ? kBfStage : kWgradStage);
   // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
   if ((P.rows + 64) * (ldx > ldy ? ldx : ldy) * 4 >= static_cast<int64_t>(kOob)) return FA_EUNSUPPORTED;
   const int64_t used = ceil_div(n, P.rows);
@@ -770,7 +968,8 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
     xv = 4;
   else if (!(j & 1) && !(ldx & 1) && !(xg & 1) && !(reinterpret_cast<uintptr_t>(x) & 7))
     xv = 2;
-  const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, P.vec != 0, xv);
+  const WgradKernel k =
+      bf ? wgrad_bf_kernel(wgrad_njt(jr), nw) : wgrad_kernel(wgrad_njt(jr), nw, P.vec != 0, xv);
   if (!k) return FA_EUNSUPPORTED;
   hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(nw * kWave)), 0, stream, P);
   if (!(out & 3) && aligned16(dw) && aligned16(scratch)) {

@@ -211,6 +211,8 @@ struct ReduceParams {
   const float* w; int64_t wg; int64_t ldw;   // W[g][j][c] = w[g*wg + j*ldw + c]
   float* z; int64_t ldz; int64_t zg;         // Z[n][g*J + j] = z[n*ldz + g*zg + j]
   int c16;                                   // 16-column groups of a row, rounded up to kRedDepth
+  int kb, cp;                                // split-bf16 form: 32-column k-blocks (a multiple
+                                             // of kRbDepth) and the LDS row in bf16
 };
 
 constexpr int kRedWaves = 8;                 // waves per reduce workgroup
@@ -686,6 +688,135 @@ __global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
   }
 }
 
+// ----- reduce on the bf16 matrix cores ----------------------------------------------------
+constexpr int kRbWaves = 12;   // waves per workgroup (one workgroup per CU: W's parts fill LDS)
+constexpr int kRbBlock = kRbWaves * kWave;
+constexpr int kRbDepth = 2;    // k-blocks of Y in flight ahead of the one multiplied
+
+// LDS row (bf16) of the split W[g]: the k-blocks, plus 8 so that the rows of a 16-lane read
+// start 4 banks apart.
+int reduce_bf_row(int c) { return static_cast<int>(round_up(ceil_div(c, 32), kRbDepth)) * 32 + 8; }
+size_t reduce_bf_lds_bytes(int j, int c) {
+  return static_cast<size_t>(3) * (j + 1) * reduce_bf_row(c) * sizeof(uint16_t);
+}
+
+// head_reduce with the split-bf16 product (see head_wgrad_bf): W[g]'s three parts in LDS
+// ([part][J+1][cp], row J zero); each wave takes two 16-row tiles of Y at a time (the B
+// operands read from LDS serve both) and runs over all C columns, 32 at a time. k-slot s of
+// lane l stands for column 32kb + 4*(l/16) + s (s < 4) or 32kb + 16 + 4*(l/16) + s - 4, so
+// that a lane's A values are two float4 loads whose 16 lanes of a row read 64 contiguous
+// bytes; W is stored in LDS in that order.
+template <int JT>
+__global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
+  extern __shared__ __align__(16) uint16_t wlb[];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int g = blockIdx.y;
+  const int cp = P.cp, rows = P.j + 1;
+  const float* w = P.w + g * P.wg;
+  for (int i = tid; i < rows * cp; i += kRbBlock) {
+    const int jr = i / cp, cc = i - jr * cp;
+    const int kb = cc >> 5, q = (cc >> 3) & 3, s = cc & 7;
+    const int src = 32 * kb + (s < 4 ? 4 * q + s : 16 + 4 * q + s - 4);
+    const float v = (jr < P.j && cc < 32 * P.kb && src < P.c) ? w[jr * P.ldw + src] : 0.f;
+    uint32_t part[3];
+    split3(v, 0.f, part);
+#pragma unroll
+    for (int pp = 0; pp < 3; ++pp) wlb[(pp * rows + jr) * cp + cc] = static_cast<uint16_t>(part[pp] & 0xffffu);
+  }
+  __syncthreads();
+  const int li = lane & 15, lq = lane >> 4;
+  int wrow[JT];
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) wrow[jt] = (16 * jt + li < P.j ? 16 * jt + li : P.j) * cp + 8 * lq;
+  const int plane = rows * cp;
+  const float* ybase = P.y + g * P.yg;
+  const int64_t pairs = (P.n + 31) / 32;
+  const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
+  for (int64_t pr = static_cast<int64_t>(blockIdx.x) * kRbWaves + wave; pr < pairs;
+       pr += static_cast<int64_t>(gridDim.x) * kRbWaves) {
+    const int64_t n0 = pr * 32;
+    const rsrc_t ry0 = tile_rsrc(ybase, P.n, n0, P.ldy, P.c);
+    const rsrc_t ry1 = tile_rsrc(ybase, P.n, n0 + 16, P.ldy, P.c);
+    // the two float4 of each tile for k-block kb (columns past C read 0)
+    auto ly = [&](int kb, f4 (&v)[2][2]) {
+      const int c0 = 32 * kb + 4 * lq, c1 = c0 + 16;
+      const uint32_t o0 = c0 < P.c ? yrow + 4u * c0 : kOob, o1 = c1 < P.c ? yrow + 4u * c1 : kOob;
+      v[0][0] = ld4(ry0, o0);
+      v[0][1] = ld4(ry0, o1);
+      v[1][0] = ld4(ry1, o0);
+      v[1][1] = ld4(ry1, o1);
+    };
+    f4 acc[2][JT];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) acc[u][jt] = f4{0.f, 0.f, 0.f, 0.f};
+    auto mm = [&](int kb, const f4 (&v)[2][2]) {
+      u4_t ap[2][3];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            uint32_t part[3];
+            split3(v[u][h][e], v[u][h][e + 1], part);
+#pragma unroll
+            for (int pp = 0; pp < 3; ++pp) ap[u][pp][2 * h + e / 2] = part[pp];
+          }
+        }
+      }
+      u4_t bp[3][JT];
+#pragma unroll
+      for (int pp = 0; pp < 3; ++pp)
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt)
+          bp[pp][jt] = *reinterpret_cast<const u4_t*>(&wlb[pp * plane + wrow[jt] + 32 * kb]);
+      constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
+      constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+          for (int jt = 0; jt < JT; ++jt) acc[u][jt] = mfma_bf(ap[u][kPa[q]], bp[kPb[q]][jt], acc[u][jt]);
+        }
+      }
+    };
+    // issued in order: ya[0] is the oldest; kRbDepth k-blocks in flight
+    f4 ya[kRbDepth][2][2];
+#pragma unroll
+    for (int d = 0; d < kRbDepth; ++d) {
+      ly(d, ya[d]);
+      pin();
+    }
+    for (int kb = 0; kb < P.kb; kb += kRbDepth) {   // kb is a multiple of kRbDepth
+#pragma unroll
+      for (int d = 0; d < kRbDepth; ++d) {
+        mm(kb + d, ya[d]);
+        pin();
+        ly(kb + d + kRbDepth, ya[d]);
+        pin();
+      }
+    }
+    // D row 4lq + r of tile u, column 16jt + li
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt) {
+        const int jj = 16 * jt + li;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t row = n0 + 16 * u + 4 * lq + r;
+          if (jj < P.j && row < P.n) P.z[row * P.ldz + g * P.zg + jj] = acc[u][jt][r];
+        }
+      }
+    }
+  }
+}
+
 // out[i] = sum over chunks k of part[k*stride + i], in chunk order: 32 outputs per
 // workgroup, 8 threads per output each summing every 8th chunk, then the 8 partial sums
 // in order through LDS.
@@ -738,6 +869,10 @@ __global__ __launch_bounds__(kBlock) void chunk_sums4(const float* part, int chu
 
 constexpr int kGemmBlocks = 1024;  // workgroups of the row-tile launches
 constexpr size_t kMaxReduceLds = 160 * 1024;
+#ifndef FA_REDUCE_BF
+#define FA_REDUCE_BF 1
+#endif
+constexpr bool kReduceBf = FA_REDUCE_BF != 0;  // reduce on the split-bf16 kernel where it fits
 
 // Byte offsets inside a 16-row tile stay below the out-of-range marker.
 bool tile_fits(int64_t ld) { return ld >= 0 && 17 * ld * 4 < static_cast<int64_t>(kOob); }
@@ -896,6 +1031,30 @@ extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t group
   P.z = z; P.ldz = ldz; P.zg = zg;
   P.c16 = static_cast<int>(round_up(ceil_div(c, 16), kRedDepth));
   const bool vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
+  // 16-byte Y rows go to the split-bf16 kernel when W's three parts fit in LDS
+  if (kReduceBf && vec && reduce_bf_lds_bytes(j, c) <= kMaxReduceLds) {
+    P.kb = static_cast<int>(round_up(ceil_div(c, 32), kRbDepth));
+    P.cp = reduce_bf_row(c);
+    const size_t lds = reduce_bf_lds_bytes(j, c);
+    void (*k)(ReduceParams) = nullptr;
+    switch (static_cast<int>(ceil_div(j, 16))) {
+      case 1: k = head_reduce_bf<1>; break;
+      case 2: k = head_reduce_bf<2>; break;
+      case 3: k = head_reduce_bf<3>; break;
+      default: k = head_reduce_bf<4>; break;
+    }
+    const void* kp = reinterpret_cast<const void*>(k);
+    if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+      return launch_status();
+    const int64_t pairs = ceil_div(n, 32);
+    int64_t gx = resident_blocks(kp, lds, kRbBlock) / groups;
+    if (gx > ceil_div(pairs, kRbWaves)) gx = ceil_div(pairs, kRbWaves);
+    if (gx < 1) gx = 1;
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(groups)),
+                       dim3(kRbBlock), lds, stream, P);
+    return launch_status();
+  }
   const size_t lds = reduce_lds_bytes(j, P.c16);
   if (lds > kMaxReduceLds) return FA_EUNSUPPORTED;
   void (*k)(ReduceParams) = nullptr;

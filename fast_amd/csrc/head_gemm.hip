@@ -5,8 +5,10 @@
 //   reduce Z[n][g*J : g*J+J] = Y[g][n][:] W[g]^T                (agg = xbar W_v^T, dQ = dq~ W_k^T)
 //   wgrad  dW[g] = sum_n X[n][g-block]^T Y[g][n][:]  (+ sum_n Y[g][n][:] as row J)
 // They are tall and skinny (N ~ 1e5 rows, J ~ 32..64, C ~ 400..700): their cost is the
-// stream over the [G][N][C] block, and each runs on the fp32 matrix cores,
+// stream over the [G][N][C] block. proj (and reduce and wgrad for unaligned Y rows) runs on
+// the fp32 matrix cores,
 //   MFMA 16x16x4 f32, lane l: A[l%16][l/16], B[l/16][l%16], D[4*(l/16)+r][l%16], r < 4,
+// and reduce and wgrad on the bf16 ones with split operands (head_reduce_bf, head_wgrad_bf),
 // with every global access of the block a 16-byte-per-lane load or store (the texture
 // unit takes one lane per clock whatever the width, so narrower accesses to the block
 // would cap the bandwidth). The small operands are staged in LDS: the X rows of a tile,

@@ -819,6 +819,137 @@ __global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
   }
 }
 
+// ----- proj on the bf16 matrix cores ------------------------------------------------------
+constexpr int kPbWaves = 8;                  // waves per workgroup (48 columns each)
+constexpr int kPbBlock = kPbWaves * kWave;
+constexpr int kPbCt = 3;                     // 16-column tiles per wave
+constexpr int kPbRows = 32;                  // rows per workgroup step (one LDS sync each)
+constexpr int kPbXp = 72;                    // bf16 per LDS row of the split X: 64 j + 8
+
+// head_proj with the split-bf16 product (see head_wgrad_bf), formed transposed as head_proj:
+// Y^T tile = W^T (A: W's three parts for the wave's 48 columns and KB k-blocks of 32 j, in
+// registers for the whole kernel) times X^T (B: the tile's X rows, split into parts in LDS,
+// [part][row][j]). The bias rides in the product as row J of W^T against an X column of
+// ones. Each lane ends with four consecutive columns of one row and stores one float4.
+template <int KB, bool BIAS>
+__global__ __launch_bounds__(kPbBlock, 2) void head_proj_bf(ProjParams P) {
+  __shared__ __align__(16) uint16_t xp[2][3][kPbRows][kPbXp];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  const int g = blockIdx.y / P.ncg4;
+  const int c0 = ((blockIdx.y - g * P.ncg4) * kPbWaves + wave) * (16 * kPbCt);
+  const bool active = c0 < P.c;                         // idle waves still stage X
+  const int li = lane & 15, lq = lane >> 4;
+  const float* w = P.w + g * P.wg;
+  // A operands: tile t, k-block kb, part q; k-slot s of lane l is j = 32kb + 8*(l/16) + s
+  u4_t wa[3][kPbCt][KB];
+#pragma unroll
+  for (int t = 0; t < kPbCt; ++t) {
+    const int cc = c0 + 16 * t + li;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int s = 0; s < 8; s += 2) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int jj = 32 * kb + 8 * lq + s + e;
+          v[e] = 0.f;
+          if (active && cc < P.c) {
+            if (jj < P.j) v[e] = w[jj * P.ldw + cc];
+            else if (BIAS && jj == P.j) v[e] = P.bias[g * P.bg + cc];
+          }
+        }
+        uint32_t part[3];
+        split3(v[0], v[1], part);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) wa[q][t][kb][s / 2] = part[q];
+      }
+    }
+  }
+  // output of tile t: columns cb .. cb+3 (cb = c0 + 16t + 4lq) of row n0 + li
+  uint32_t yo[kPbCt];
+#pragma unroll
+  for (int t = 0; t < kPbCt; ++t) {
+    const int cb = c0 + 16 * t + 4 * lq;
+    yo[t] = (active && cb < P.c) ? 4u * static_cast<uint32_t>(li * P.ldy + cb) : kOob;
+  }
+  // X elements of this thread: column `lane` of the step rows wave + kPbWaves*i; columns
+  // J .. 32KB hold the ones column (with a bias) and zeros
+  constexpr int XE = kPbRows / kPbWaves;
+  const bool xin = lane < P.j;
+  const float xpad = (BIAS && lane == P.j) ? 1.f : 0.f;
+  const uint32_t xo = xin ? 4u * static_cast<uint32_t>(wave * P.ldx + lane) : kOob;
+  const uint32_t xstep = 4u * static_cast<uint32_t>(kPbWaves * P.ldx);
+  const float* xbase = P.x + g * P.xg;
+  float* ybase = P.y + g * P.yg;
+  const int64_t steps = (P.n + kPbRows - 1) / kPbRows;
+  float xv[XE];
+  auto gload = [&](int64_t step) {
+    const int64_t n0 = step * kPbRows;
+    const int64_t rows = P.n - n0 < kPbRows ? P.n - n0 : kPbRows;
+    const rsrc_t rx = rsrc(xbase + n0 * P.ldx, rows > 0 ? 4 * ((rows - 1) * P.ldx + P.j) : 0);
+#pragma unroll
+    for (int i = 0; i < XE; ++i) xv[i] = ld1(rx, xo == kOob ? kOob : xo + i * xstep);
+  };
+  auto lstore = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < XE; i += 2) {
+      uint32_t part[3];
+      split3(xin ? xv[i] : xpad, xin ? xv[i + 1] : xpad, part);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        xp[b][q][wave + kPbWaves * i][lane] = static_cast<uint16_t>(part[q] & 0xffffu);
+        xp[b][q][wave + kPbWaves * (i + 1)][lane] = static_cast<uint16_t>(part[q] >> 16);
+      }
+    }
+  };
+  // the k-blocks past 64 j (KB = 3: j = 64 with the bias row) read LDS columns 64 .. 95,
+  // which this layout does not hold: KB is at most 2 here
+  static_assert(KB <= 2, "head_proj_bf covers j + bias <= 64");
+  int64_t step = blockIdx.x;
+  gload(step);
+  lstore(0);
+  __syncthreads();
+  int b = 0;
+  constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
+  constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
+  for (; step < steps; step += gridDim.x) {
+    gload(step + gridDim.x);
+    pin();
+    if (active) {
+#pragma unroll
+      for (int rt = 0; rt < kPbRows / 16; ++rt) {
+        u4_t xb[3][KB];
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+            xb[q][kb] = *reinterpret_cast<const u4_t*>(&xp[b][q][16 * rt + li][32 * kb + 8 * lq]);
+        f4 acc[kPbCt];
+#pragma unroll
+        for (int t = 0; t < kPbCt; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pr = 0; pr < 6; ++pr) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int t = 0; t < kPbCt; ++t)
+              acc[t] = mfma_bf(wa[kPa[pr]][t][kb], xb[kPb[pr]][kb], acc[t]);
+          }
+        }
+        const rsrc_t ry = tile_rsrc(ybase, P.n, step * kPbRows + 16 * rt, P.ldy, P.c);
+#pragma unroll
+        for (int t = 0; t < kPbCt; ++t) st4(ry, yo[t], acc[t]);
+      }
+    }
+    lstore(b ^ 1);
+    __syncthreads();
+    b ^= 1;
+  }
+}
+
 // out[i] = sum over chunks k of part[k*stride + i], in chunk order: 32 outputs per
 // workgroup, 8 threads per output each summing every 8th chunk, then the 8 partial sums
 // in order through LDS.
@@ -871,6 +1002,10 @@ __global__ __launch_bounds__(kBlock) void chunk_sums4(const float* part, int chu
 
 constexpr int kGemmBlocks = 1024;  // workgroups of the row-tile launches
 constexpr size_t kMaxReduceLds = 160 * 1024;
+#ifndef FA_PROJ_BF
+#define FA_PROJ_BF 1
+#endif
+constexpr bool kProjBf = FA_PROJ_BF != 0;  // proj on the split-bf16 kernel (j + bias <= 64)
 #ifndef FA_REDUCE_BF
 #define FA_REDUCE_BF 1
 #endif
@@ -993,6 +1128,22 @@ extern "C" int fa_head_proj_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
   P.x = x; P.ldx = ldx; P.xg = xg; P.w = w; P.wg = wg; P.ldw = ldw;
   P.bias = bias; P.bg = bg; P.y = y; P.yg = yg; P.ldy = ldy;
   P.vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
+  const int jb = j + (bias ? 1 : 0);   // k rows with the bias row
+  if (kProjBf && P.vec && jb <= 64) {
+    // split-bf16 kernel: 8 waves of 48 columns per workgroup
+    P.ncg4 = static_cast<int>(ceil_div(ceil_div(c, 16 * kPbCt), kPbWaves));
+    const int gyb = groups * P.ncg4;
+    void (*k)(ProjParams) = nullptr;
+    if (jb <= 32) k = bias ? head_proj_bf<1, true> : head_proj_bf<1, false>;
+    else k = bias ? head_proj_bf<2, true> : head_proj_bf<2, false>;
+    const int64_t steps = ceil_div(n, kPbRows);
+    int64_t gx = resident_blocks(reinterpret_cast<const void*>(k), 0, kPbBlock) / gyb;
+    if (gx > steps) gx = steps;
+    if (gx < 1) gx = 1;
+    hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gyb)),
+                       dim3(kPbBlock), 0, stream, P);
+    return launch_status();
+  }
   const int ncg = static_cast<int>(ceil_div(c, 16 * kProjCt));
   P.ncg4 = static_cast<int>(ceil_div(ncg, kWavesPerBlock));
   const int gy = groups * P.ncg4;

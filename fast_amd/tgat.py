@@ -393,6 +393,20 @@ def _reduce(y, w):
     return z.transpose(0, 1).reshape(y.shape[1], G * J)
 
 
+def _rows_mm(x, a):
+    """x @ a^T for x [N, K] with many rows and a small a [M, K]: the per-head reduce kernel
+    with every group reading the same rows of x (fastAgg.head_reduce with a zero group
+    stride; M split into G groups of at most HEAD_KERNEL_MAX_J rows of a), used where its
+    split-bf16 form applies (rows of x in whole 16-byte chunks); torch's GEMM otherwise."""
+    m, k = a.shape
+    g = next((d for d in range(1, m + 1) if m % d == 0 and m // d <= HEAD_KERNEL_MAX_J), None)
+    if (g is None or x.dim() != 2 or x.stride(1) != 1 or k % 4 or x.stride(0) % 4
+            or x.data_ptr() % 16):
+        return x @ a.t()
+    a = a.contiguous()
+    return fastAgg.head_reduce(x.unsqueeze(0).expand(g, x.shape[0], k), a.view(g, m // g, k))
+
+
 class _SplitRows(torch.autograd.Function):
     """(h[:n], h[n:]): the destination rows and the rows feeding the edges of a dense
     source-feature tensor. Its backward concatenates the two gradients into one tensor (two
@@ -483,19 +497,20 @@ class TgatEpilogue(torch.autograd.Function):
 
 
 class RowsMM(torch.autograd.Function):
-    """y = x W^T for x [N, K] with many rows and a small W [M, K] (no bias). The weight
-    gradient x^T dy is the split-row reduction of fastAgg.head_wgrad (deterministic)."""
+    """y = x W^T for x [N, K] with many rows and a small W [M, K] (no bias), and dx = dy W,
+    on the per-head reduce kernel (`_rows_mm`). The weight gradient x^T dy is the split-row
+    reduction of fastAgg.head_wgrad (deterministic)."""
 
     @staticmethod
     def forward(ctx, x, W):
         ctx.save_for_backward(x, W)
-        return x @ W.t()
+        return _rows_mm(x, W)
 
     @staticmethod
     def backward(ctx, dy):
         x, W = ctx.saved_tensors
         dy = dy.contiguous()
-        dx = dy @ W if ctx.needs_input_grad[0] else None
+        dx = _rows_mm(dy, W.t()) if ctx.needs_input_grad[0] else None
         dW = None
         if ctx.needs_input_grad[1]:   # dy^T x, written [M, K] (no transposed view)
             dW = fastAgg.head_wgrad(dy, x.unsqueeze(0), 1, False)[0]
@@ -510,7 +525,7 @@ class DstProj(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, Wq, Wr):
         ctx.save_for_backward(h, Wq, Wr)
-        t = h @ torch.cat([Wq, Wr], 0).t()
+        t = _rows_mm(h, torch.cat([Wq, Wr], 0))
         mq = Wq.shape[0]
         return t[:, :mq], t[:, mq:]
 

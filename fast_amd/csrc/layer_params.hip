@@ -90,14 +90,19 @@ __global__ __launch_bounds__(kBlock) void layer_params_fwd(LpParams P, const flo
     P.wk_aug[e] = aug_value(P.wk, P.ldk, P.bk, P, i, c);
     P.wv_aug[e] = aug_value(P.wv, P.ldv, P.bv, P, i, c);
   }
-  for (int64_t e = tid; e < static_cast<int64_t>(P.H) * P.kp; e += stride) {
+  // qbk[h, c] = sum_j qb[h*dh + j] wk_aug[h*dh + j, c]: a wave per output, lanes over j,
+  // fixed-order wave sums (a thread per output would wait on dh loads in a row)
+  const int64_t wave = tid / kWave, waves = stride / kWave;
+  const int lane = lane_id();
+  for (int64_t e = wave; e < static_cast<int64_t>(P.H) * P.kp; e += waves) {
     const int h = static_cast<int>(e / P.kp), c = static_cast<int>(e - static_cast<int64_t>(h) * P.kp);
     float s = 0.f;
-    for (int j = 0; j < P.dh; ++j) {
+    for (int j = lane; j < P.dh; j += kWave) {
       const int i = h * P.dh + j;
       s = fmaf(qb[i], aug_value(P.wk, P.ldk, P.bk, P, i, c), s);
     }
-    P.qbk[e] = s;
+    s = wave_sum(s);
+    if (lane == 0) P.qbk[e] = s;
   }
   for (int64_t e = tid; e < static_cast<int64_t>(P.D) * P.Dn; e += stride) {
     const int i = static_cast<int>(e / P.Dn), n = static_cast<int>(e - static_cast<int64_t>(i) * P.Dn);
@@ -148,10 +153,14 @@ __global__ __launch_bounds__(kBlock) void layer_params_bwd(LpParams P, const flo
   }
   for (int64_t e = tid; e < P.D; e += stride) P.d_bq[e] = dqb[e];
   // b_t: -sin(b_t[t]) sum_i dqb[i] W_q[i, Dn + t]
-  for (int64_t t = tid; t < P.Dt; t += stride) {
+  // (a wave per t, lanes over i, fixed-order wave sums)
+  const int64_t wave = tid / kWave, waves = stride / kWave;
+  const int lane = lane_id();
+  for (int64_t t = wave; t < P.Dt; t += waves) {
     float s = 0.f;
-    for (int i = 0; i < P.D; ++i) s = fmaf(dqb[i], P.wq[i * P.ldq + P.Dn + t], s);
-    P.d_bt[t] = -sinf(P.bt[t]) * s;
+    for (int i = lane; i < P.D; i += kWave) s = fmaf(dqb[i], P.wq[i * P.ldq + P.Dn + t], s);
+    s = wave_sum(s);
+    if (lane == 0) P.d_bt[t] = -sinf(P.bt[t]) * s;
   }
   // W_o = [wo1 | wo2]
   const int do_in = P.D + P.Dn;

@@ -627,7 +627,7 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
                                       uint64_t drop_seed, double drop_p,
                                       std::optional<at::Tensor> xbar, at::Tensor scores,
                                       at::Tensor stats, at::Tensor dxbar, bool need_d_node,
-                                      std::optional<at::Tensor> tdot) {
+                                      std::optional<at::Tensor> tdot, int64_t d_node_front) {
   fa_tgat_graph g = make_graph(rowptr, node_tab, node_idx, edge_tab, edge_idx, dt, time_w, time_b);
   TORCH_CHECK(qt.dim() == 3, "qt must be [heads, n_dst, Kp]");
   const int64_t H = qt.size(0);
@@ -662,8 +662,12 @@ std::vector<at::Tensor> tgat_attn_bwd(at::Tensor rowptr, at::Tensor node_tab,
   }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(qt.device());
   auto dqt = new_block(H, g.n_dst, qt.size(2), qt.options());
+  // d_node: rows [d_node_front, d_node_front + E) of one allocation, the rows in front left
+  // for the caller (the gradient of the destination rows of the same source tensor)
+  TORCH_CHECK(d_node_front >= 0, "d_node_front must be >= 0");
   at::Tensor d_node;
-  if (need_d_node) d_node = at::empty({g.n_edges, g.dn}, qt.options());
+  if (need_d_node)
+    d_node = at::empty({d_node_front + g.n_edges, g.dn}, qt.options()).narrow(0, d_node_front, g.n_edges);
   auto d_tw = at::empty({g.dt_dim}, qt.options());
   auto d_tb = at::empty({g.dt_dim}, qt.options());
   const size_t sb = fa_tgat_attn_bwd_scratch_bytes(g.n_dst, g.dt_dim);
@@ -1071,7 +1075,7 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("dt"), py::arg("time_w"), py::arg("time_b"), py::arg("qt"), py::arg("slope"),
         py::arg("drop"), py::arg("drop_seed"), py::arg("drop_p"), py::arg("xbar"),
         py::arg("scores"), py::arg("stats"), py::arg("dxbar"), py::arg("need_d_node"),
-        py::arg("tdot") = py::none());
+        py::arg("tdot") = py::none(), py::arg("d_node_front") = 0);
   m.def("dropout_mask", &dropout_mask, "multipliers of the hashed attention dropout",
         py::arg("n_edges"), py::arg("heads"), py::arg("seed"), py::arg("p"), py::arg("device"));
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",

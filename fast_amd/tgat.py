@@ -278,14 +278,18 @@ timer: Optional[KernelTimer] = None  # set by a benchmark to time the fused kern
 class _Graph:
     """Non-differentiable per-block operands of the fused kernels."""
 
-    __slots__ = ("rowptr", "node_idx", "edge_tab", "edge_idx", "dt")
+    __slots__ = ("rowptr", "node_idx", "edge_tab", "edge_idx", "dt", "node_front")
 
-    def __init__(self, rowptr, node_idx, edge_tab, edge_idx, dt):
+    def __init__(self, rowptr, node_idx, edge_tab, edge_idx, dt, node_front: int = 0):
         self.rowptr = rowptr
         self.node_idx = node_idx
         self.edge_tab = edge_tab
         self.edge_idx = edge_idx
         self.dt = dt
+        # rows of the source tensor in front of the edge rows (the destination rows, when the
+        # edge rows are h[N:] of a dense h): the backward leaves them free in front of the
+        # edge-row gradient so that the two gradients form one tensor without a copy
+        self.node_front = node_front
 
 
 class TgatAttention(torch.autograd.Function):
@@ -339,7 +343,8 @@ class TgatAttention(torch.autograd.Function):
                                                         time_b, qt, ctx.slope, drop,
                                                         ctx.drop_seed, ctx.drop_p,
                                                         None if tdot is not None else xbar,
-                                                        scores, stats, dxbar, need_node, tdot)
+                                                        scores, stats, dxbar, need_node, tdot,
+                                                        g.node_front if g.node_idx is None else 0)
         if t0 is not None:
             nb = fused_kernel_bytes(qt.shape[1], g.dt.numel(), node_src.shape[1],
                                     g.edge_tab.shape[1], time_w.numel(), qt.shape[0],
@@ -421,6 +426,13 @@ class _SplitRows(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_dst, g_src):
         n, (rows, dim) = ctx.n, ctx.shape
+        base = g_src._base if g_src is not None else None
+        if (g_dst is not None and base is not None and base.shape == (rows, dim)
+                and base.is_contiguous() and g_src.data_ptr() == base[n:].data_ptr()):
+            # the fused backward wrote g_src into rows n.. of a full-size tensor (its
+            # d_node_front): fill the rows in front instead of concatenating
+            base[:n].copy_(g_dst)
+            return base, None
         if g_dst is None:
             g_dst = torch.zeros(n, dim, device=g_src.device, dtype=g_src.dtype)
         if g_src is None:
@@ -687,7 +699,8 @@ class TransfomerAttentionLayer(torch.nn.Module):
         else:
             tw = tb = torch.empty(0, device=dev)
             dt = torch.zeros(E, device=dev)
-        g = _Graph(b.rowptr(), node_idx, edge_tab, edge_idx, dt)
+        split = Dn > 0 and "h" in b.srcdata
+        g = _Graph(b.rowptr(), node_idx, edge_tab, edge_idx, dt, N if split else 0)
         link = _TdotLink()
         xbar = TgatAttention.apply(qt, tw, tb, node_src, g, self.negative_slope, drop, drop_seed,
                                    drop_p, link)

@@ -247,3 +247,24 @@ def test_to_blocks_mirrors_to_dgl_blocks():
     assert torch.equal(s2, torch.from_numpy(r.row()).long()) and rb.num_dst_nodes() == r.dim_in()
     assert torch.equal(rb.dstdata["ID"], torch.from_numpy(r.nodes()))
     assert torch.equal(rb.edata["dt"], torch.from_numpy(r.dts())[r.dim_out():])
+
+
+def test_split_rows_backward_fills_the_rows_in_front():
+    """_SplitRows.backward: when the edge-row gradient is rows n.. of a full-size tensor (the
+    fused backward's d_node_front), the destination-row gradient goes into the rows in front
+    and that tensor is the result (no concatenation); any other gradient is concatenated."""
+    class Ctx:
+        n, shape = 4, (10, 3)
+
+    gen = torch.Generator().manual_seed(0)
+    full = torch.zeros(10, 3)
+    g_src = full[4:]
+    g_src.copy_(torch.randn(6, 3, generator=gen))
+    g_dst = torch.randn(4, 3, generator=gen)
+    want = torch.cat([g_dst, g_src])
+    out, _ = tgat._SplitRows.backward(Ctx(), g_dst, g_src)
+    assert out.data_ptr() == full.data_ptr() and torch.equal(out, want)
+    out2, _ = tgat._SplitRows.backward(Ctx(), g_dst, g_src.clone())
+    assert torch.equal(out2, want)
+    out3, _ = tgat._SplitRows.backward(Ctx(), None, g_src.clone())
+    assert torch.equal(out3[:4], torch.zeros(4, 3)) and torch.equal(out3[4:], g_src)

@@ -379,6 +379,28 @@ __device__ __forceinline__ void load_rows(const float* base, int64_t rs, int64_t
   }
 }
 
+// q~ chunks the backward reads: the node chunks (with a node-row gradient) and the time
+// chunks (the time gradient); the edge chunks and the bias chunk enter no gradient through q~.
+__device__ __forceinline__ bool q_chunk_used(const TgatParams& P, int c) {
+  const int t0 = P.cn + P.ce;
+  return (c >= t0 && c < t0 + P.ct) || (P.d_node && c < P.cn);
+}
+
+// load_rows of q~ for the backward: the chunks it does not read come back as zeros, unread.
+template <int H, int NS>
+__device__ __forceinline__ void load_q_rows(const TgatParams& P, int64_t v, float4 (&r)[H][NS]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const rsrc_t rr = make_rsrc(P.qt + v * P.qt_rs + h * P.qt_hs, 4u * static_cast<uint32_t>(P.kp));
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int c = lane + k * kWave;
+      r[h][k] = bload4(rr, q_chunk_used(P, c) ? 16u * static_cast<uint32_t>(c) : 0x7ffffff0u);
+    }
+  }
+}
+
 template <int H, int NS>
 __device__ __forceinline__ void store_rows(float* base, int64_t rs, int64_t hs, int64_t v,
                                            int64_t kp, const float4 (&r)[H][NS]) {
@@ -954,7 +976,7 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     int cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
     EdgeMeta<H, true> M;
     stage_meta<H, true>(P, c0, cnt, M);
-    load_rows<H, NS>(P.qt, P.qt_rs, P.qt_hs, v, P.kp, S.q);
+    load_q_rows<H, NS>(P, v, S.q);
     load_rows<H, NS>(P.dxbar, P.dxbar_rs, P.dxbar_hs, v, P.kp, S.g);
 #pragma unroll
     for (int h = 0; h < H; ++h) {
@@ -1183,7 +1205,8 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     stage_meta<H, true>(P, c0, cnt, M);
     float4 xa[NS], xb[NS];
     pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
-    // the destination's rows: q~ and dxbar into LDS, T = dxbar . xbar per head
+    // the destination's rows: q~ (the chunks the backward reads, q_chunk_used) and dxbar
+    // into LDS, T = dxbar . xbar per head
     lds_sync();  // the previous destination's reads of qs / gs are done
 #pragma unroll
     for (int h = 0; h < H; ++h) {
@@ -1197,7 +1220,7 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
           const int c = lane + r * kWave;
-          qv[r] = c < P.cp ? qr[c] : f4_zero();
+          qv[r] = c < P.cp && q_chunk_used(P, c) ? qr[c] : f4_zero();
           gv[r] = c < P.cp ? gr[c] : f4_zero();
         }
 #pragma unroll
@@ -1213,7 +1236,7 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
         const float4* xr = reinterpret_cast<const float4*>(P.xbar + v * P.xbar_rs + h * P.xbar_hs);
         for (int c = lane; c < P.cp; c += kWave) {
           const float4 g = gr[c];
-          qs[h * QS + c] = qr[c];
+          qs[h * QS + c] = q_chunk_used(P, c) ? qr[c] : f4_zero();
           gs[h * QS + c] = g;
           d += dot4(g, xr[c]);
         }

@@ -219,14 +219,17 @@ def fused_kernel_bytes(n_dst: int, n_edges: int, dn: int, de: int, dt: int, head
                + score (4*heads, written / read)
                [+ d_node row (4*dn) written in backward when requested]
     per dst  : forward  qt read + xbar written (2 * 4*heads*Kp) + stats written (8*heads)
-               backward qt, xbar, dxbar read + dqt written (4 * 4*heads*Kp) + stats read (8*heads);
+               backward dxbar, xbar read + dqt written (3 * 4*heads*Kp) + stats read (8*heads)
+               + the qt chunks the backward uses (4*heads*4*(ct + cn with d_node): the time
+               part, and the node part when the node-row gradient is written);
                with ``tdot`` the per-head dot products (4*heads) are read instead of xbar
     plus the row offsets 4*(n_dst+1) and the time parameters 8*dt."""
     kp = kspace_width(dn, de, dt)
     edge_in = (8 if node_idx else 0) + (8 if edge_idx else 0) + 4 + node_bytes * dn + edge_bytes * de
     common = 4 * (n_dst + 1) + 8 * dt
     fwd = common + n_edges * (edge_in + 4 * heads) + n_dst * (2 * 4 * heads * kp + 8 * heads)
-    dst_rows = (3 * 4 * heads * kp + 4 * heads) if tdot else 4 * 4 * heads * kp
+    q_read = 16 * heads * ((dt + 3) // 4 + ((dn + 3) // 4 if d_node else 0))
+    dst_rows = q_read + ((2 * 4 * heads * kp + 4 * heads) if tdot else 3 * 4 * heads * kp)
     bwd = (common + n_edges * (edge_in + 4 * heads + (4 * dn if d_node else 0))
            + n_dst * (dst_rows + 8 * heads))
     return {"fwd": fwd, "bwd": bwd}

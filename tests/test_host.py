@@ -136,9 +136,15 @@ def test_fused_kernel_bytes_accounting():
     b = tgat.fused_kernel_bytes(n, e, dn, de, dt, H, True, True)
     per_edge = 8 + 8 + 4 + 4 * (dn + de) + 4 * H
     assert b["fwd"] == 4 * (n + 1) + 8 * dt + e * per_edge + n * (8 * H * kp + 8 * H)
-    assert b["bwd"] == 4 * (n + 1) + 8 * dt + e * per_edge + n * (16 * H * kp + 8 * H)
+    # backward: xbar and dxbar read, dqt written, and of qt the time chunks (25 here) read;
+    # with the node-row gradient also qt's node chunks (25) and the rows written
+    q_time, q_node = 16 * H * 25, 16 * H * 25
+    assert b["bwd"] == 4 * (n + 1) + 8 * dt + e * per_edge + n * (12 * H * kp + q_time + 8 * H)
     assert tgat.fused_kernel_bytes(n, e, dn, de, dt, H, True, True, d_node=True)["bwd"] == \
-        b["bwd"] + e * 4 * dn
+        b["bwd"] + e * 4 * dn + n * q_node
+    # with T = dxbar . xbar given, xbar's rows are replaced by one float per head
+    assert tgat.fused_kernel_bytes(n, e, dn, de, dt, H, True, True, tdot=True)["bwd"] == \
+        b["bwd"] - n * (4 * H * kp - 4 * H)
 
 
 def test_layer_construction_order_matches_reference():

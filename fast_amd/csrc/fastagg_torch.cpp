@@ -719,7 +719,8 @@ at::Tensor tgat_attn_weights(at::Tensor dst, at::Tensor scores, at::Tensor stats
   return att;
 }
 
-at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n) {
+// -> [n, max(dim, width)] float32; columns past dim (when width > dim) are zero
+at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n, int64_t width) {
   check_table(tab, "tab");
   const int64_t* ip = nullptr;
   if (idx.has_value()) {
@@ -729,15 +730,17 @@ at::Tensor gather_rows(at::Tensor tab, std::optional<at::Tensor> idx, int64_t n)
     ip = idx->data_ptr<int64_t>();
   }
   c10::hip::HIPGuardMasqueradingAsCUDA guard(tab.device());
-  auto out = at::empty({n, tab.size(1)}, tab.options().dtype(at::kFloat));
+  const int64_t ow = width > tab.size(1) ? width : tab.size(1);
+  auto out = at::empty({n, ow}, tab.options().dtype(at::kFloat));
+  if (ow > tab.size(1) && n > 0) out.narrow(1, tab.size(1), ow - tab.size(1)).zero_();
   const int64_t ld = tab.size(1) > 0 ? tab.stride(0) : 0;
   const int32_t dim = static_cast<int32_t>(tab.size(1));
   const int st = tab.scalar_type() == at::kBFloat16
                      ? fa_gather_rows_bf16_f32(reinterpret_cast<const uint16_t*>(tab.data_ptr()), ld,
-                                               tab.size(0), ip, n, dim, out.data_ptr<float>(), dim,
+                                               tab.size(0), ip, n, dim, out.data_ptr<float>(), ow,
                                                stream_of(tab))
                      : fa_gather_rows_f32(tab.data_ptr<float>(), ld, tab.size(0), ip, n, dim,
-                                          out.data_ptr<float>(), dim, stream_of(tab));
+                                          out.data_ptr<float>(), ow, stream_of(tab));
   check_status(st, "gather_rows");
   return out;
 }
@@ -1081,7 +1084,7 @@ PYBIND11_MODULE(fastAgg, m) {
   m.def("tgat_attn_weights", &tgat_attn_weights, "normalised attention from scores and stats",
         py::arg("dst"), py::arg("scores"), py::arg("stats"));
   m.def("gather_rows", &gather_rows, "row gather tab[idx] (float32 or bf16 table, float32 rows)", py::arg("tab"), py::arg("idx"),
-        py::arg("n"));
+        py::arg("n"), py::arg("width") = 0);
   m.def("head_proj", &head_proj, "per-head projection y[g] = x[:, g-block] @ w[g] (+ bias[g])",
         py::arg("x"), py::arg("w"), py::arg("bias") = py::none());
   m.def("head_reduce", &head_reduce, "per-head transpose product z[:, g-block] = y[g] @ w[g]^T",

@@ -108,13 +108,16 @@ class Block:
         return b
 
     # -- feature access -----------------------------------------------------------------
-    def dst_node_feats(self) -> Optional[torch.Tensor]:
+    def dst_node_feats(self, pad4: bool = False) -> Optional[torch.Tensor]:
+        """The destination rows' node features [N, Dn]; with ``pad4`` and a gathered table,
+        [N, Dn rounded up to 4] with zero columns past Dn (rows in whole 16-byte chunks)."""
         N = self._num_dst
         if "h" in self.srcdata:
             return self.srcdata["h"][:N]
         if self.node_table is not None:
             ids = self.srcdata["ID"][:N]
-            return fastAgg.gather_rows(self.node_table, ids, N)
+            width = -(-self.node_table.shape[1] // 4) * 4 if pad4 else 0
+            return fastAgg.gather_rows(self.node_table, ids, N, width)
         return None
 
     def src_node_source(self):
@@ -663,8 +666,10 @@ class TransfomerAttentionLayer(torch.nn.Module):
         node_src = node_idx = None
         if Dn > 0 and "h" in b.srcdata:
             hdst, node_src = _SplitRows.apply(b.srcdata["h"], N)
+            if Dn % 4:   # rows in whole 16-byte chunks for the row products, as gathered ones
+                hdst = torch.nn.functional.pad(hdst, (0, (-Dn) % 4))
         else:
-            hdst = b.dst_node_feats() if Dn > 0 else None
+            hdst = b.dst_node_feats(pad4=True) if Dn > 0 else None
             if Dn > 0:
                 node_src, node_idx = b.src_node_source()
         kp = kspace_width(Dn, De, Dt)
@@ -677,6 +682,9 @@ class TransfomerAttentionLayer(torch.nn.Module):
                 self.w_q.weight, self.w_q.bias, self.w_k.weight, self.w_k.bias, self.w_v.weight,
                 self.w_v.bias, self.time_enc.w.bias if Dt > 0 else None, Wo, (H, Dn, De, Dt))
             wk, wv = wk.view(H, dh, kp), wv.view(H, dh, kp)
+            if hdst.shape[1] > Dn:   # zero-padded rows: the weights take zero columns to match
+                wq_node = torch.nn.functional.pad(wq_node, (0, hdst.shape[1] - Dn))
+                wo2 = torch.nn.functional.pad(wo2, (0, hdst.shape[1] - Dn))
             # Absorbed keys, head by head: qt[h, v, :] = Q[v, h, :] W_k,aug[h], with
             # q = hdst W_q[:, :Dn]^T and the h_dst half of w_out from one product
             q, r2 = DstProj.apply(hdst, wq_node, wo2)

@@ -691,8 +691,18 @@ __global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
 }
 
 // ----- reduce on the bf16 matrix cores ----------------------------------------------------
-constexpr int kRbWaves = 12;   // waves per workgroup (one workgroup per CU: W's parts fill LDS)
+#ifndef FA_RB_WAVES
+#define FA_RB_WAVES 12
+#endif
+#ifndef FA_RB_TILES
+#define FA_RB_TILES 2
+#endif
+#ifndef FA_RB_MINW
+#define FA_RB_MINW 3
+#endif
+constexpr int kRbWaves = FA_RB_WAVES;  // waves per workgroup (one per CU: W's parts fill LDS)
 constexpr int kRbBlock = kRbWaves * kWave;
+constexpr int kRbTiles = FA_RB_TILES;  // 16-row tiles per wave step (share the B operands)
 constexpr int kRbDepth = 2;    // k-blocks of Y in flight ahead of the one multiplied
 
 // LDS row (bf16) of the split W[g]: the k-blocks, plus 8 so that the rows of a 16-lane read
@@ -709,7 +719,7 @@ size_t reduce_bf_lds_bytes(int j, int c) {
 // that a lane's A values are two float4 loads whose 16 lanes of a row read 64 contiguous
 // bytes; W is stored in LDS in that order.
 template <int JT>
-__global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
+__global__ __launch_bounds__(kRbBlock, FA_RB_MINW) void head_reduce_bf(ReduceParams P) {
   extern __shared__ __align__(16) uint16_t wlb[];
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -734,31 +744,33 @@ __global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
   for (int jt = 0; jt < JT; ++jt) wrow[jt] = (16 * jt + li < P.j ? 16 * jt + li : P.j) * cp + 8 * lq;
   const int plane = rows * cp;
   const float* ybase = P.y + g * P.yg;
-  const int64_t pairs = (P.n + 31) / 32;
+  const int64_t pairs = (P.n + 16 * kRbTiles - 1) / (16 * kRbTiles);
   const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
   for (int64_t pr = static_cast<int64_t>(blockIdx.x) * kRbWaves + wave; pr < pairs;
        pr += static_cast<int64_t>(gridDim.x) * kRbWaves) {
-    const int64_t n0 = pr * 32;
-    const rsrc_t ry0 = tile_rsrc(ybase, P.n, n0, P.ldy, P.c);
-    const rsrc_t ry1 = tile_rsrc(ybase, P.n, n0 + 16, P.ldy, P.c);
+    const int64_t n0 = pr * 16 * kRbTiles;
+    rsrc_t ry[kRbTiles];
+#pragma unroll
+    for (int u = 0; u < kRbTiles; ++u) ry[u] = tile_rsrc(ybase, P.n, n0 + 16 * u, P.ldy, P.c);
     // the two float4 of each tile for k-block kb (columns past C read 0)
-    auto ly = [&](int kb, f4 (&v)[2][2]) {
+    auto ly = [&](int kb, f4 (&v)[kRbTiles][2]) {
       const int c0 = 32 * kb + 4 * lq, c1 = c0 + 16;
       const uint32_t o0 = c0 < P.c ? yrow + 4u * c0 : kOob, o1 = c1 < P.c ? yrow + 4u * c1 : kOob;
-      v[0][0] = ld4(ry0, o0);
-      v[0][1] = ld4(ry0, o1);
-      v[1][0] = ld4(ry1, o0);
-      v[1][1] = ld4(ry1, o1);
-    };
-    f4 acc[2][JT];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < kRbTiles; ++u) {
+        v[u][0] = ld4(ry[u], o0);
+        v[u][1] = ld4(ry[u], o1);
+      }
+    };
+    f4 acc[kRbTiles][JT];
+#pragma unroll
+    for (int u = 0; u < kRbTiles; ++u)
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) acc[u][jt] = f4{0.f, 0.f, 0.f, 0.f};
-    auto mm = [&](int kb, const f4 (&v)[2][2]) {
-      u4_t ap[2][3];
+    auto mm = [&](int kb, const f4 (&v)[kRbTiles][2]) {
+      u4_t ap[kRbTiles][3];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < kRbTiles; ++u) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -781,14 +793,14 @@ __global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
 #pragma unroll
       for (int q = 0; q < 6; ++q) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < kRbTiles; ++u) {
 #pragma unroll
           for (int jt = 0; jt < JT; ++jt) acc[u][jt] = mfma_bf(ap[u][kPa[q]], bp[kPb[q]][jt], acc[u][jt]);
         }
       }
     };
     // issued in order: ya[0] is the oldest; kRbDepth k-blocks in flight
-    f4 ya[kRbDepth][2][2];
+    f4 ya[kRbDepth][kRbTiles][2];
 #pragma unroll
     for (int d = 0; d < kRbDepth; ++d) {
       ly(d, ya[d]);
@@ -805,7 +817,7 @@ __global__ __launch_bounds__(kRbBlock, 3) void head_reduce_bf(ReduceParams P) {
     }
     // D row 4lq + r of tile u, column 16jt + li
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kRbTiles; ++u) {
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) {
         const int jj = 16 * jt + li;
@@ -1200,7 +1212,7 @@ extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t group
     if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess)
       return launch_status();
-    const int64_t pairs = ceil_div(n, 32);
+    const int64_t pairs = ceil_div(n, 16 * kRbTiles);
     int64_t gx = resident_blocks(kp, lds, kRbBlock) / groups;
     if (gx > ceil_div(pairs, kRbWaves)) gx = ceil_div(pairs, kRbWaves);
     if (gx < 1) gx = 1;

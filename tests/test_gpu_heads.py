@@ -138,3 +138,47 @@ def test_row_group_dots(dev, n, g, j):
     ref = (a.double().view(n, g, j) * b.double().view(n, g, j)).sum(-1)
     mag = (a.double().abs().view(n, g, j) * b.double().abs().view(n, g, j)).sum(-1)
     _bound_check(got, ref, mag, j, "row_group_dots")
+
+
+@pytest.mark.parametrize("op", ["proj", "reduce", "wgrad"])
+def test_head_ops_wide_magnitudes(dev, op):
+    """The split-bf16 kernels (every fp32 operand as three exact bf16 parts) meet the same
+    float64 error bound as float32 products when rows and columns span twelve decades
+    (scales 10^-6 .. 10^6): the split is exact at every exponent, not only near 1."""
+    from fast_amd import fastAgg
+
+    n, g, j, c = 2000, 2, 50, 376
+    gen = torch.Generator().manual_seed(11)
+    scale = lambda *s: 10.0 ** (torch.rand(*s, generator=gen) * 12 - 6)
+    x = torch.randn(n, g * j, generator=gen) * scale(n, 1) * scale(1, g * j)
+    w = torch.randn(g, j, c, generator=gen) * scale(g, j, 1) * scale(g, 1, c)
+    y = torch.randn(g, n, c, generator=gen) * scale(1, n, 1) * scale(g, 1, c)
+    b = torch.randn(g, c, generator=gen) * scale(g, c)
+    xh = x.view(n, g, j).transpose(0, 1).double()
+    xf = x.view(n, g, j).transpose(0, 1).contiguous()                           # [g, n, j] f32
+    if op == "proj":
+        got = fastAgg.head_proj(x.to(dev), w.to(dev), b.to(dev))
+        f32 = torch.matmul(xf.to(dev), w.to(dev)) + b.to(dev)[:, None, :]
+        ref = torch.matmul(xh, w.double()) + b.double()[:, None, :]
+        mag = torch.matmul(xh.abs(), w.double().abs()) + b.double().abs()[:, None, :]
+        _bound_check(got, ref, mag, j + 1, "head_proj")
+    elif op == "reduce":
+        got = fastAgg.head_reduce(y.to(dev), w.to(dev)).view(n, g, j).transpose(0, 1)
+        f32 = torch.matmul(y.to(dev), w.transpose(1, 2).contiguous().to(dev))
+        ref = torch.matmul(y.double(), w.double().transpose(1, 2).contiguous())
+        mag = torch.matmul(y.double().abs(), w.double().abs().transpose(1, 2).contiguous())
+        _bound_check(got, ref, mag, c, "head_reduce")
+    else:
+        got = fastAgg.head_wgrad(x.to(dev), y.to(dev), g, True)
+        f32 = torch.matmul(xf.transpose(1, 2).contiguous().to(dev), y.to(dev))
+        ref = torch.matmul(xh.transpose(1, 2).contiguous(), y.double())
+        mag = torch.matmul(xh.abs().transpose(1, 2).contiguous(), y.double().abs())
+        _bound_check(got[:, :j], ref, mag, n, "head_wgrad")
+        _bound_check(got[:, j], y.double().sum(1), y.double().abs().sum(1), n, "ones row")
+        got = got[:, :j]
+    # as accurate as a float32 product: the largest error relative to sum |a b| stays within a
+    # small factor of torch's float32 GEMM on the same operands (a split into two bf16 parts,
+    # or a dropped part product, is 2^8 times worse)
+    err = float(((got.double().cpu() - ref).abs() / mag).max())
+    err32 = float(((f32.double().cpu() - ref).abs() / mag).max())
+    assert err <= 8 * err32 + 1e-12, f"{op}: {err:.3e} against float32 {err32:.3e}"

@@ -835,7 +835,10 @@ __global__ __launch_bounds__(kRbBlock, FA_RB_MINW) void head_reduce_bf(ReducePar
 constexpr int kPbWaves = 8;                  // waves per workgroup (48 columns each)
 constexpr int kPbBlock = kPbWaves * kWave;
 constexpr int kPbCt = 3;                     // 16-column tiles per wave
-constexpr int kPbRows = 32;                  // rows per workgroup step (one LDS sync each)
+#ifndef FA_PB_ROWS
+#define FA_PB_ROWS 32
+#endif
+constexpr int kPbRows = FA_PB_ROWS;          // rows per workgroup step (one LDS sync each)
 constexpr int kPbXp = 72;                    // bf16 per LDS row of the split X: 64 j + 8
 
 // head_proj with the split-bf16 product (see head_wgrad_bf), formed transposed as head_proj:

@@ -30,6 +30,10 @@
 //   da'     = dxbar[h] . x_e
 //   dz      = a * (drop*da' - T_h) * leaky'(s)
 //   dqt[h] += dz * x_e
+//   (bias column of dqt, x_e = 1: with sum_e a = 1 and T_h = sum_e a*drop*da', the sum of dz
+//    over the destination's edges is -(1 - slope) * sum over the edges with s <= 0 of
+//    a * (drop*da' - T_h); that form is accumulated instead, since the plain sum of dz
+//    cancels to a small number and would keep only the rounding of its terms)
 //   dx_e    = sum_h a*drop*dxbar[h] + dz*qt[h]        -> node-row gradient, time-encoding grads
 #include <float.h>
 
@@ -871,6 +875,7 @@ struct BwdState {
   float4 q[H][NS], g[H][NS], dq[H][NS];
   float4 gw, gb;  // time-grad accumulators of this lane's time chunk (at most one: ct <= 64)
   float mh[H], il[H], T[H];  // row max, 1 / softmax denominator, dxbar . xbar
+  float cb[H];               // bias column of dq~ (the non-cancelling form, see top of file)
 };
 
 template <int H, int NS>
@@ -902,7 +907,9 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
       const float dr = lane_flt(M.dr[h], j);
       const float a = exp_fast(s - S.mh[h]) * S.il[h];
       ad[h] = a * dr;
-      dz[h] = a * (dr * dap[b][h] - S.T[h]) * (s > 0.f ? 1.f : P.slope);
+      const float gz = a * (dr * dap[b][h] - S.T[h]);
+      dz[h] = gz * (s > 0.f ? 1.f : P.slope);
+      S.cb[h] += s > 0.f ? 0.f : (P.slope - 1.f) * gz;
 #pragma unroll
       for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[b][k]);
     }
@@ -963,9 +970,11 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
     const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
 #pragma unroll
-    for (int h = 0; h < H; ++h)
+    for (int h = 0; h < H; ++h) {
+      S.cb[h] = 0.f;
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
+    }
     if (e1 <= e0) {
       store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
       continue;
@@ -1018,6 +1027,12 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
       stage_meta<H, true>(P, c0, cnt, M);
       issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     }
+    // the bias column of dq~ (chunk cp-1, component x) from cb
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+      for (int k = 0; k < NS; ++k)
+        if (lane_id() + k * kWave == P.cp - 1) S.dq[h][k].x = S.cb[h];
     store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
   }
 
@@ -1062,6 +1077,7 @@ struct PairBwd {
   float4 dq[H][NS];
   float4 gw, gb;              // time-grad accumulators of this lane's time chunk
   float mh[H], il[H], T[H];   // row max, 1 / softmax denominator, dxbar . xbar
+  float cb[H];                // bias column of dq~ (the non-cancelling form, see top of file)
 };
 
 template <int H, int NS>
@@ -1111,7 +1127,9 @@ __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx
     const float dr = pick_flt(M.dr[h], jj);
     const float a = valid ? exp_fast(sc - S.mh[h]) * S.il[h] : 0.f;
     ad[h] = a * dr;
-    dz[h] = a * (dr * dap[h] - S.T[h]) * (sc > 0.f ? 1.f : P.slope);
+    const float gz = a * (dr * dap[h] - S.T[h]);
+    dz[h] = gz * (sc > 0.f ? 1.f : P.slope);
+    S.cb[h] += sc > 0.f ? 0.f : (P.slope - 1.f) * gz;
 #pragma unroll
     for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[k]);
   }
@@ -1186,9 +1204,11 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
     const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
 #pragma unroll
-    for (int h = 0; h < H; ++h)
+    for (int h = 0; h < H; ++h) {
+      S.cb[h] = 0.f;
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
+    }
     if (e1 <= e0) {
 #pragma unroll
       for (int h = 0; h < H; ++h) {
@@ -1262,15 +1282,17 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
       stage_meta<H, true>(P, c0, cnt, M);
       pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
     }
-    // dq~ = the two halves' sums
+    // dq~ = the two halves' sums (the bias column from the halves' cb, merged by every lane)
 #pragma unroll
     for (int h = 0; h < H; ++h) {
+      const float cbs = S.cb[h] + pick_flt(S.cb[h], other);
       float* dst = P.dqt + v * P.dqt_rs + h * P.dqt_hs;
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
         const float4 o = pick_f4(S.dq[h][k], other);
         const float4 a = S.dq[h][k];
-        const float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+        float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
+        if (hl + k * kHalf == P.cp - 1) sum.x = cbs;
         if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = sum;
       }
     }
@@ -1817,16 +1839,15 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
   return static_cast<size_t>(bwd_grid(n_dst)) * 2 * static_cast<size_t>(dt_dim) * sizeof(float);
 }
 
-extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
-                                    int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
-                                    uint64_t drop_seed, float drop_p, const float* xbar,
-                                    int64_t xbar_rs, int64_t xbar_hs, const float* tdot,
-                                    const float* scores,
-                                    const float* stats, const float* dxbar, int64_t dxbar_rs,
-                                    int64_t dxbar_hs, float* dqt, int64_t dqt_rs, int64_t dqt_hs,
-                                    float* d_node, int64_t ld_dnode,
-                                    float* d_time_w, float* d_time_b, void* scratch,
-                                    size_t scratch_bytes, hipStream_t stream) {
+// The backward: `partial` is the caller's time-gradient scratch.
+static int tgat_bwd_impl(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                         int64_t qt_rs, int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
+                         float drop_p, const float* xbar, int64_t xbar_rs, int64_t xbar_hs,
+                         const float* tdot, const float* scores, const float* stats,
+                         const float* dxbar, int64_t dxbar_rs, int64_t dxbar_hs, float* dqt,
+                         int64_t dqt_rs, int64_t dqt_hs, float* d_node, int64_t ld_dnode,
+                         float* d_time_w, float* d_time_b, void* partial, size_t partial_bytes,
+                         hipStream_t stream) {
   TgatParams P;
   int st = fill_params(g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, P);
   if (st != FA_OK) return st;
@@ -1846,7 +1867,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   if (d_node && P.node_bf16) return FA_EUNSUPPORTED;  // node gradients for float32 rows only
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   int grid = bwd_grid(P.n_dst);   // the most workgroups a launch uses (scratch rows)
-  if (P.dt_dim > 0 && (!scratch || scratch_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
+  if (P.dt_dim > 0 && (!partial || partial_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
   P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs; P.tdot = tdot;
   P.dxbar = dxbar; P.dxbar_rs = dxbar_rs; P.dxbar_hs = dxbar_hs;
@@ -1854,7 +1875,7 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
   P.d_node = d_node; P.ld_dnode = ld_dnode; P.scores = const_cast<float*>(scores);
   // 16-byte node-gradient stores need 16-byte aligned gradient rows as well
   if (d_node && (!aligned16(d_node) || (ld_dnode & 3))) P.dnode_dwords = 1;
-  P.stats = const_cast<float*>(stats); P.partial = static_cast<float*>(scratch);
+  P.stats = const_cast<float*>(stats); P.partial = static_cast<float*>(partial);
   if (static_cast<int64_t>(kBatch) * heads > kWave) return FA_EUNSUPPORTED;
   switch (heads) {
     case 1: st = launch_bwd_h<1>(P, grid, stream); break;
@@ -1868,6 +1889,23 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
                      dim3(kBlock), 0, stream, P.partial, grid, P.dt_dim, d_time_w, d_time_b);
   return launch_status();
 }
+
+extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                                    int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
+                                    uint64_t drop_seed, float drop_p, const float* xbar,
+                                    int64_t xbar_rs, int64_t xbar_hs, const float* tdot,
+                                    const float* scores,
+                                    const float* stats, const float* dxbar, int64_t dxbar_rs,
+                                    int64_t dxbar_hs, float* dqt, int64_t dqt_rs, int64_t dqt_hs,
+                                    float* d_node, int64_t ld_dnode,
+                                    float* d_time_w, float* d_time_b, void* scratch,
+                                    size_t scratch_bytes, hipStream_t stream) {
+  return tgat_bwd_impl(g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, xbar,
+                       xbar_rs, xbar_hs, tdot, scores, stats, dxbar, dxbar_rs, dxbar_hs, dqt,
+                       dqt_rs, dqt_hs, d_node, ld_dnode, d_time_w, d_time_b, scratch,
+                       scratch_bytes, stream);
+}
+
 
 __global__ __launch_bounds__(kBlock) void dropout_mask(uint64_t seed, float p, float scale,
                                                       int64_t n, float* out) {

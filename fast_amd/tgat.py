@@ -279,6 +279,11 @@ class KernelTimer:
 
 
 timer: Optional[KernelTimer] = None  # set by a benchmark to time the fused kernels
+# When set to a list, each layer's forward appends its post-activation values, whose signs
+# are the branches its backward takes: ("score", [E, H] post-LeakyReLU scores) from the fused
+# kernel, then ("relu", [N, D] post-dropout, post-ReLU values) from the epilogue. A parity
+# test reads them.
+branch_sink: Optional[list] = None
 
 
 class _Graph:
@@ -320,6 +325,8 @@ class TgatAttention(torch.autograd.Function):
                                     node_bytes=node_src.element_size(),
                                     edge_bytes=g.edge_tab.element_size())["fwd"]
             timer.end("tgat_fwd", t0, nb)
+        if branch_sink is not None:
+            branch_sink.append(("score", scores))
         ctx.g = g
         ctx.link = link
         ctx.slope = float(slope)
@@ -499,6 +506,8 @@ class TgatEpilogue(torch.autograd.Function):
     def forward(ctx, r1, r2, bias, gamma, beta, eps: float, seed: int, p: float):
         out, y, stats = fastAgg.tgat_epilogue_fwd(r1, r2, bias, gamma, beta, float(eps),
                                                   int(seed), float(p))
+        if branch_sink is not None:
+            branch_sink.append(("relu", y))
         ctx.save_for_backward(y, stats, gamma)
         ctx.p = float(p)
         ctx.has_r2 = r2 is not None

@@ -263,15 +263,54 @@ def layer_params(layer) -> dict:
     return out
 
 
+# Half-width of the kink bands, relative to the absolute terms of the pre-activation value.
+KINK_RTOL = 1e-5
+
+
+def _kink(name, z, zabs, hint, slope, stats):
+    """The branch (z > 0) of a piecewise-linear activation, with an implementation's branch
+    taken inside the band |z| <= KINK_RTOL * zabs around the kink. ``hint`` holds the
+    implementation's post-activation values (their signs are its branches; slope > 0 maps
+    them back to its pre-activation values, which give the deviation statistics)."""
+    with torch.no_grad():
+        near = z.abs() <= KINK_RTOL * zabs
+        mine = hint > 0
+        pos = torch.where(near, mine, z > 0)
+        if stats is not None:
+            pre = torch.where(mine, hint, hint / slope) if slope > 0 else hint
+            seen = mine if slope <= 0 else torch.ones_like(mine)
+            dev = ((pre.to(z.dtype) - z).abs() / zabs.clamp_min(1e-300))[seen & (zabs > 0)]
+            zero = zabs == 0   # exactly at the kink: every term is 0 (a dropped entry)
+            stats[name + "_zero"] = stats.get(name + "_zero", 0) + int(zero.sum())
+            stats[name + "_near"] = stats.get(name + "_near", 0) + int((near & ~zero).sum())
+            stats[name + "_disagree"] = (stats.get(name + "_disagree", 0)
+                                         + int((mine != (z > 0))[~near].sum()))
+            stats[name + "_dev"] = max(stats.get(name + "_dev", 0.0),
+                                       float(dev.max()) if dev.numel() else 0.0)
+    return pos
+
+
 def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src: torch.Tensor,
                dst: torch.Tensor, num_dst: int, slope: float = 0.2, att_drop=None,
-               dtype=torch.float64, out_drop=None) -> torch.Tensor:
+               dtype=torch.float64, out_drop=None, hints=None, kink_stats=None) -> torch.Tensor:
     """layers.py:98-240, TGAT branch with DGL semantics, eval-mode dropout except for an
     optional attention multiplier ``att_drop`` [E,H] and an optional output multiplier
     ``out_drop`` [N,D] (keep/(1-p) or 0).
 
     h: [N+E, Dn] source-node features (row N+e feeds edge e); f: [E, De]; dt: [E];
     src/dst: int64 [E] source / destination ids.
+
+    ``hints`` (optional dict): an implementation's post-activation values, "score" [E,H]
+    (after LeakyReLU) and "relu" [N,D] (after the output dropout and ReLU). LeakyReLU's and
+    ReLU's derivatives jump at 0, so for a pre-activation value within float32 rounding of 0
+    the branch is not fixed by the inputs at float32 precision: where |z| <= KINK_RTOL times
+    the sum of the absolute values of z's terms, the restatement takes the implementation's
+    branch (the sign of its value); everywhere else the sign of its own z. With a dict
+    ``kink_stats`` it adds, per activation ("score", "relu"), the entries in the band
+    ("_near", not counting those whose terms are all 0, "_zero"), the entries outside it
+    whose hinted branch differs from the sign of z ("_disagree"), and keeps the largest
+    deviation of the implementation's pre-activation value from z, relative to the absolute
+    terms ("_dev"; for ReLU over the entries the implementation kept).
     """
     Dn, De, Dt, D = P["_dims"]
     H = P["_heads"]
@@ -296,7 +335,16 @@ def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src:
     K = torch.nn.functional.linear(kv, cast(P["w_k.weight"]), cast(P["w_k.bias"]))
     V = torch.nn.functional.linear(kv, cast(P["w_v.weight"]), cast(P["w_v.bias"]))
     Q, K, V = Q.view(E, H, -1), K.view(E, H, -1), V.view(E, H, -1)
-    scores = torch.nn.functional.leaky_relu((Q * K).sum(2), slope)
+    z = (Q * K).sum(2)
+    if hints is None or "score" not in hints:
+        scores = torch.nn.functional.leaky_relu(z, slope)
+    else:
+        with torch.no_grad():
+            kabs = torch.nn.functional.linear(kv.abs(), cast(P["w_k.weight"]).abs(),
+                                              cast(P["w_k.bias"]).abs()).view(E, H, -1)
+            zabs = (Q.abs() * kabs).sum(2)
+        pos = _kink("score", z, zabs, hints["score"], slope, kink_stats)
+        scores = torch.where(pos, z, slope * z)
     att = edge_softmax(scores, dst, N)
     if att_drop is not None:
         att = att * cast(att_drop)
@@ -304,9 +352,19 @@ def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src:
     v_src = torch.cat([torch.zeros((N, v.shape[1]), dtype=dtype), v], 0)
     agg = copy_u_sum(v_src, src, dst, N)
     rst = torch.cat([agg, cast(h[:N])], 1) if Dn else agg
-    rst = torch.nn.functional.linear(rst, cast(P["w_out.weight"]), cast(P["w_out.bias"]))
+    rin = rst
+    rst = torch.nn.functional.linear(rin, cast(P["w_out.weight"]), cast(P["w_out.bias"]))
     if out_drop is not None:  # layers.py:235 self.dropout, as multipliers [N, D]
         rst = rst * cast(out_drop)
-    rst = torch.relu(rst)
+    if hints is None or "relu" not in hints:
+        rst = torch.relu(rst)
+    else:
+        with torch.no_grad():
+            uabs = torch.nn.functional.linear(rin.abs(), cast(P["w_out.weight"]).abs(),
+                                              cast(P["w_out.bias"]).abs())
+            if out_drop is not None:
+                uabs = uabs * cast(out_drop)
+        pos = _kink("relu", rst, uabs, hints["relu"], 0.0, kink_stats)
+        rst = torch.where(pos, rst, torch.zeros_like(rst))
     return torch.nn.functional.layer_norm(rst, (D,), cast(P["layer_norm.weight"]),
                                           cast(P["layer_norm.bias"]), P["_eps"])

@@ -299,6 +299,79 @@ def test_tgat_layer_golden_gradients():
         assert math.isclose(got, fd, rel_tol=5e-4, abs_tol=1e-6), (key, got, fd)
 
 
+def _grads_with_hints(c, P, h, src, dst, N, hints, stats=None):
+    for v in list(P.values()) + [h]:
+        if isinstance(v, torch.Tensor) and v.grad is not None:
+            v.grad = None
+    out = ref_cpu.tgat_layer(P, h, torch.tensor(c["f"]), torch.tensor(c["dt"], dtype=torch.float32),
+                             src, dst, N, hints=hints, kink_stats=stats)
+    (out * torch.tensor(c["wsum"], dtype=torch.float64)).sum().backward()
+    return out.detach(), {k: v.grad.clone() for k, v in P.items()
+                          if isinstance(v, torch.Tensor) and v.grad is not None}
+
+
+def test_tgat_layer_branch_hints_outside_the_kink_band_change_nothing():
+    """With branch hints, the restatement takes them only inside the float32 rounding band of
+    a kink: hints of either sign everywhere (every score of this case is far from 0) give the
+    plain layer, and the hinted branches outside the band are counted as disagreeing where
+    they differ from the sign of z (all of them, over the two hints)."""
+    c, P, h, src, dst, N = _layer_case()
+    E, H = dst.numel(), P["_heads"]
+    out0, g0 = _grads_with_hints(c, P, h, src, dst, N, None)
+    dis = 0
+    for sign in (1.0, -1.0):
+        st = {}
+        out1, g1 = _grads_with_hints(c, P, h, src, dst, N, {"score": sign * torch.ones(E, H)}, st)
+        assert torch.equal(out1, out0)
+        for k in g0:
+            assert torch.equal(g1[k], g0[k]), k
+        assert st["score_near"] == 0
+        dis += st["score_disagree"]
+    assert dis == E * H
+
+
+def test_tgat_layer_branch_hint_at_the_score_kink():
+    """Scores exactly at the kink (a zero query: z = 0 for every edge) are all in the band,
+    and the hint picks the derivative: the query-weight gradient flows through LeakyReLU's
+    derivative only, so the positive branch's gradient is exactly 1/slope times the negative
+    branch's."""
+    c, P, h, src, dst, N = _layer_case()
+    E, H = dst.numel(), P["_heads"]
+    with torch.no_grad():
+        P["w_q.weight"].zero_()
+        P["w_q.bias"].zero_()
+    st_pos, st_neg = {}, {}
+    out_p, gp = _grads_with_hints(c, P, h, src, dst, N, {"score": torch.ones(E, H)}, st_pos)
+    out_n, gn = _grads_with_hints(c, P, h, src, dst, N, {"score": -torch.ones(E, H)}, st_neg)
+    for st in (st_pos, st_neg):   # a zero query: every term of every score is 0
+        assert st["score_zero"] == E * H and st["score_disagree"] == 0
+    assert torch.equal(out_p, out_n)   # the value is continuous at the kink
+    assert gp["w_q.weight"].abs().max() > 0
+    assert torch.allclose(gp["w_q.weight"] * 0.2, gn["w_q.weight"], rtol=1e-12, atol=1e-15)
+
+
+def test_tgat_layer_branch_hint_at_the_relu_kink():
+    """A zero output projection puts every ReLU input at the kink: the output is the
+    LayerNorm shift either way; with the ReLU hinted off no gradient reaches w_out, hinted
+    on it does, and the deviation statistic measures the hint against the float64 value."""
+    c, P, h, src, dst, N = _layer_case()
+    D = P["_dims"][3]
+    with torch.no_grad():
+        P["w_out.weight"].zero_()
+        P["w_out.bias"].zero_()
+    st_on, st_off = {}, {}
+    out_on, g_on = _grads_with_hints(c, P, h, src, dst, N, {"relu": 1e-3 * torch.ones(N, D)}, st_on)
+    out_off, g_off = _grads_with_hints(c, P, h, src, dst, N, {"relu": torch.zeros(N, D)}, st_off)
+    for st in (st_on, st_off):
+        assert st["relu_zero"] == N * D and st["relu_near"] == 0 and st["relu_disagree"] == 0
+    beta = P["layer_norm.bias"].detach()
+    assert torch.allclose(out_on, beta.expand(N, D)) and torch.allclose(out_off, beta.expand(N, D))
+    assert torch.count_nonzero(g_off["w_out.weight"]) == 0
+    assert torch.count_nonzero(g_on["w_out.weight"]) > 0
+    # |hint - z| / |terms| with z = 0 and terms = 0 everywhere: excluded, so no deviation
+    assert st_on["relu_dev"] == 0.0
+
+
 def test_tgat_layer_zero_edges():
     """layers.py:101-102: a block without edges returns zeros [N, D] (no w_out, no norm)."""
     c, P, h, src, dst, N = _layer_case()

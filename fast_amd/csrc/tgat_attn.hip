@@ -1839,8 +1839,44 @@ extern "C" size_t fa_tgat_attn_bwd_scratch_bytes(int64_t n_dst, int32_t dt_dim) 
   return static_cast<size_t>(bwd_grid(n_dst)) * 2 * static_cast<size_t>(dt_dim) * sizeof(float);
 }
 
-// The backward: `partial` is the caller's time-gradient scratch.
-static int tgat_bwd_impl(const fa_tgat_graph* g, int32_t heads, const float* qt,
+// ---------------------------------------------------------------------------------
+// The backward without allocation: its time-gradient partials live in `scratch`, a static
+// device array (one copy per GPU, held until the process ends). Every workgroup the backward
+// launches writes its whole partial row before the reduction reads it, so nothing has to be
+// cleared between calls. Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------------
+// Rows for the largest grid (kMaxBlocks workgroups) at the widest time encoding the backward
+// takes (256): 4 MiB.
+constexpr size_t kNoAllocScratchFloats = static_cast<size_t>(kMaxBlocks) * 2 * 256;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of the current device's copy of `scratch`, looked up once per device
+// (the array's name is a host-side stand-in and must never reach a kernel).
+static int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return FA_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return FA_ESCRATCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FA_OK;
+}
+
+// The backward behind both entry points: `partial` is the caller's time-gradient scratch;
+// with `lib_scratch` the library's static array is used instead, looked up after every
+// argument check.
+static int tgat_bwd_impl(bool lib_scratch, const fa_tgat_graph* g, int32_t heads, const float* qt,
                          int64_t qt_rs, int64_t qt_hs, float slope, const float* drop, uint64_t drop_seed,
                          float drop_p, const float* xbar, int64_t xbar_rs, int64_t xbar_hs,
                          const float* tdot, const float* scores, const float* stats,
@@ -1867,6 +1903,7 @@ static int tgat_bwd_impl(const fa_tgat_graph* g, int32_t heads, const float* qt,
   if (d_node && P.node_bf16) return FA_EUNSUPPORTED;  // node gradients for float32 rows only
   if (P.dt_dim > 0 && (!d_time_w || !d_time_b)) return FA_EINVAL;
   int grid = bwd_grid(P.n_dst);   // the most workgroups a launch uses (scratch rows)
+  if (lib_scratch && (st = noalloc_scratch(&partial)) != FA_OK) return st;
   if (P.dt_dim > 0 && (!partial || partial_bytes < fa_tgat_attn_bwd_scratch_bytes(P.n_dst, P.dt_dim)))
     return FA_ESCRATCH;
   P.xbar = const_cast<float*>(xbar); P.xbar_rs = xbar_rs; P.xbar_hs = xbar_hs; P.tdot = tdot;
@@ -1900,12 +1937,29 @@ extern "C" int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const
                                     float* d_node, int64_t ld_dnode,
                                     float* d_time_w, float* d_time_b, void* scratch,
                                     size_t scratch_bytes, hipStream_t stream) {
-  return tgat_bwd_impl(g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, xbar,
+  return tgat_bwd_impl(false, g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, xbar,
                        xbar_rs, xbar_hs, tdot, scores, stats, dxbar, dxbar_rs, dxbar_hs, dqt,
                        dqt_rs, dqt_hs, d_node, ld_dnode, d_time_w, d_time_b, scratch,
                        scratch_bytes, stream);
 }
 
+extern "C" int fa_tgat_attn_bwd_noalloc_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                                            int64_t qt_rs, int64_t qt_hs, float slope,
+                                            const float* drop, uint64_t drop_seed, float drop_p,
+                                            const float* xbar, int64_t xbar_rs, int64_t xbar_hs,
+                                            const float* tdot, const float* scores,
+                                            const float* stats, const float* dxbar,
+                                            int64_t dxbar_rs, int64_t dxbar_hs, float* dqt,
+                                            int64_t dqt_rs, int64_t dqt_hs, float* d_node,
+                                            int64_t ld_dnode, float* d_time_w, float* d_time_b,
+                                            hipStream_t stream) {
+  // a shape whose partials exceed the array is refused (FA_ESCRATCH) by the size check in
+  // tgat_bwd_impl, before any launch
+  return tgat_bwd_impl(true, g, heads, qt, qt_rs, qt_hs, slope, drop, drop_seed, drop_p, xbar,
+                       xbar_rs, xbar_hs, tdot, scores, stats, dxbar, dxbar_rs, dxbar_hs, dqt,
+                       dqt_rs, dqt_hs, d_node, ld_dnode, d_time_w, d_time_b, nullptr,
+                       sizeof(scratch), stream);
+}
 
 __global__ __launch_bounds__(kBlock) void dropout_mask(uint64_t seed, float p, float scale,
                                                       int64_t n, float* out) {

@@ -250,6 +250,23 @@ int fa_tgat_attn_bwd_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
                          float* d_time_w, float* d_time_b, void* scratch,
                          size_t scratch_bytes, hipStream_t stream);
 
+/* The backward above without caller scratch, for callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). No counterpart in the reference.
+ * Same arguments, outputs and limits as fa_tgat_attn_bwd_f32; the time-gradient partials
+ * live in a static device array of 4 MiB per GPU (held until the process ends; enough for
+ * every shape the backward takes: at most 2048 workgroups x 2 x dt_dim <= 256 floats), a
+ * shape needing more returns FA_ESCRATCH. It calls no hipMalloc/hipFree. The current
+ * device must be the one `stream` belongs to. All calls on one GPU share its array: calls
+ * that overlap in time on one GPU (different streams, no ordering) race. */
+int fa_tgat_attn_bwd_noalloc_f32(const fa_tgat_graph* g, int32_t heads, const float* qt,
+                                 int64_t qt_rs, int64_t qt_hs, float slope, const float* drop,
+                                 uint64_t drop_seed, float drop_p, const float* xbar,
+                                 int64_t xbar_rs, int64_t xbar_hs, const float* tdot,
+                                 const float* scores, const float* stats, const float* dxbar,
+                                 int64_t dxbar_rs, int64_t dxbar_hs, float* dqt, int64_t dqt_rs,
+                                 int64_t dqt_hs, float* d_node, int64_t ld_dnode,
+                                 float* d_time_w, float* d_time_b, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------------
  * Per-head projections of the K-space blocks (new ops: the reference applies w_q, w_k,
  * w_v per edge as torch GEMMs, layers.py:162-169). G heads, J = dim_out/heads (<= 64),

@@ -138,6 +138,19 @@ def test_tgat_fwd_rejects_bad_arguments(lib):
     assert _fwd(lib, g, heads=0, qt=64) == FA_EINVAL
 
 
+def test_noalloc_backward_rejects_bad_arguments(lib):
+    """The no-allocation backward checks its arguments like the scratch-taking one, before
+    it looks up its device array or launches anything (no GPU needed here)."""
+    f = lib.fa_tgat_attn_bwd_noalloc_f32
+    none = [None] * 25
+    assert f(None, ctypes.c_int32(2), *none) == FA_EINVAL
+    g = TgatGraph(n_dst=-1)
+    assert f(ctypes.byref(g), ctypes.c_int32(2), *none) == FA_EINVAL
+    g = TgatGraph(n_dst=4, n_edges=8, rowptr=16)
+    # qt given, but neither xbar nor tdot, and no outputs
+    assert f(ctypes.byref(g), ctypes.c_int32(2), ctypes.c_void_p(64), *([None] * 24)) == FA_EINVAL
+
+
 def test_tgat_block_layouts_are_checked(lib):
     """Per-destination blocks: 16-byte alignment, strides in whole float4s, and output rows
     that do not overlap (destination-major or head-major); all rejected before a launch."""

@@ -92,11 +92,14 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
 // Orders this wave's LDS accesses across lanes (a wave-level barrier with workgroup-scope
-// release/acquire fences); enough when only this wave touches the LDS region.
+// release/acquire fences on LDS only); enough when only this wave touches the LDS region.
+// The fences name the local address space: a fence over every address space would also
+// wait for the wave's outstanding global loads (s_waitcnt vmcnt(0)), draining every load a
+// kernel has put in flight ahead of its use.
 __device__ __forceinline__ void lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Adds a row held as float4 chunks (lane l: columns 4l.. of slot k at 4(l + 64k)) into

@@ -33,7 +33,10 @@
 //   (bias column of dqt, x_e = 1: with sum_e a = 1 and T_h = sum_e a*drop*da', the sum of dz
 //    over the destination's edges is -(1 - slope) * sum over the edges with s <= 0 of
 //    a * (drop*da' - T_h); that form is accumulated instead, since the plain sum of dz
-//    cancels to a small number and would keep only the rounding of its terms)
+//    cancels to a small number and would keep only the rounding of its terms. The bias chunk
+//    (1, 0, 0, 0) is the last chunk, so it lies in the last register slot of one lane, which
+//    multiplies that slot by dz * (s > 0 ? 0 : (slope - 1) / slope) = the term above in place
+//    of dz: see bias_dz. A slope of 0 leaves the plain sum of dz)
 //   dx_e    = sum_h a*drop*dxbar[h] + dz*qt[h]        -> node-row gradient, time-encoding grads
 #include <float.h>
 
@@ -179,6 +182,13 @@ __device__ __forceinline__ float lane_flt(float v, int j) {
 // rows) come from global memory; every other chunk is read from the wave's LDS tile row of
 // the edge, laid out as [time chunks (ct) | bias chunk (1,0,0,0) | zero chunk], so a lane
 // picks between two values with one select and no branch.
+// The multiplier of the last register slot: dz, except in the lane holding the bias chunk,
+// where it is the bias column's non-cancelling term dz * (s > 0 ? 0 : (slope - 1) / slope).
+__device__ __forceinline__ float bias_dz(const TgatParams& P, bool bias_lane, float s, float dz) {
+  const float kq = P.slope != 0.f ? (P.slope - 1.f) / P.slope : 1.f;
+  return bias_lane ? dz * (s > 0.f && P.slope != 0.f ? 0.f : kq) : dz;
+}
+
 template <int NS>
 struct LaneCtx {
   uint32_t noff[NS];      // byte offset of a node chunk in the node row (kOob elsewhere)
@@ -188,6 +198,7 @@ struct LaneCtx {
   bool slot_node[NS], slot_time[NS];  // wave-uniform: slot k holds some node / time chunk
   uint32_t time_off;      // LDS tile offset of this lane's time chunk (zero chunk if none)
   float w0, b0, w1, b1;   // time dims j = lane and lane + 64
+  bool bias_lane;         // slot NS-1 holds the bias chunk (chunk cp-1)
 };
 
 template <int NS>
@@ -217,6 +228,7 @@ __device__ __forceinline__ void setup_lane(const TgatParams& P, LaneCtx<NS>& L) 
       L.toff[k] = 4u * static_cast<uint32_t>(P.ct);
     }
   }
+  L.bias_lane = lane + (NS - 1) * kWave == P.cp - 1;
   L.w0 = lane < P.dt_dim ? P.time_w[lane] : 0.f;
   L.b0 = lane < P.dt_dim ? P.time_b[lane] : 0.f;
   L.w1 = lane + kWave < P.dt_dim ? P.time_w[lane + kWave] : 0.f;
@@ -581,16 +593,30 @@ __global__ __launch_bounds__(kBlock, fwd_min_waves(H, NS)) void tgat_fwd(TgatPar
 // [2][tvs].
 // ---------------------------------------------------------------------------------
 
+// Pairs whose row loads are in flight in the pair forward, and the waves per SIMD its
+// register budget is sized for.
+#ifndef FA_PAIR_DEPTH
+#define FA_PAIR_DEPTH 2
+#endif
+#ifndef FA_PAIR_FWD_WAVES
+#define FA_PAIR_FWD_WAVES 4
+#endif
+constexpr int kPairDepth = FA_PAIR_DEPTH;
+
 template <int NS>
 struct PairCtx {
   // byte offset of the lane's chunk in its node / edge row, or float offset of its chunk in
   // the time-tile row (time, bias or zero chunk)
   uint32_t off[NS];
+  // float offset in the time-tile row of the lane's chunk: the chunk itself for time, bias
+  // and padding chunks, the tile's zero chunk for row chunks (every lane reads one)
+  uint32_t toff[NS];
   bool is_node[NS], is_edge[NS], live[NS];   // live: chunk < cp (stored)
   // The lane's time chunk (at most one per lane while ct <= 32): its K-space chunk index,
   // else `zero_chunk`, and its offset in a tile row, else the tile's zero chunk.
   int tci;
   uint32_t ttoff;
+  bool bias_lane;   // slot NS-1 holds the bias chunk (chunk cp-1)
 };
 
 template <int NS>
@@ -598,6 +624,7 @@ __device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L, 
   const int hl = lane_id() & (kHalf - 1);
   L.tci = zero_chunk;
   L.ttoff = 4u * static_cast<uint32_t>(P.ct + 1);
+  L.bias_lane = hl + (NS - 1) * kHalf == P.cp - 1;
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
     const int c = hl + k * kHalf;
@@ -615,6 +642,7 @@ __device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L, 
       off = 4u * static_cast<uint32_t>(P.ct);
     }
     L.off[k] = off;
+    L.toff[k] = (L.is_node[k] || L.is_edge[k]) ? 4u * static_cast<uint32_t>(P.ct + 1) : off;
   }
 }
 
@@ -647,18 +675,59 @@ __device__ __forceinline__ float pick_flt(float v, int j) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(j << 2, __float_as_int(v)));
 }
 
-// One chunk of a table row at `row + off` (float32, or bf16 widened).
-__device__ __forceinline__ float4 pair_chunk(const char* row, uint32_t off, int bf16) {
-  if (bf16) {
-    const uint2 w = *reinterpret_cast<const uint2*>(row + off);
-    return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+// A zero chunk in global memory: the load of every lane without a row chunk to read. It is a
+// plain (non-const) global so that selecting between it and a table row keeps a global
+// pointer: a generic pointer would make the loads flat loads, which also count against the
+// LDS wait counter. Nothing writes it.
+__device__ __align__(16) float g_zero_chunk[4] = {0.f, 0.f, 0.f, 0.f};
+
+// Row chunks of one edge per half-wave, loaded as they are stored: float4 (BF = false) or
+// four bf16 words in x.x, x.y (BF = true, widened by pair_widen where the chunk is used).
+// Every lane issues its load with the whole wave active: a lane whose chunk is no row chunk,
+// or whose row is missing, reads the zero chunk. No branch and no conversion sits between a
+// load and the code that consumes it a step later, so the compiler can wait for exactly that
+// load (a conditional write into a register that still has a load in flight, or a branch
+// around the load, makes it wait for every load the wave has in flight).
+template <int NS, bool BF>
+__device__ __forceinline__ void pair_load(const TgatParams& P, const PairCtx<NS>& L, uint32_t nid,
+                                          uint32_t eid, bool ok, float4 (&x)[NS]) {
+  const bool nok = ok && nid != kNoRow, eok = ok && eid != kNoRow;
+  const char* nrow = P.node_tab + static_cast<uint64_t>(nok ? nid : 0u) * P.node_stride;
+  const char* erow = P.edge_tab + static_cast<uint64_t>(eok ? eid : 0u) * P.edge_stride;
+  const char* zero = reinterpret_cast<const char*>(g_zero_chunk);
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const char* a = (L.is_node[k] && nok) ? nrow + L.off[k] : ((L.is_edge[k] && eok) ? erow + L.off[k] : zero);
+    if constexpr (BF) {
+      const uint2 w = *reinterpret_cast<const uint2*>(a);
+      x[k] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), 0.f, 0.f);
+    } else {
+      x[k] = *reinterpret_cast<const float4*>(a);
+    }
   }
-  return *reinterpret_cast<const float4*>(row + off);
+}
+
+// The K-space chunks of the lane's edge: row chunks from the loads (bf16 words widened),
+// every other chunk (time, bias, padding) from the time-tile row, by selects.
+template <int NS, bool BF>
+__device__ __forceinline__ void pair_widen(const PairCtx<NS>& L, const float* row,
+                                           const float4 (&x)[NS], float4 (&xs)[NS]) {
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(row + L.toff[k]);
+    float4 v = x[k];
+    if constexpr (BF) {
+      const uint32_t w0 = __float_as_uint(v.x), w1 = __float_as_uint(v.y);
+      v = make_float4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1));
+    }
+    const bool r = L.is_node[k] || L.is_edge[k];
+    xs[k] = make_float4(r ? v.x : t.x, r ? v.y : t.y, r ? v.z : t.z, r ? v.w : t.w);
+  }
 }
 
 // Row chunks of this lane's edge of pair p (edge index 2p + half among the staged ones);
 // lanes whose edge is past cnt, or whose row is missing, get zeros.
-template <int NS, int H, bool SC>
+template <int NS, int H, bool SC, bool BF>
 __device__ __forceinline__ void pair_rows(const TgatParams& P, const PairCtx<NS>& L,
                                           const EdgeMeta<H, SC>& M, int p, int cnt,
                                           float4 (&x)[NS]) {
@@ -666,16 +735,7 @@ __device__ __forceinline__ void pair_rows(const TgatParams& P, const PairCtx<NS>
   const int jj = j < cnt ? j : 0;
   const uint32_t nid = static_cast<uint32_t>(pick_int(static_cast<int>(M.nid), jj));
   const uint32_t eid = static_cast<uint32_t>(pick_int(static_cast<int>(M.eid), jj));
-  const bool nok = j < cnt && nid != kNoRow, eok = j < cnt && eid != kNoRow;
-  const char* nrow = P.node_tab + static_cast<uint64_t>(nok ? nid : 0u) * P.node_stride;
-  const char* erow = P.edge_tab + static_cast<uint64_t>(eok ? eid : 0u) * P.edge_stride;
-#pragma unroll
-  for (int k = 0; k < NS; ++k) {
-    float4 v = f4_zero();
-    if (L.is_node[k] && nok) v = pair_chunk(nrow, L.off[k], P.node_bf16);
-    else if (L.is_edge[k] && eok) v = pair_chunk(erow, L.off[k], P.edge_bf16);
-    x[k] = v;
-  }
+  pair_load<NS, BF>(P, L, nid, eid, j < cnt, x);
 }
 
 template <int H, int NS>
@@ -687,11 +747,11 @@ struct PairState {
 
 // Pair p: time encoding of both edges into the halves' tile rows, the other chunks from
 // the tiles, scores, and the two online-softmax updates.
-template <int H, int NS>
+template <int H, int NS, bool BF>
 __device__ __forceinline__ void pair_step(const TgatParams& P, const PairCtx<NS>& L,
                                           const EdgeMeta<H, false>& M, int64_t c0, int p,
                                           int cnt, const float2* twb, float* tile,
-                                          float4 (&x)[NS], PairState<H, NS>& S) {
+                                          const float4 (&xr)[NS], PairState<H, NS>& S) {
   const int lane = lane_id();
   const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
   const int j = 2 * p + half;
@@ -704,9 +764,8 @@ __device__ __forceinline__ void pair_step(const TgatParams& P, const PairCtx<NS>
     for (int d = hl; d < P.dt_dim; d += kHalf) pair_time(t, twb[d], row, d, true);
     lds_sync();
   }
-#pragma unroll
-  for (int k = 0; k < NS; ++k)
-    if (!(L.is_node[k] || L.is_edge[k])) x[k] = *reinterpret_cast<const float4*>(row + L.off[k]);
+  float4 x[NS];
+  pair_widen<NS, BF>(L, row, xr, x);
   float sc[H];
 #pragma unroll
   for (int h = 0; h < H; ++h) {
@@ -745,8 +804,8 @@ __device__ __forceinline__ void pair_step(const TgatParams& P, const PairCtx<NS>
   }
 }
 
-template <int H, int NS>
-__global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
+template <int H, int NS, bool BF>
+__global__ __launch_bounds__(kBlock, FA_PAIR_FWD_WAVES) void tgat_fwd_pair(TgatParams P) {
   extern __shared__ float lds[];
   const int wave = uniform(threadIdx.x / kWave);
   const int lane = lane_id();
@@ -806,8 +865,9 @@ __global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
         qv[h][r] = c < P.cp ? src[c] : f4_zero();
       }
     }
-    float4 xa[NS], xb[NS];
-    pair_rows<NS, H, false>(P, L, M, 0, cnt, xa);
+    float4 xr[kPairDepth][NS];
+#pragma unroll
+    for (int r = 0; r < kPairDepth; ++r) pair_rows<NS, H, false, BF>(P, L, M, r, cnt, xr[r]);
     lds_sync();  // the previous destination's reads of qs are done
 #pragma unroll
     for (int h = 0; h < H; ++h)
@@ -819,19 +879,23 @@ __global__ __launch_bounds__(kBlock, 4) void tgat_fwd_pair(TgatParams P) {
     lds_sync();
     for (;;) {
       const int np = (cnt + 1) >> 1;
-      for (int p = 0; p < np; p += 2) {
-        if (p + 1 < np) pair_rows<NS, H, false>(P, L, M, p + 1, cnt, xb);
-        pair_step<H, NS>(P, L, M, c0, p, cnt, twb, tile, xa, S);
-        if (p + 1 < np) {
-          if (p + 2 < np) pair_rows<NS, H, false>(P, L, M, p + 2, cnt, xa);
-          pair_step<H, NS>(P, L, M, c0, p + 1, cnt, twb, tile, xb, S);
+      // A ring of kPairDepth pairs in flight: each slot is refilled right after its pair is
+      // processed, with the loads of the pair kPairDepth ahead, issued whether or not that
+      // pair exists (past the last pair they read the zero chunk), so every path leaves the
+      // same loads in flight and the compiler waits for exactly the pair it processes.
+      for (int p = 0; p < np; p += kPairDepth) {
+#pragma unroll
+        for (int r = 0; r < kPairDepth; ++r) {
+          if (p + r < np) pair_step<H, NS, BF>(P, L, M, c0, p + r, cnt, twb, tile, xr[r], S);
+          pair_rows<NS, H, false, BF>(P, L, M, p + r + kPairDepth, cnt, xr[r]);
         }
       }
       c0 += kWave;
       if (c0 >= e1) break;
       cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
       stage_meta<H, false>(P, c0, cnt, M);
-      pair_rows<NS, H, false>(P, L, M, 0, cnt, xa);
+#pragma unroll
+      for (int r = 0; r < kPairDepth; ++r) pair_rows<NS, H, false, BF>(P, L, M, r, cnt, xr[r]);
     }
     // merge the halves: M = max(m0, m1), weights exp(m - M) (0 for a half without edges)
     const int other = lane ^ kHalf;
@@ -875,7 +939,7 @@ struct BwdState {
   float4 q[H][NS], g[H][NS], dq[H][NS];
   float4 gw, gb;  // time-grad accumulators of this lane's time chunk (at most one: ct <= 64)
   float mh[H], il[H], T[H];  // row max, 1 / softmax denominator, dxbar . xbar
-  float cb[H];               // bias column of dq~ (the non-cancelling form, see top of file)
+  float cb;       // lane h < H: the bias column of head h's dq~ (the non-cancelling form)
 };
 
 template <int H, int NS>
@@ -889,27 +953,25 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
     lds_sync();
   }
   assemble_x<NS>(P, L, nb, tc, x);
-  float dap[kBatch][H];
-#pragma unroll
-  for (int b = 0; b < kBatch; ++b)
-#pragma unroll
-    for (int h = 0; h < H; ++h) dap[b][h] = wave_sum(row_dot<NS>(S.g[h], x[b]));
   const int lane = lane_id();
 #pragma unroll
   for (int b = 0; b < kBatch; ++b) {
     if (b >= nb) break;
     const int j = jb + b;
     const int64_t e = c0 + j;
-    float ad[H], dz[H];
+    float dap[H], ad[H], dz[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) dap[h] = wave_sum(row_dot<NS>(S.g[h], x[b]));
 #pragma unroll
     for (int h = 0; h < H; ++h) {
       const float s = lane_flt(M.sc[h], j);
       const float dr = lane_flt(M.dr[h], j);
       const float a = exp_fast(s - S.mh[h]) * S.il[h];
       ad[h] = a * dr;
-      const float gz = a * (dr * dap[b][h] - S.T[h]);
+      const float gz = a * (dr * dap[h] - S.T[h]);
       dz[h] = gz * (s > 0.f ? 1.f : P.slope);
-      S.cb[h] += s > 0.f ? 0.f : (P.slope - 1.f) * gz;
+      const float cz = s > 0.f ? 0.f : (P.slope - 1.f) * gz;
+      S.cb = lane == h ? S.cb + cz : S.cb;
 #pragma unroll
       for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[b][k]);
     }
@@ -945,7 +1007,6 @@ __device__ __forceinline__ void bwd_batch(const TgatParams& P, const LaneCtx<NS>
         fma4(S.gw, t, pr);
       }
     }
-    (void)lane;
   }
 }
 
@@ -970,11 +1031,10 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
     const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
     const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
-      S.cb[h] = 0.f;
+    for (int h = 0; h < H; ++h)
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
-    }
+    S.cb = 0.f;
     if (e1 <= e0) {
       store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
       continue;
@@ -1027,12 +1087,12 @@ __global__ __launch_bounds__(kBlock, bwd_min_waves(H, NS)) void tgat_bwd(TgatPar
       stage_meta<H, true>(P, c0, cnt, M);
       issue_rows<NS, H, true>(P, L, M, 0, cnt < kBatch ? cnt : kBatch, xa);
     }
-    // the bias column of dq~ (chunk cp-1, component x) from cb
+    // the bias column (chunk cp-1, component x) from the lanes of cb
 #pragma unroll
-    for (int h = 0; h < H; ++h)
-#pragma unroll
-      for (int k = 0; k < NS; ++k)
-        if (lane_id() + k * kWave == P.cp - 1) S.dq[h][k].x = S.cb[h];
+    for (int h = 0; h < H; ++h) {
+      const float cb = lane_read(S.cb, h);
+      if (L.bias_lane) S.dq[h][NS - 1].x = cb;
+    }
     store_rows<H, NS>(P.dqt, P.dqt_rs, P.dqt_hs, v, P.kp, S.dq);
   }
 
@@ -1077,15 +1137,14 @@ struct PairBwd {
   float4 dq[H][NS];
   float4 gw, gb;              // time-grad accumulators of this lane's time chunk
   float mh[H], il[H], T[H];   // row max, 1 / softmax denominator, dxbar . xbar
-  float cb[H];                // bias column of dq~ (the non-cancelling form, see top of file)
 };
 
-template <int H, int NS>
+template <int H, int NS, bool BF>
 __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx<NS>& L,
                                               const EdgeMeta<H, true>& M, int64_t c0, int p,
                                               int cnt, const float2* twb, float* tc, float* ts,
                                               const float4* qs, const float4* gs,
-                                              float4 (&x)[NS], PairBwd<H, NS>& S) {
+                                              const float4 (&xr)[NS], PairBwd<H, NS>& S) {
   constexpr int QS = NS * kHalf + 1;
   const int lane = lane_id();
   const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
@@ -1108,9 +1167,8 @@ __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx
     }
     lds_sync();
   }
-#pragma unroll
-  for (int k = 0; k < NS; ++k)
-    if (!(L.is_node[k] || L.is_edge[k])) x[k] = *reinterpret_cast<const float4*>(rc + L.off[k]);
+  float4 x[NS];
+  pair_widen<NS, BF>(L, rc, xr, x);
   float dap[H];
 #pragma unroll
   for (int h = 0; h < H; ++h) {
@@ -1129,9 +1187,9 @@ __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx
     ad[h] = a * dr;
     const float gz = a * (dr * dap[h] - S.T[h]);
     dz[h] = gz * (sc > 0.f ? 1.f : P.slope);
-    S.cb[h] += sc > 0.f ? 0.f : (P.slope - 1.f) * gz;
 #pragma unroll
-    for (int k = 0; k < NS; ++k) fma4(S.dq[h][k], dz[h], x[k]);
+    for (int k = 0; k < NS - 1; ++k) fma4(S.dq[h][k], dz[h], x[k]);
+    fma4(S.dq[h][NS - 1], bias_dz(P, L.bias_lane, sc, dz[h]), x[NS - 1]);
   }
   // node-row gradient of this half's edge: dx = sum_h ad_h dxbar_h + dz_h q~_h
   if (P.d_node) {
@@ -1173,7 +1231,7 @@ __device__ __forceinline__ float4 pick_f4(const float4& v, int j) {
 // Waves per SIMD the register budget is sized for (three leave 168 registers for the widest).
 constexpr int pair_bwd_min_waves(int H, int NS) { return H * NS >= 6 ? 3 : 4; }
 
-template <int H, int NS>
+template <int H, int NS, bool BF>
 __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pair(TgatParams P) {
   constexpr int QS = NS * kHalf + 1;
   extern __shared__ float lds[];
@@ -1204,11 +1262,9 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     const int64_t e0 = clamp_edge(P.rowptr[v], P.n_edges);
     const int64_t e1 = clamp_edge(P.rowptr[v + 1], P.n_edges);
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
-      S.cb[h] = 0.f;
+    for (int h = 0; h < H; ++h)
 #pragma unroll
       for (int k = 0; k < NS; ++k) S.dq[h][k] = f4_zero();
-    }
     if (e1 <= e0) {
 #pragma unroll
       for (int h = 0; h < H; ++h) {
@@ -1224,7 +1280,7 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     EdgeMeta<H, true> M;
     stage_meta<H, true>(P, c0, cnt, M);
     float4 xa[NS], xb[NS];
-    pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
+    pair_rows<NS, H, true, BF>(P, L, M, 0, cnt, xa);
     // the destination's rows: q~ (the chunks the backward reads, q_chunk_used) and dxbar
     // into LDS, T = dxbar . xbar per head
     lds_sync();  // the previous destination's reads of qs / gs are done
@@ -1268,31 +1324,28 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
     lds_sync();
     for (;;) {
       const int np = (cnt + 1) >> 1;
+      // next pair's loads issued unconditionally (see the forward)
       for (int p = 0; p < np; p += 2) {
-        if (p + 1 < np) pair_rows<NS, H, true>(P, L, M, p + 1, cnt, xb);
-        pair_bwd_step<H, NS>(P, L, M, c0, p, cnt, twb, tc, ts, qs, gs, xa, S);
-        if (p + 1 < np) {
-          if (p + 2 < np) pair_rows<NS, H, true>(P, L, M, p + 2, cnt, xa);
-          pair_bwd_step<H, NS>(P, L, M, c0, p + 1, cnt, twb, tc, ts, qs, gs, xb, S);
-        }
+        pair_rows<NS, H, true, BF>(P, L, M, p + 1, cnt, xb);
+        pair_bwd_step<H, NS, BF>(P, L, M, c0, p, cnt, twb, tc, ts, qs, gs, xa, S);
+        pair_rows<NS, H, true, BF>(P, L, M, p + 2, cnt, xa);
+        if (p + 1 < np) pair_bwd_step<H, NS, BF>(P, L, M, c0, p + 1, cnt, twb, tc, ts, qs, gs, xb, S);
       }
       c0 += kWave;
       if (c0 >= e1) break;
       cnt = static_cast<int>(e1 - c0 < kWave ? e1 - c0 : kWave);
       stage_meta<H, true>(P, c0, cnt, M);
-      pair_rows<NS, H, true>(P, L, M, 0, cnt, xa);
+      pair_rows<NS, H, true, BF>(P, L, M, 0, cnt, xa);
     }
-    // dq~ = the two halves' sums (the bias column from the halves' cb, merged by every lane)
+    // dq~ = the two halves' sums
 #pragma unroll
     for (int h = 0; h < H; ++h) {
-      const float cbs = S.cb[h] + pick_flt(S.cb[h], other);
       float* dst = P.dqt + v * P.dqt_rs + h * P.dqt_hs;
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
         const float4 o = pick_f4(S.dq[h][k], other);
         const float4 a = S.dq[h][k];
-        float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
-        if (hl + k * kHalf == P.cp - 1) sum.x = cbs;
+        const float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
         if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = sum;
       }
     }
@@ -1676,10 +1729,15 @@ int persistent_grid(int64_t n_dst, const void* kernel, size_t lds) {
   return want < res ? want : res;
 }
 
+// The pair kernels read both tables with one element type (a template parameter): a table
+// without columns takes the other's.
+bool pair_one_type(const TgatParams& P) { return P.dn == 0 || P.de == 0 || P.node_bf16 == P.edge_bf16; }
+bool pair_bf16(const TgatParams& P) { return P.dn > 0 ? P.node_bf16 : P.edge_bf16; }
+
 // The two-edge forward: whole-chunk rows (mode 0), up to 2 heads, up to 128 chunks for one
 // head and 96 for two (beyond that its registers spill).
 bool pair_fwd_fits(const TgatParams& P, int heads) {
-  return heads <= 2 && P.node_tail == 0 && P.edge_tail == 0 &&
+  return heads <= 2 && P.node_tail == 0 && P.edge_tail == 0 && pair_one_type(P) &&
          P.cp <= (heads == 1 ? 4 : 3) * kHalf;
 }
 
@@ -1722,11 +1780,12 @@ int launch_fwd_h(const TgatParams& P, hipStream_t stream) {
   }
   if constexpr (H <= 2) if (pair_fwd_fits(P, H)) {
     lds = pair_lds_bytes(P, H);
+    const bool bf = pair_bf16(P);
     switch (ceil_div(P.cp, kHalf)) {
-      case 1: k = tgat_fwd_pair<H, 1>; break;
-      case 2: k = tgat_fwd_pair<H, 2>; break;
-      case 3: k = tgat_fwd_pair<H, 3>; break;
-      default: k = tgat_fwd_pair<H, (H == 1 ? 4 : 3)>; break;
+      case 1: k = bf ? tgat_fwd_pair<H, 1, true> : tgat_fwd_pair<H, 1, false>; break;
+      case 2: k = bf ? tgat_fwd_pair<H, 2, true> : tgat_fwd_pair<H, 2, false>; break;
+      case 3: k = bf ? tgat_fwd_pair<H, 3, true> : tgat_fwd_pair<H, 3, false>; break;
+      default: k = bf ? tgat_fwd_pair<H, (H == 1 ? 4 : 3), true> : tgat_fwd_pair<H, (H == 1 ? 4 : 3), false>; break;
     }
     const dim3 grid(static_cast<unsigned>(persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds)));
     hipLaunchKernelGGL(k, grid, dim3(kBlock), lds, stream, P);
@@ -1779,9 +1838,9 @@ int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
     const int pns = static_cast<int>(ceil_div(P.cp, kHalf));
     lds = pair_bwd_lds_bytes(P, H);
     switch (pns) {
-      case 1: k = tgat_bwd_pair<H, 1>; break;
-      case 2: k = tgat_bwd_pair<H, 2>; break;
-      default: k = tgat_bwd_pair<H, 3>; break;
+      case 1: k = pair_bf16(P) ? tgat_bwd_pair<H, 1, true> : tgat_bwd_pair<H, 1, false>; break;
+      case 2: k = pair_bf16(P) ? tgat_bwd_pair<H, 2, true> : tgat_bwd_pair<H, 2, false>; break;
+      default: k = pair_bf16(P) ? tgat_bwd_pair<H, 3, true> : tgat_bwd_pair<H, 3, false>; break;
     }
   }
   grid = persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds);

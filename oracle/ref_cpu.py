@@ -211,6 +211,51 @@ C = _C()
 
 
 # ---------------------------------------------------------------------------------------
+# sampler output -> message-flow-graph blocks (utils.py:67-87) and the sampler's cntE
+# ---------------------------------------------------------------------------------------
+def sampler_cnte(row) -> np.ndarray:
+    """cntE of a sampler result (sampler_core.cpp:384-409, with the leading 0 pushed at
+    :247): 0, then the running sum of the lengths of the runs of equal consecutive `row`
+    values (the edges grouped by destination). int32."""
+    row = np.asarray(row)
+    if row.size == 0:
+        return np.zeros(1, np.int32)
+    ends = np.flatnonzero(np.diff(row) != 0) + 1
+    return np.concatenate([[0], ends, [row.size]]).astype(np.int32)
+
+
+def full_rowptr(row, n_dst: int) -> np.ndarray:
+    """The CSR over every destination 0..n_dst of edges sorted by destination `row`
+    (zero-degree destinations included): rowptr[v] = number of edges with row < v."""
+    return np.searchsorted(np.asarray(row), np.arange(n_dst + 1), side="left").astype(np.int32)
+
+
+def to_dgl_blocks(ret, hist: int, reverse: bool = False) -> list:
+    """utils.py:67-87 without DGL: per sampler result a dict with the edges of
+    dgl.create_block((src, dst)) - (col, row) with num_src = dim_in and num_dst = dim_out,
+    or (row, col) with the counts swapped when `reverse` - the node ids and timestamps on the
+    source side (destination side with `reverse`), dt = dts[dim_out:] (the edges' dts follow
+    the dim_out destination entries), the edge ids; grouped `hist` at a time, the incomplete
+    last group dropped, the groups reversed."""
+    blocks = []
+    for r in ret:
+        row, col = np.asarray(r.row()).astype(np.int64), np.asarray(r.col()).astype(np.int64)
+        dim_in, dim_out = int(r.dim_in()), int(r.dim_out())
+        if not reverse:
+            b = {"src": col, "dst": row, "num_src": dim_in, "num_dst": dim_out, "node_side": "src"}
+        else:
+            b = {"src": row, "dst": col, "num_src": dim_out, "num_dst": dim_in, "node_side": "dst"}
+        b["ID"] = np.asarray(r.nodes())
+        b["ts"] = np.asarray(r.ts())
+        b["dt"] = np.asarray(r.dts())[dim_out:]
+        b["eID"] = np.asarray(r.eid())
+        blocks.append(b)
+    groups = [blocks[g * hist:(g + 1) * hist] for g in range(len(blocks) // hist)]
+    groups.reverse()
+    return groups
+
+
+# ---------------------------------------------------------------------------------------
 # torch restatement of the TGAT layer
 # ---------------------------------------------------------------------------------------
 def time_encoding_weight(dim: int) -> torch.Tensor:

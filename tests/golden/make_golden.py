@@ -296,6 +296,63 @@ def time_weight() -> dict:
     return {"w_float32": [float(v) for v in w], "w_exact": exact}
 
 
+def mfg_case() -> dict:
+    """Sampler results (sampler_core.cpp layout: edges grouped by ascending destination
+    `row`, edge e from source dim_out + e; some destinations without edges) and the blocks
+    utils.py:67-87 to_dgl_blocks builds from them (dgl.create_block((src, dst)) with the
+    roles of row / col set by `reverse`), grouped `hist` at a time with the incomplete last
+    group dropped (zip(*[iter(x)] * hist)) and the groups reversed; plus the sampler's cntE
+    (sampler_core.cpp:384-409: 0, then the running sum of the run lengths of `row`) and the
+    full CSR over every destination. A generator of its own, so the other fixtures keep
+    their values."""
+    rng = random.Random(7001)
+    results = []
+    for dim_out in (4, 1, 6, 3, 5):
+        degs = [rng.choice([0, 1, 2, 3, 5]) for _ in range(dim_out)]
+        row = [v for v in range(dim_out) for _ in range(degs[v])]
+        E = len(row)
+        dim_in = dim_out + E
+        results.append({
+            "row": row, "col": [dim_out + e for e in range(E)],
+            "nodes": [rng.randrange(10 ** 6) for _ in range(dim_in)],
+            "dts": [f32(rng.random() * 1e4) for _ in range(dim_in)],
+            "ts": [f32(rng.random() * 1e6) for _ in range(dim_in)],
+            "eid": [rng.randrange(10 ** 7) for _ in range(E)],
+            "dim_in": dim_in, "dim_out": dim_out})
+
+    def blocks(reverse):
+        out = []
+        for r in results:
+            if not reverse:
+                b = {"src": r["col"], "dst": r["row"], "num_src": r["dim_in"], "num_dst": r["dim_out"],
+                     "node_side": "src", "dt": r["dts"][r["dim_out"]:]}
+            else:
+                b = {"src": r["row"], "dst": r["col"], "num_src": r["dim_out"], "num_dst": r["dim_in"],
+                     "node_side": "dst", "dt": r["dts"][r["dim_out"]:]}
+            b.update(ID=r["nodes"], ts=r["ts"], eID=r["eid"])
+            out.append(b)
+        return out
+
+    expect = {}
+    for hist in (1, 2):
+        for reverse in (False, True):
+            bl = blocks(reverse)
+            groups = [bl[g * hist:(g + 1) * hist] for g in range(len(bl) // hist)]
+            groups.reverse()
+            expect[f"hist{hist}_rev{int(reverse)}"] = groups
+    cnte, rowptr = [], []
+    for r in results:
+        c, run = [0], 0
+        for i, v in enumerate(r["row"]):
+            run += 1
+            if i + 1 == len(r["row"]) or r["row"][i + 1] != v:
+                c.append(c[-1] + run)
+                run = 0
+        cnte.append(c)
+        rowptr.append([sum(1 for v in r["row"] if v < d) for d in range(r["dim_out"] + 1)])
+    return {"results": results, "blocks": expect, "cnte": cnte, "rowptr": rowptr}
+
+
 def main():
     rng = random.Random(20240611)
     fixtures = {
@@ -305,6 +362,7 @@ def main():
         "fused_attn.json": fused_attn_case(rng),
         "tgat_layer_tiny.json": tgat_case(rng),
         "time_weight.json": time_weight(),
+        "mfg.json": mfg_case(),
     }
     for name, data in fixtures.items():
         with open(os.path.join(HERE, name), "w") as fh:

@@ -64,6 +64,46 @@ def test_cnte_golden():
         np.testing.assert_array_equal(C.exclusive_sum(counts), c["out"])
 
 
+class _GoldenSample:
+    """A sampler result with the FAST sampler's accessors, from a golden fixture entry."""
+
+    def __init__(self, d):
+        self.d = d
+
+    def row(self): return np.asarray(self.d["row"], np.int32)
+    def col(self): return np.asarray(self.d["col"], np.int32)
+    def nodes(self): return np.asarray(self.d["nodes"], np.int64)
+    def dts(self): return np.asarray(self.d["dts"], np.float32)
+    def ts(self): return np.asarray(self.d["ts"], np.float32)
+    def eid(self): return np.asarray(self.d["eid"], np.int64)
+    def dim_in(self): return self.d["dim_in"]
+    def dim_out(self): return self.d["dim_out"]
+
+
+def test_to_dgl_blocks_golden():
+    """oracle.to_dgl_blocks (utils.py:67-87) against the blocks of the golden fixture, for
+    hist 1 and 2 (an odd result count: the incomplete last group is dropped) and both
+    directions; the sampler's cntE and the full CSR likewise."""
+    c = _load("mfg.json")
+    ret = [_GoldenSample(d) for d in c["results"]]
+    for key, want in c["blocks"].items():
+        hist, rev = int(key[4]), key.endswith("rev1")
+        got = ref_cpu.to_dgl_blocks(ret, hist, reverse=rev)
+        assert [len(g) for g in got] == [len(g) for g in want], key
+        for gg, gw in zip(got, want):
+            for b, w in zip(gg, gw):
+                for k in ("num_src", "num_dst", "node_side"):
+                    assert b[k] == w[k], (key, k)
+                for k in ("src", "dst", "ID", "eID"):
+                    np.testing.assert_array_equal(b[k], np.asarray(w[k]), err_msg=f"{key} {k}")
+                for k in ("ts", "dt"):
+                    np.testing.assert_array_equal(b[k], np.asarray(w[k], np.float32), err_msg=f"{key} {k}")
+    for r, cn, rp in zip(ret, c["cnte"], c["rowptr"]):
+        np.testing.assert_array_equal(ref_cpu.sampler_cnte(r.row()), cn)
+        np.testing.assert_array_equal(ref_cpu.full_rowptr(r.row(), r.dim_out()), rp)
+        np.testing.assert_array_equal(C.rowptr(r.row(), r.dim_out()), rp)
+
+
 def test_bookkeeping_closed_forms():
     rng = np.random.default_rng(3)
     x = rng.integers(0, 50, 10_000)

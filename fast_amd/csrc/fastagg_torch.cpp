@@ -1089,6 +1089,13 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("x"), py::arg("w"), py::arg("bias") = py::none());
   m.def("head_reduce", &head_reduce, "per-head transpose product z[:, g-block] = y[g] @ w[g]^T",
         py::arg("y"), py::arg("w"));
+  m.def("head_reduce_supported",
+        [](int64_t j, int64_t c, int64_t ldy, bool rows16) {
+          return fa_head_reduce_supported(static_cast<int32_t>(j), static_cast<int32_t>(c), ldy,
+                                          rows16 ? 1 : 0);
+        },
+        "path head_reduce takes for (j, c, ldy): 2 split-bf16, 1 float32, 0 unsupported",
+        py::arg("j"), py::arg("c"), py::arg("ldy"), py::arg("rows16"));
   m.def("head_wgrad", &head_wgrad, "per-head weight gradient x[:, g-block]^T @ y[g]",
         py::arg("x"), py::arg("y"), py::arg("groups"), py::arg("ones") = false);
   m.def("tgat_epilogue_fwd", &tgat_epilogue_fwd, "LayerNorm(ReLU(dropout(r1 + r2 + bias)))",

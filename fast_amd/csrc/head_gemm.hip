@@ -1184,6 +1184,19 @@ extern "C" int fa_head_proj_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
   return launch_status();
 }
 
+// Which path a head_reduce call would take (0: none, FA_EUNSUPPORTED; 1: the float32 kernel;
+// 2: the split-bf16 kernel), from the same tests fa_head_reduce_f32 makes.
+static int head_reduce_path(int32_t j, int32_t c, int64_t ldy, bool vec) {
+  if (j <= 0 || c <= 0 || j > 64 || ldy < c || !tile_fits(ldy)) return 0;
+  if (kReduceBf && vec && reduce_bf_lds_bytes(j, c) <= kMaxReduceLds) return 2;
+  const int c16 = static_cast<int>(round_up(ceil_div(c, 16), kRedDepth));
+  return reduce_lds_bytes(j, c16) <= kMaxReduceLds ? 1 : 0;
+}
+
+extern "C" int fa_head_reduce_supported(int32_t j, int32_t c, int64_t ldy, int32_t rows16) {
+  return head_reduce_path(j, c, ldy, rows16 != 0);
+}
+
 extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t groups,
                                   const float* y, int64_t yg, int64_t ldy, const float* w,
                                   int64_t wg, int64_t ldw, float* z, int64_t ldz, int64_t zg,

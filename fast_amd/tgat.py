@@ -279,6 +279,22 @@ class KernelTimer:
 
 
 timer: Optional[KernelTimer] = None  # set by a benchmark to time the fused kernels
+
+
+def _timed(name: str, nbytes: int, fn, *args):
+    """fn(*args), bracketed by timer events with its algorithmic bytes when a timer is set."""
+    t0 = timer.begin() if timer is not None else None
+    out = fn(*args)
+    if t0 is not None:
+        timer.end(name, t0, nbytes)
+    return out
+
+
+def _head_bytes(n: int, g: int, j: int, c: int, x_groups: bool = True) -> int:
+    """Algorithmic bytes of a per-head product over an [n, g*j] side and a [g, n, c] block:
+    both read or written once (the [g, n, c] side once per group unless it is one array
+    shared by every group, x_groups False), plus the [g, j, c] weights."""
+    return 4 * (n * g * j + (g if x_groups else 1) * n * c + g * j * c)
 # When set to a list, each layer's forward appends its post-activation values, whose signs
 # are the branches its backward takes: ("score", [E, H] post-LeakyReLU scores) from the fused
 # kernel, then ("relu", [N, D] post-dropout, post-ReLU values) from the epilogue. A parity
@@ -395,20 +411,45 @@ HEAD_KERNEL_MAX_J = 64
 
 def _proj(x, w, bias):
     """[N, G*J] x [G, J, C] (+ [G, C]) -> [G, N, C]."""
-    G, J, _ = w.shape
+    G, J, C = w.shape
     if J <= HEAD_KERNEL_MAX_J:
-        return fastAgg.head_proj(x, w, bias)
+        return _timed("head_proj", _head_bytes(x.shape[0], G, J, C), fastAgg.head_proj, x, w, bias)
     y = torch.matmul(x.view(-1, G, J).transpose(0, 1), w)
     return y if bias is None else y + bias[:, None, :]
 
 
+def _rows16(t) -> bool:
+    """Rows of whole 16-byte chunks: 16-byte aligned, unit inner stride, other strides and
+    the width multiples of 4 (the split-bf16 kernels' condition)."""
+    return (t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and t.shape[-1] % 4 == 0
+            and all(st % 4 == 0 for st in t.stride()[:-1]))
+
+
+def _reduce_path(y, J: int) -> int:
+    """The head_reduce kernel path for y [G, N, C] and heads of width J (0: none)."""
+    if J > HEAD_KERNEL_MAX_J or y.stride(-1) != 1:
+        return 0
+    return int(fastAgg.head_reduce_supported(J, y.shape[2], y.stride(1), _rows16(y)))
+
+
 def _reduce(y, w):
-    """[G, N, C] x [G, J, C]^T -> [N, G*J]."""
-    G, J, _ = w.shape
-    if J <= HEAD_KERNEL_MAX_J:
-        return fastAgg.head_reduce(y, w)
+    """[G, N, C] x [G, J, C]^T -> [N, G*J]; batched torch GEMMs where the head kernel does
+    not take the shape (heads wider than 64, or W[g] too large for LDS)."""
+    G, J, C = w.shape
+    if _reduce_path(y, J):
+        return _timed("head_reduce", _head_bytes(y.shape[1], G, J, C, y.stride(0) != 0),
+                      fastAgg.head_reduce, y, w)
     z = torch.matmul(y, w.transpose(1, 2).contiguous())
     return z.transpose(0, 1).reshape(y.shape[1], G * J)
+
+
+def _wgrad(x, y, groups: int, ones: bool):
+    """fastAgg.head_wgrad (dw[g] = x[:, g-block]^T y[g], plus the column sums of y[g] with
+    ``ones``), timed as head_wgrad: x [N, G*J] and y [G, N, C] read once, dw written."""
+    G, n, C = y.shape
+    J = x.shape[1] // groups
+    nb = 4 * (n * groups * J + (G if y.stride(0) != 0 else 1) * n * C + groups * (J + int(ones)) * C)
+    return _timed("head_wgrad", nb, fastAgg.head_wgrad, x, y, groups, ones)
 
 
 def _rows_mm(x, a):
@@ -417,12 +458,19 @@ def _rows_mm(x, a):
     stride; M split into G groups of at most HEAD_KERNEL_MAX_J rows of a), used where its
     split-bf16 form applies (rows of x in whole 16-byte chunks); torch's GEMM otherwise."""
     m, k = a.shape
-    g = next((d for d in range(1, m + 1) if m % d == 0 and m // d <= HEAD_KERNEL_MAX_J), None)
-    if (g is None or x.dim() != 2 or x.stride(1) != 1 or k % 4 or x.stride(0) % 4
-            or x.data_ptr() % 16):
+    if x.dim() != 2 or x.stride(1) != 1 or k % 4 or x.stride(0) % 4 or x.data_ptr() % 16:
+        return x @ a.t()
+    # the fewest groups (widest heads, at most 64 rows of a each) that the split-bf16 kernel
+    # takes, else that the float32 kernel takes, else torch's GEMM
+    xs = x.unsqueeze(0).expand(1, x.shape[0], k)
+    cands = [d for d in range(1, m + 1) if m % d == 0 and m // d <= HEAD_KERNEL_MAX_J]
+    g = next((d for d in cands if _reduce_path(xs, m // d) == 2), None)
+    if g is None:
+        g = next((d for d in cands if _reduce_path(xs, m // d) == 1), None)
+    if g is None:
         return x @ a.t()
     a = a.contiguous()
-    return fastAgg.head_reduce(x.unsqueeze(0).expand(g, x.shape[0], k), a.view(g, m // g, k))
+    return _reduce(x.unsqueeze(0).expand(g, x.shape[0], k), a.view(g, m // g, k))
 
 
 class _SplitRows(torch.autograd.Function):
@@ -469,7 +517,7 @@ class HeadProj(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = _reduce(dy, w)
         if ctx.needs_input_grad[1] or (ctx.has_bias and ctx.needs_input_grad[2]):
-            gw = fastAgg.head_wgrad(x, dy, w.shape[0], ctx.has_bias)
+            gw = _wgrad(x, dy, w.shape[0], ctx.has_bias)
             dw = gw[:, :w.shape[1]]
             db = gw[:, w.shape[1]] if ctx.has_bias else None
         return dx, dw, db
@@ -492,7 +540,7 @@ class HeadReduce(torch.autograd.Function):
         y, w, z = ctx.saved_tensors
         dz = dz.contiguous()
         dy = _proj(dz, w, None) if ctx.needs_input_grad[0] else None
-        dw = fastAgg.head_wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
+        dw = _wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
         if ctx.link is not None and dy is not None:
             ctx.link.tdot = fastAgg.row_group_dots(dz, z, w.shape[0])
         return dy, dw, None
@@ -540,7 +588,7 @@ class RowsMM(torch.autograd.Function):
         dx = _rows_mm(dy, W.t()) if ctx.needs_input_grad[0] else None
         dW = None
         if ctx.needs_input_grad[1]:   # dy^T x, written [M, K] (no transposed view)
-            dW = fastAgg.head_wgrad(dy, x.unsqueeze(0), 1, False)[0]
+            dW = _wgrad(dy, x.unsqueeze(0), 1, False)[0]
         return dx, dW
 
 
@@ -573,9 +621,9 @@ class DstProj(torch.autograd.Function):
                 dh = dr @ Wr
         hc = h.contiguous() if (ctx.needs_input_grad[1] or ctx.needs_input_grad[2]) else h
         if ctx.needs_input_grad[1] and dq is not None:
-            dWq = fastAgg.head_wgrad(dq, hc.unsqueeze(0), 1, False)[0]
+            dWq = _wgrad(dq, hc.unsqueeze(0), 1, False)[0]
         if ctx.needs_input_grad[2] and dr is not None:
-            dWr = fastAgg.head_wgrad(dr, hc.unsqueeze(0), 1, False)[0]
+            dWr = _wgrad(dr, hc.unsqueeze(0), 1, False)[0]
         return dh, dWq, dWr
 
 

@@ -270,7 +270,10 @@ int fa_tgat_attn_bwd_noalloc_f32(const fa_tgat_graph* g, int32_t heads, const fl
 /* ---------------------------------------------------------------------------------
  * Per-head projections of the K-space blocks (new ops: the reference applies w_q, w_k,
  * w_v per edge as torch GEMMs, layers.py:162-169). G heads, J = dim_out/heads (<= 64),
- * C = Kp columns; W[g][j][c] = w[g*wg + j*ldw + c]. All float32 on the matrix cores.
+ * C = Kp columns; W[g][j][c] = w[g*wg + j*ldw + c]. Float32 in and out, on the matrix
+ * cores: where the rows allow, every operand is split into three bf16 parts (hi + mid + lo =
+ * the float exactly) and the six products above 2^-16 of the whole are summed in float32
+ * (the bf16 MFMA); otherwise the float32 MFMA. Either keeps float32 accuracy.
  * ------------------------------------------------------------------------------- */
 
 /* Y[g][n][c] = sum_j X[n][j] W[g][j][c] (+ bias[g*bg + c] when bias != NULL), with
@@ -281,10 +284,19 @@ int fa_head_proj_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const floa
                      hipStream_t stream);
 
 /* Z[n][g][j] = z[n*ldz + g*zg + j] = sum_c Y[g][n][c] W[g][j][c]
- * (the transpose product of fa_head_proj_f32), Y[g][n][c] = y[g*yg + n*ldy + c]. */
+ * (the transpose product of fa_head_proj_f32), Y[g][n][c] = y[g*yg + n*ldy + c].
+ * W[g] is held in LDS (160 KiB): as three bf16 parts, (j+1) x (c rounded up to 64, + 8)
+ * each, when Y's rows are whole 16-byte chunks (y 16-byte aligned, ldy, yg and c multiples
+ * of 4); else as float32 chunks, (j+1) x (c rounded up to 64) floats. A shape that fits
+ * neither returns FA_EUNSUPPORTED (e.g. j = 64 with c > 512 on unaligned rows, or
+ * c > 680 on any rows); fa_head_reduce_supported tells beforehand. */
 int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t groups, const float* y,
                        int64_t yg, int64_t ldy, const float* w, int64_t wg, int64_t ldw,
                        float* z, int64_t ldz, int64_t zg, hipStream_t stream);
+/* Whether fa_head_reduce_f32 takes (j, c, ldy) with rows of whole 16-byte chunks (rows16 != 0)
+ * or not: 2 on the split-bf16 kernel, 1 on the float32 kernel, 0 unsupported
+ * (FA_EUNSUPPORTED). No device access. */
+int fa_head_reduce_supported(int32_t j, int32_t c, int64_t ldy, int32_t rows16);
 
 /* dw[g][j][c] = sum_n X[n][j] Y[g][n][c] (X, Y as in fa_head_proj_f32 / fa_head_reduce_f32),
  * [groups][j + ones][c] contiguous; with ones != 0 row j holds sum_n Y[g][n][c] (the

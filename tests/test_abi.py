@@ -194,6 +194,19 @@ def test_head_gemm_rejects_bad_arguments(lib):
              ctypes.c_void_p(512), ctypes.c_size_t(16), None) == FA_ESCRATCH
 
 
+def test_head_reduce_supported(lib):
+    """The query names the head_reduce path from the same LDS rules the entry point applies:
+    split-bf16 for 16-byte rows when W's three bf16 parts fit, float32 when its float32 copy
+    fits, nothing beyond (or past 64 rows per head)."""
+    q = lambda j, c, ld, r16: lib.fa_head_reduce_supported(ctypes.c_int32(j), ctypes.c_int32(c),
+                                                           ctypes.c_int64(ld), ctypes.c_int32(r16))
+    assert q(50, 376, 384, 1) == 2 and q(50, 376, 384, 0) == 1    # C3: K-space reduce
+    assert q(32, 708, 736, 1) == 2                                # C5: 8 heads of 32
+    assert q(64, 708, 736, 1) == 0 and q(64, 708, 736, 0) == 0    # 4 heads of 64 over Kp 708
+    assert q(64, 416, 416, 1) == 1                                # bf16 parts too large
+    assert q(65, 100, 100, 1) == 0 and q(0, 100, 100, 1) == 0 and q(8, 100, 50, 1) == 0
+
+
 def test_softmax_rejects_bad_arguments(lib):
     f = lib.fa_edge_softmax_fwd_f32
     # (indptr, n_seg, n_edges, x, ldx, heads, y, ldy, mode, stream)

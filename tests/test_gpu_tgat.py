@@ -64,7 +64,10 @@ def _check_layer(dev, dn, de, dt, H, D, degrees, seed=0, time_bias=False, p_drop
 
 @pytest.mark.parametrize("dims", [(100, 172, 100, 2, 100), (7, 5, 3, 1, 4), (8, 0, 4, 2, 8),
                                   (0, 12, 9, 4, 16), (13, 6, 0, 8, 64), (100, 172, 100, 8, 256),
-                                  (200, 172, 100, 1, 64)])
+                                  (200, 172, 100, 1, 64),
+                                  # heads of 64 over Kp = 708: W[g] fits neither head_reduce form
+                                  # in LDS, so those products fall back to torch GEMMs
+                                  (413, 186, 100, 4, 256)])
 def test_layer_small(dev, dims):
     dn, de, dt, H, D = dims
     degrees = [0, 1, 2, 3, 10, 10, 17, 0, 20, 5, 64, 70, 1]
@@ -477,23 +480,30 @@ def test_layer_params_match_torch(dev, dims):
         assert_rel(g.grad, r.grad, FP32_TOL, f"layer params grad {name}")
 
 
-def test_to_blocks_on_device_match_host(dev):
-    """The pinned, packed transfer gives the same blocks on the GPU as on the host, for more
-    results than staging buffers (buffer reuse after its copy finished), and a layer runs
-    on them with the offsets derived on the device."""
+def test_to_blocks_on_device_match_restatement(dev):
+    """The pinned, packed transfer to the GPU gives the blocks of the oracle's restatement of
+    utils.py:67-87 (sampler results with ragged degrees and zero-degree destinations, more
+    results than staging buffers, so buffers are reused after their copy finished), and the
+    destination offsets derived on the device equal the restatement's full CSR, whose
+    non-empty part is the sampler's cntE (sampler_core.cpp:384-409)."""
+    from fast_amd import fastAgg
     from fast_amd.mfg import PinnedStager, to_blocks
-    from tests.test_host import _FakeSample
+    from oracle.ref_cpu import full_rowptr, sampler_cnte, to_dgl_blocks
+    from tests.test_host import _assert_block_matches
+    from tests.test_oracle import _GoldenSample, _load
 
-    ret = [_FakeSample(40 + i, 3 + i, i) for i in range(5)]
-    cpu = to_blocks(ret, device="cpu")
-    gpu = to_blocks(ret, device=dev, stager=PinnedStager(buffers=2))
-    for gc, gg in zip(cpu, gpu):
-        for bc, bg in zip(gc, gg):
-            for a, b in zip(bc.edges(), bg.edges()):
-                assert torch.equal(a, b.cpu())
-            for k in ("ID", "ts"):
-                assert torch.equal(bc.srcdata[k], bg.srcdata[k].cpu())
-            for k in ("dt", "ID"):
-                assert torch.equal(bc.edata[k], bg.edata[k].cpu())
-            rp = bg.rowptr().cpu()
-            assert int(rp[-1]) == bc.num_edges() and bool((rp[1:] >= rp[:-1]).all())
+    ret = [_GoldenSample(d) for d in _load("mfg.json")["results"]]
+    got = to_blocks(ret, hist=1, device=dev, stager=PinnedStager(buffers=2))
+    want = to_dgl_blocks(ret, 1)
+    assert len(got) == len(want)
+    for (b,), (w,), r in zip(got, want, reversed(ret)):
+        assert b.device.type == "cuda"
+        _assert_block_matches(b, w)
+        rp = b.rowptr().cpu().numpy()
+        np.testing.assert_array_equal(rp, full_rowptr(r.row(), r.dim_out()))
+        # the non-empty destinations' offsets are the sampler's cntE (unique2indptr)
+        np.testing.assert_array_equal(np.unique(rp), sampler_cnte(r.row()))
+        dst = b.edges()[1]
+        if dst.numel():
+            ip = fastAgg.exclusive_sum(torch.unique(dst, return_counts=True)[1].to(torch.int32))
+            np.testing.assert_array_equal(ip.cpu().numpy(), sampler_cnte(r.row()))

@@ -198,6 +198,29 @@ def test_ragged_degrees():
     assert 0.03 < zero < 0.08  # about 5 % of the destinations carry no edges
 
 
+def test_bench_traffic_only_for_unchanged_kernel_sources(tmp_path, monkeypatch):
+    """bench.py reports roofline.traffic from a committed rocprofv3 summary only while the
+    kernel sources it was measured on are unchanged (the summary records their hash)."""
+    import shutil
+
+    import bench
+
+    for rel in bench.TRAFFIC_SOURCES:
+        (tmp_path / rel).parent.mkdir(parents=True, exist_ok=True)
+        shutil.copy(os.path.join(ROOT, rel), tmp_path / rel)
+    (tmp_path / "profiles").mkdir()
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    prof = tmp_path / "profiles" / "tgat_C9_pmc_traffic.md"
+    assert bench.measured_traffic("c9", "tgat_bwd")[0] is None          # no summary
+    prof.write_text(f"source_sha {bench.source_hash()}\ntraffic_per_launch tgat_bwd 123\n")
+    assert bench.measured_traffic("c9", "tgat_bwd")[0] == 123
+    assert bench.measured_traffic("c9", "tgat_fwd")[0] is None          # kernel not listed
+    src = tmp_path / bench.TRAFFIC_SOURCES[0]
+    src.write_text(src.read_text() + "\n// edited\n")
+    value, note = bench.measured_traffic("c9", "tgat_bwd")
+    assert value is None and "other kernel sources" in note
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=300)
@@ -253,6 +276,37 @@ def test_to_blocks_mirrors_to_dgl_blocks():
     assert torch.equal(s2, torch.from_numpy(r.row()).long()) and rb.num_dst_nodes() == r.dim_in()
     assert torch.equal(rb.dstdata["ID"], torch.from_numpy(r.nodes()))
     assert torch.equal(rb.edata["dt"], torch.from_numpy(r.dts())[r.dim_out():])
+
+
+def test_to_blocks_on_host_match_restatement():
+    """fast_amd.mfg.to_blocks on the host equals the oracle's restatement of utils.py:67-87
+    on the golden fixture's sampler results (ragged degrees, zero-degree destinations), for
+    both directions and hist 1 and 2."""
+    from fast_amd.mfg import to_blocks
+    from oracle.ref_cpu import to_dgl_blocks
+    from tests.test_oracle import _GoldenSample, _load
+
+    ret = [_GoldenSample(d) for d in _load("mfg.json")["results"]]
+    for hist in (1, 2):
+        for rev in (False, True):
+            got = to_blocks(ret, hist=hist, reverse=rev, device="cpu")
+            want = to_dgl_blocks(ret, hist, reverse=rev)
+            assert [len(g) for g in got] == [len(g) for g in want]
+            for gg, gw in zip(got, want):
+                for b, w in zip(gg, gw):
+                    _assert_block_matches(b, w)
+
+
+def _assert_block_matches(b, w):
+    src, dst = b.edges()
+    np.testing.assert_array_equal(src.cpu().numpy(), w["src"])
+    np.testing.assert_array_equal(dst.cpu().numpy(), w["dst"])
+    assert (b.num_src_nodes(), b.num_dst_nodes()) == (w["num_src"], w["num_dst"])
+    side = b.srcdata if w["node_side"] == "src" else b.dstdata
+    np.testing.assert_array_equal(side["ID"].cpu().numpy(), w["ID"])
+    np.testing.assert_array_equal(side["ts"].cpu().numpy(), w["ts"])
+    np.testing.assert_array_equal(b.edata["dt"].cpu().numpy(), w["dt"])
+    np.testing.assert_array_equal(b.edata["ID"].cpu().numpy(), w["eID"])
 
 
 def test_split_rows_backward_fills_the_rows_in_front():

@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--dropin", action="store_true",
                     help="instead of the training step, time each drop-in fastAgg operator on the "
                          "ragged config (one JSON line per operator)")
+    ap.add_argument("--launch-log", default=None,
+                    help="write the timed kernels of one step (name, algorithmic bytes, in launch "
+                         "order) and the number of steps the process runs to this JSON file")
     ap.add_argument("--copy-probe-mb", type=int, default=256,
                     help="after the timed steps, one plain row copy of this many MiB "
                          "(fastAgg.gather_rows over rows of 1024 floats): the known-size kernel "
@@ -378,6 +381,11 @@ def main():
     torch.cuda.synchronize()
     tgat.timer = None
     progress(f"{args.steps} steps with kernel events done")
+    if args.launch_log:
+        per = len(timer.records) // args.steps
+        with open(args.launch_log, "w") as fh:
+            json.dump({"config": args.config, "steps_run": args.warmup + 2 * args.steps,
+                       "per_step": [[n, b] for n, _, _, b in timer.records[:per]]}, fh)
     if args.copy_probe_mb > 0:
         copy_probe(args.copy_probe_mb)
     ms = (t1 - t0) * 1e3 / args.steps

@@ -23,7 +23,7 @@ LIBDIR = os.path.join(PKG, "lib")
 OBJDIR = os.path.join(PKG, "_build")
 
 HIP_SOURCES = ["capi.hip", "bookkeeping.hip", "softmax.hip", "aggregate.hip", "fused_attn.hip",
-               "tgat_attn.hip", "epilogue.hip", "head_gemm.hip", "layer_params.hip"]
+               "tgat_attn.hip", "epilogue.hip", "head_gemm.hip", "layer_params.hip", "memory.hip"]
 ARCH = "gfx950"
 LIB_NAME = "libfastagg_hip.so"
 EXT_NAME = "fastAgg"

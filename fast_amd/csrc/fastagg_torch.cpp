@@ -1012,6 +1012,239 @@ at::Tensor head_wgrad(at::Tensor x, at::Tensor y, int64_t groups, bool ones) {
   return dw;
 }
 
+
+// ----------------------------------------------------------------------------------
+// TGN node memory (memorys.py): mail gather, time rows, recurrent cell gates, write-back
+// ----------------------------------------------------------------------------------
+void check_ids(const at::Tensor& ids, const char* name) {
+  CHECK_INPUT(ids);
+  TORCH_CHECK(ids.scalar_type() == at::kInt || ids.scalar_type() == at::kLong, name,
+              " must be int32 or int64, got ", ids.scalar_type());
+  CHECK_DIM(ids, 1);
+}
+
+void check_f32(const at::Tensor& t, int64_t dims, const char* name) {
+  CHECK_INPUT(t);
+  CHECK_DTYPE(t, at::kFloat);
+  TORCH_CHECK(t.dim() == dims, name, " must be ", dims, "-D, got ", t.dim(), "-D");
+}
+
+// -> [mem [n, m], mem_ts [n], x [n, x_width] (mails in columns [0, slots*mail)), mail_ts [n, slots]]
+std::vector<at::Tensor> mail_gather(at::Tensor ids, at::Tensor node_memory, at::Tensor node_memory_ts,
+                                    at::Tensor mailbox, at::Tensor mailbox_ts, int64_t x_width) {
+  check_ids(ids, "ids");
+  check_f32(node_memory, 2, "node_memory");
+  check_f32(node_memory_ts, 1, "node_memory_ts");
+  check_f32(mailbox, 3, "mailbox");
+  check_f32(mailbox_ts, 2, "mailbox_ts");
+  const int64_t nodes = node_memory.size(0), m = node_memory.size(1);
+  const int64_t slots = mailbox.size(1), mail_w = slots * mailbox.size(2);
+  TORCH_CHECK(node_memory_ts.numel() == nodes && mailbox.size(0) == nodes &&
+                  mailbox_ts.size(0) == nodes && mailbox_ts.size(1) == slots,
+              "mail_gather: the memory and mailbox tensors must have one row per node");
+  TORCH_CHECK(x_width >= mail_w, "mail_gather: x_width must hold the mails (", mail_w, ")");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(ids.device());
+  const int64_t n = ids.numel();
+  auto opt = node_memory.options();
+  auto mem = at::empty({n, m}, opt);
+  auto mem_ts = at::empty({n}, opt);
+  auto x = at::empty({n, x_width}, opt);
+  auto mail_ts = at::empty({n, slots}, opt);
+  const int st = fa_mail_gather_f32(
+      n, ids.data_ptr(), ids.scalar_type() == at::kLong ? 1 : 0, nodes, node_memory.data_ptr<float>(),
+      m, static_cast<int32_t>(m), node_memory_ts.data_ptr<float>(), mailbox.data_ptr<float>(), mail_w,
+      mail_w, mailbox_ts.data_ptr<float>(), static_cast<int32_t>(slots), mem.data_ptr<float>(), m,
+      mem_ts.data_ptr<float>(), x.data_ptr<float>(), x_width, mail_ts.data_ptr<float>(),
+      stream_of(ids));
+  check_status(st, "mail_gather");
+  return {mem, mem_ts, x, mail_ts};
+}
+
+// out[:, col:col+dt] = cos(w (ts - mem_ts) + b), in place.
+void time_rows_(at::Tensor out, int64_t col, at::Tensor ts, std::optional<at::Tensor> mem_ts,
+                at::Tensor w, at::Tensor b) {
+  check_f32(out, 2, "out");
+  check_f32(ts, 1, "ts");
+  CHECK_INPUT(w);
+  CHECK_INPUT(b);
+  CHECK_DTYPE(w, at::kFloat);
+  CHECK_DTYPE(b, at::kFloat);
+  const int64_t n = out.size(0), dt = w.numel();
+  TORCH_CHECK(b.numel() == dt && ts.numel() == n, "time_rows_: w, b of dt and ts of n rows");
+  TORCH_CHECK(col >= 0 && col + dt <= out.size(1), "time_rows_: columns out of range");
+  const float* mt = opt_ptr(mem_ts, n, "mem_ts");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
+  const int st = fa_time_rows_f32(n, ts.data_ptr<float>(), mt, w.data_ptr<float>(), b.data_ptr<float>(),
+                                  static_cast<int32_t>(dt), out.data_ptr<float>() + col, out.size(1),
+                                  stream_of(out));
+  check_status(st, "time_rows_");
+}
+
+// -> [dw [dt], db [dt]] for g [n, dt] (rows of any stride, unit column stride)
+std::vector<at::Tensor> time_rows_grad(at::Tensor g, at::Tensor ts, std::optional<at::Tensor> mem_ts,
+                                       at::Tensor w, at::Tensor b) {
+  CHECK_CUDA(g);
+  CHECK_DTYPE(g, at::kFloat);
+  CHECK_DIM(g, 2);
+  TORCH_CHECK(g.stride(1) == 1 || g.size(1) <= 1, "time_rows_grad: g must have unit column stride");
+  check_f32(ts, 1, "ts");
+  CHECK_INPUT(w);
+  CHECK_INPUT(b);
+  CHECK_DTYPE(w, at::kFloat);
+  CHECK_DTYPE(b, at::kFloat);
+  const int64_t n = g.size(0), dt = w.numel();
+  TORCH_CHECK(g.size(1) == dt && b.numel() == dt && ts.numel() == n, "time_rows_grad: shapes");
+  const float* mt = opt_ptr(mem_ts, n, "mem_ts");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(g.device());
+  auto dw = at::empty({dt}, w.options());
+  auto db = at::empty({dt}, w.options());
+  const size_t sb = fa_time_rows_grad_scratch_bytes(static_cast<int32_t>(dt));
+  auto scratch = at::empty({static_cast<int64_t>(sb / 4 + 1)}, w.options());
+  const int64_t ld = n > 0 ? g.stride(0) : dt;
+  const int st = fa_time_rows_grad_f32(n, ts.data_ptr<float>(), mt, w.data_ptr<float>(),
+                                       b.data_ptr<float>(), static_cast<int32_t>(dt),
+                                       g.data_ptr<float>(), ld < dt ? dt : ld, dw.data_ptr<float>(),
+                                       db.data_ptr<float>(), scratch.data_ptr<float>(), sb,
+                                       stream_of(g));
+  check_status(st, "time_rows_grad");
+  return {dw, db};
+}
+
+// -> [hy [n, m], workspace [n, 4m]]
+std::vector<at::Tensor> gru_fwd(at::Tensor gi, at::Tensor gh, std::optional<at::Tensor> h) {
+  check_f32(gi, 2, "gi");
+  check_f32(gh, 2, "gh");
+  const int64_t n = gi.size(0), m = gi.size(1) / 3;
+  TORCH_CHECK(gi.size(1) == 3 * m && gh.sizes() == gi.sizes(), "gru_fwd: gi, gh must be [n, 3m]");
+  const float* hp = opt_ptr(h, n * m, "h");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(gi.device());
+  auto hy = at::empty({n, m}, gi.options());
+  auto ws = at::empty({n, 4 * m}, gi.options());
+  const int st = fa_gru_fwd_f32(n, static_cast<int32_t>(m), gi.data_ptr<float>(), 3 * m,
+                                gh.data_ptr<float>(), 3 * m, hp, m, hy.data_ptr<float>(), m,
+                                ws.data_ptr<float>(), stream_of(gi));
+  check_status(st, "gru_fwd");
+  return {hy, ws};
+}
+
+// -> [dgi [n, 3m], dgh [n, 3m], dh [n, m] (dhy z; empty unless need_dh)]
+std::vector<at::Tensor> gru_bwd(at::Tensor dhy, at::Tensor ws, std::optional<at::Tensor> h,
+                                bool need_dh) {
+  check_f32(dhy, 2, "dhy");
+  check_f32(ws, 2, "workspace");
+  const int64_t n = dhy.size(0), m = dhy.size(1);
+  TORCH_CHECK(ws.size(0) == n && ws.size(1) == 4 * m, "gru_bwd: workspace must be [n, 4m]");
+  const float* hp = opt_ptr(h, n * m, "h");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(dhy.device());
+  auto dgi = at::empty({n, 3 * m}, dhy.options());
+  auto dgh = at::empty({n, 3 * m}, dhy.options());
+  auto dh = need_dh ? at::empty({n, m}, dhy.options()) : at::empty({0}, dhy.options());
+  const int st = fa_gru_bwd_f32(n, static_cast<int32_t>(m), dhy.data_ptr<float>(), m,
+                                ws.data_ptr<float>(), hp, m, dgi.data_ptr<float>(), 3 * m,
+                                dgh.data_ptr<float>(), 3 * m, need_dh ? dh.data_ptr<float>() : nullptr,
+                                m, stream_of(dhy));
+  check_status(st, "gru_bwd");
+  return {dgi, dgh, dh};
+}
+
+at::Tensor rnn_fwd(at::Tensor gi, at::Tensor gh) {
+  check_f32(gi, 2, "gi");
+  check_f32(gh, 2, "gh");
+  TORCH_CHECK(gh.sizes() == gi.sizes(), "rnn_fwd: gi, gh must have one shape");
+  const int64_t n = gi.size(0), m = gi.size(1);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(gi.device());
+  auto hy = at::empty({n, m}, gi.options());
+  const int st = fa_rnn_fwd_f32(n, static_cast<int32_t>(m), gi.data_ptr<float>(), m,
+                                gh.data_ptr<float>(), m, hy.data_ptr<float>(), m, stream_of(gi));
+  check_status(st, "rnn_fwd");
+  return hy;
+}
+
+at::Tensor rnn_bwd(at::Tensor dhy, at::Tensor hy) {
+  check_f32(dhy, 2, "dhy");
+  check_f32(hy, 2, "hy");
+  TORCH_CHECK(dhy.sizes() == hy.sizes(), "rnn_bwd: dhy, hy must have one shape");
+  const int64_t n = hy.size(0), m = hy.size(1);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(hy.device());
+  auto da = at::empty({n, m}, hy.options());
+  const int st = fa_rnn_bwd_f32(n, static_cast<int32_t>(m), dhy.data_ptr<float>(), m,
+                                hy.data_ptr<float>(), m, da.data_ptr<float>(), m, stream_of(hy));
+  check_status(st, "rnn_bwd");
+  return da;
+}
+
+void check_last(const at::Tensor& last, int64_t nodes, int64_t generation) {
+  CHECK_INPUT(last);
+  CHECK_DTYPE(last, at::kLong);
+  TORCH_CHECK(last.numel() == nodes, "last must hold one tag per node");
+  TORCH_CHECK(generation > 0 && generation <= 0xffffffffLL, "generation must be in [1, 2^32)");
+}
+
+// node_memory[ids[r]] = mem[r], node_memory_ts[ids[r]] = ts[r], the last row of an id winning.
+void memory_update_(at::Tensor ids, at::Tensor mem, at::Tensor ts, at::Tensor node_memory,
+                    at::Tensor node_memory_ts, at::Tensor last, int64_t generation) {
+  check_ids(ids, "ids");
+  check_f32(mem, 2, "mem");
+  check_f32(ts, 1, "ts");
+  check_f32(node_memory, 2, "node_memory");
+  check_f32(node_memory_ts, 1, "node_memory_ts");
+  const int64_t rows = ids.numel(), nodes = node_memory.size(0), m = node_memory.size(1);
+  TORCH_CHECK(mem.size(0) == rows && mem.size(1) == m && ts.numel() == rows,
+              "memory_update_: mem [rows, m] and ts [rows] for the ids");
+  TORCH_CHECK(node_memory_ts.numel() == nodes, "memory_update_: node_memory_ts [num_nodes]");
+  check_last(last, nodes, generation);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(ids.device());
+  const int st = fa_memory_update_f32(
+      rows, ids.data_ptr(), ids.scalar_type() == at::kLong ? 1 : 0, mem.data_ptr<float>(), m,
+      static_cast<int32_t>(m), ts.data_ptr<float>(), node_memory.data_ptr<float>(), m,
+      node_memory_ts.data_ptr<float>(), nodes,
+      reinterpret_cast<unsigned long long*>(last.data_ptr<int64_t>()),
+      static_cast<uint32_t>(generation), stream_of(ids));
+  check_status(st, "memory_update_");
+}
+
+// The mails of n edges (mem rows 0..n-1 sources, n..2n-1 destinations) into the mailbox.
+void mailbox_update_(at::Tensor src_ids, at::Tensor dst_ids, at::Tensor mem,
+                     std::optional<at::Tensor> edge_feats, at::Tensor ts, at::Tensor mailbox,
+                     at::Tensor mailbox_ts, at::Tensor next_pos, at::Tensor last, int64_t generation) {
+  check_ids(src_ids, "src_ids");
+  check_ids(dst_ids, "dst_ids");
+  TORCH_CHECK(src_ids.scalar_type() == dst_ids.scalar_type() && src_ids.numel() == dst_ids.numel(),
+              "mailbox_update_: src_ids and dst_ids must match in dtype and length");
+  check_f32(mem, 2, "mem");
+  check_f32(ts, 1, "ts");
+  check_f32(mailbox, 3, "mailbox");
+  check_f32(mailbox_ts, 2, "mailbox_ts");
+  CHECK_INPUT(next_pos);
+  CHECK_DTYPE(next_pos, at::kLong);
+  const int64_t n = src_ids.numel(), nodes = mailbox.size(0), slots = mailbox.size(1);
+  const int64_t m = mem.size(1);
+  int64_t de = 0;
+  const float* ef = nullptr;
+  if (edge_feats.has_value() && edge_feats->defined()) {
+    check_f32(*edge_feats, 2, "edge_feats");
+    TORCH_CHECK(edge_feats->size(0) == n, "mailbox_update_: edge_feats [n, de]");
+    de = edge_feats->size(1);
+    ef = edge_feats->data_ptr<float>();
+  }
+  TORCH_CHECK(mem.size(0) >= 2 * n, "mailbox_update_: mem needs 2n rows");
+  TORCH_CHECK(ts.numel() >= 2 * n, "mailbox_update_: ts needs 2n entries");
+  TORCH_CHECK(mailbox.size(2) == 2 * m + de, "mailbox_update_: mailbox rows of 2m + de, got ",
+              mailbox.size(2), " for m = ", m, ", de = ", de);
+  TORCH_CHECK(mailbox_ts.size(0) == nodes && mailbox_ts.size(1) == slots && next_pos.numel() == nodes,
+              "mailbox_update_: mailbox_ts [num_nodes, slots] and next_pos [num_nodes]");
+  check_last(last, nodes, generation);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(mem.device());
+  const int st = fa_mailbox_update_f32(
+      n, src_ids.data_ptr(), dst_ids.data_ptr(), src_ids.scalar_type() == at::kLong ? 1 : 0,
+      mem.data_ptr<float>(), m, static_cast<int32_t>(m), ef, de, static_cast<int32_t>(de),
+      ts.data_ptr<float>(), mailbox.data_ptr<float>(), slots * mailbox.size(2),
+      mailbox_ts.data_ptr<float>(), next_pos.data_ptr<int64_t>(), static_cast<int32_t>(slots), nodes,
+      reinterpret_cast<unsigned long long*>(last.data_ptr<int64_t>()),
+      static_cast<uint32_t>(generation), stream_of(mem));
+  check_status(st, "mailbox_update_");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(fastAgg, m) {
@@ -1113,5 +1346,26 @@ PYBIND11_MODULE(fastAgg, m) {
   m.def("tgat_epilogue_bwd", &tgat_epilogue_bwd, "backward of tgat_epilogue_fwd", py::arg("dout"),
         py::arg("y"), py::arg("stats"), py::arg("gamma"), py::arg("drop_p"),
         py::arg("need_dbias") = false);
+  // TGN node memory
+  m.def("mail_gather", &mail_gather, "per-row memory, mails and times gathered by node id",
+        py::arg("ids"), py::arg("node_memory"), py::arg("node_memory_ts"), py::arg("mailbox"),
+        py::arg("mailbox_ts"), py::arg("x_width"));
+  m.def("time_rows_", &time_rows_, "out[:, col:col+dt] = cos(w (ts - mem_ts) + b)", py::arg("out"),
+        py::arg("col"), py::arg("ts"), py::arg("mem_ts"), py::arg("w"), py::arg("b"));
+  m.def("time_rows_grad", &time_rows_grad, "dw, db of time_rows_ for the column gradient g",
+        py::arg("g"), py::arg("ts"), py::arg("mem_ts"), py::arg("w"), py::arg("b"));
+  m.def("gru_fwd", &gru_fwd, "GRUCell gates from gi, gh (and h)", py::arg("gi"), py::arg("gh"),
+        py::arg("h") = py::none());
+  m.def("gru_bwd", &gru_bwd, "GRUCell gate gradients", py::arg("dhy"), py::arg("workspace"),
+        py::arg("h") = py::none(), py::arg("need_dh") = false);
+  m.def("rnn_fwd", &rnn_fwd, "RNNCell (tanh) from gi, gh", py::arg("gi"), py::arg("gh"));
+  m.def("rnn_bwd", &rnn_bwd, "RNNCell (tanh) gradient of gi and gh", py::arg("dhy"), py::arg("hy"));
+  m.def("memory_update_", &memory_update_, "node memory write-back, last row of an id wins",
+        py::arg("ids"), py::arg("mem"), py::arg("ts"), py::arg("node_memory"),
+        py::arg("node_memory_ts"), py::arg("last"), py::arg("generation"));
+  m.def("mailbox_update_", &mailbox_update_, "mailbox write-back ('self', 'last')",
+        py::arg("src_ids"), py::arg("dst_ids"), py::arg("mem"), py::arg("edge_feats"), py::arg("ts"),
+        py::arg("mailbox"), py::arg("mailbox_ts"), py::arg("next_pos"), py::arg("last"),
+        py::arg("generation"));
   m.attr("abi_version") = fa_abi_version();
 }

@@ -374,6 +374,80 @@ int fa_gather_rows_bf16_f32(const uint16_t* tab, int64_t ld_tab, int64_t n_tab,
                             const int64_t* idx, int64_t n, int32_t dim, float* out,
                             int64_t ld_out, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------------
+ * TGN node memory (memorys.py:6-304). The state of a MailBox is node_memory
+ * [num_nodes][m], node_memory_ts [num_nodes], mailbox [num_nodes][slots][2m + de] (rows of
+ * ld_mailbox floats), mailbox_ts [num_nodes][slots] and next_pos [num_nodes] (int64).
+ * Node ids are int32 (ids_are_int64 = 0) or int64; an id outside [0, num_nodes) gathers
+ * zeros and writes nothing.
+ * ------------------------------------------------------------------------------- */
+
+/* Per source row i: mem_out[i] = node_memory[ids[i]], mem_ts_out[i] = node_memory_ts[ids[i]],
+ * x_out[i, 0:mail_width] = mailbox[ids[i]] (the slots' mails, flattened), mail_ts_out[i] =
+ * mailbox_ts[ids[i]]. Replaces MailBox.prep_input_mails (memorys.py:57-71), writing the mails
+ * into the rows of the memory updater's input. */
+int fa_mail_gather_f32(int64_t n, const void* ids, int32_t ids_are_int64, int64_t num_nodes,
+                       const float* memory, int64_t ld_memory, int32_t dim_memory,
+                       const float* memory_ts, const float* mailbox, int64_t ld_mailbox,
+                       int64_t mail_width, const float* mailbox_ts, int32_t slots,
+                       float* mem_out, int64_t ld_mem_out, float* mem_ts_out, float* x_out,
+                       int64_t ld_x, float* mail_ts_out, hipStream_t stream);
+
+/* out[i, j] = cos(w[j] * t_i + b[j]), t_i = ts[i] - mem_ts[i] (mem_ts NULL => ts[i]), j < dt,
+ * the product and the sum rounded separately as in the reference's Linear(1, dt). The time
+ * features of GRUMemeoryUpdater.forward (memorys.py:288-290, layers.py:17-29). */
+int fa_time_rows_f32(int64_t n, const float* ts, const float* mem_ts, const float* w,
+                     const float* b, int32_t dt, float* out, int64_t ld_out, hipStream_t stream);
+/* Their gradient: dw[j] = sum_i -sin(w[j] t_i + b[j]) t_i g[i, j], db[j] the same without t_i.
+ * Fixed-order sums (deterministic); scratch of fa_time_rows_grad_scratch_bytes(dt). */
+size_t fa_time_rows_grad_scratch_bytes(int32_t dt);
+int fa_time_rows_grad_f32(int64_t n, const float* ts, const float* mem_ts, const float* w,
+                          const float* b, int32_t dt, const float* g, int64_t ld_g, float* dw,
+                          float* db, void* scratch, size_t scratch_bytes, hipStream_t stream);
+
+/* Elementwise part of torch.nn.GRUCell (memorys.py:291): gi = x W_ih^T + b_ih and
+ * gh = h W_hh^T + b_hh with gate blocks [r | z | n], each m wide; hy = (1 - z) c + z h with
+ * r = sigmoid(gi_r + gh_r), z = sigmoid(gi_z + gh_z), c = tanh(gi_n + r gh_n) (h NULL => 0).
+ * workspace [n][4m] keeps r, z, c, gh_n for fa_gru_bwd_f32. */
+int fa_gru_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const float* gh,
+                   int64_t ld_gh, const float* h, int64_t ld_h, float* hy, int64_t ld_hy,
+                   float* workspace, hipStream_t stream);
+/* dgi, dgh [n][3m] (the gradients of gi and gh) from dhy; dh (optional) = dhy z, the direct
+ * path only (the caller adds dgh W_hh). */
+int fa_gru_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy, const float* workspace,
+                   const float* h, int64_t ld_h, float* dgi, int64_t ld_dgi, float* dgh,
+                   int64_t ld_dgh, float* dh, int64_t ld_dh, hipStream_t stream);
+/* torch.nn.RNNCell with tanh (RNNMemeoryUpdater, memorys.py:332): hy = tanh(gi + gh); the
+ * backward gives da = dhy (1 - hy^2), the gradient of both gi and gh. */
+int fa_rnn_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const float* gh,
+                   int64_t ld_gh, float* hy, int64_t ld_hy, hipStream_t stream);
+int fa_rnn_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy, const float* hy,
+                   int64_t ld_hy, float* da, int64_t ld_da, hipStream_t stream);
+
+/* node_memory[ids[r]] = mem[r], node_memory_ts[ids[r]] = ts[r] for r < rows, the last row of
+ * each id winning (MailBox.update_memory, memorys.py:84-103, whose device index_put leaves the
+ * winner among repeated ids unspecified). `last` [num_nodes] holds one tag per node, zero at
+ * first use and kept by the caller between calls; `generation` must be non-zero and grow with
+ * every call that shares `last` (rows < 2^32). */
+int fa_memory_update_f32(int64_t rows, const void* ids, int32_t ids_are_int64, const float* mem,
+                         int64_t ld_mem, int32_t dim_memory, const float* ts, float* node_memory,
+                         int64_t ld_node_memory, float* node_memory_ts, int64_t num_nodes,
+                         unsigned long long* last, uint32_t generation, hipStream_t stream);
+
+/* MailBox.update_mailbox for deliver_to 'self', mail_combine 'last' (memorys.py:105-139):
+ * n edges with sources src_ids and destinations dst_ids; write rows interleaved
+ * (src_0, dst_0, src_1, ...). Row 2k writes [mem[k], mem[n+k], edge_feats[k]] for src_ids[k],
+ * row 2k+1 writes [mem[n+k], mem[k], edge_feats[k]] for dst_ids[k]; row r's time is ts[r] (the
+ * reference pairs the interleaved mails with ts[:2n] in its own order). The last row of each
+ * node wins; it writes slot next_pos[node] and, with slots > 1, advances next_pos by one
+ * modulo slots. `last` and `generation` as in fa_memory_update_f32 (2n < 2^32). */
+int fa_mailbox_update_f32(int64_t n, const void* src_ids, const void* dst_ids,
+                          int32_t ids_are_int64, const float* mem, int64_t ld_mem,
+                          int32_t dim_memory, const float* edge_feats, int64_t ld_edge,
+                          int32_t dim_edge, const float* ts, float* mailbox, int64_t ld_mailbox,
+                          float* mailbox_ts, int64_t* next_pos, int32_t slots, int64_t num_nodes,
+                          unsigned long long* last, uint32_t generation, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

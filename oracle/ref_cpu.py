@@ -9,7 +9,9 @@ Two parts:
     fastAgg operators (getFastAgg/cuda_operators/*), numpy in / numpy out;
   * torch functions restating ``layers.py``'s TGAT layer with DGL semantics
     (``dgl.ops.edge_softmax`` at layers.py:192, ``update_all(copy_u, sum)`` at
-    layers.py:207), in float32 or float64, differentiable with torch autograd.
+    layers.py:207), in float32 or float64, differentiable with torch autograd;
+  * the TGN node memory of ``memorys.py`` (mail gather, GRU / RNN updater, the mailbox and
+    memory write-back), numpy state, torch for the differentiable updater.
 """
 from __future__ import annotations
 
@@ -413,3 +415,131 @@ def tgat_layer(P: dict, h: torch.Tensor, f: torch.Tensor, dt: torch.Tensor, src:
         rst = torch.where(pos, rst, torch.zeros_like(rst))
     return torch.nn.functional.layer_norm(rst, (D,), cast(P["layer_norm.weight"]),
                                           cast(P["layer_norm.bias"]), P["_eps"])
+
+
+
+# ---------------------------------------------------------------------------------------
+# TGN node memory (memorys.py)
+# ---------------------------------------------------------------------------------------
+def mailbox_state(num_nodes: int, m: int, de: int, slots: int, seed: int = 0) -> dict:
+    """A MailBox's tensors (memorys.py:13-18) as numpy arrays, filled with seeded values."""
+    rng = np.random.default_rng(seed)
+    return {"node_memory": rng.standard_normal((num_nodes, m)).astype(np.float32),
+            "node_memory_ts": (rng.random(num_nodes) * 1e5).astype(np.float32),
+            "mailbox": rng.standard_normal((num_nodes, slots, 2 * m + de)).astype(np.float32),
+            "mailbox_ts": (rng.random((num_nodes, slots)) * 1e5).astype(np.float32),
+            "next_mail_pos": rng.integers(0, slots, num_nodes).astype(np.int64)}
+
+
+def mail_inputs(state: dict, ids) -> dict:
+    """MailBox.prep_input_mails (memorys.py:67-71): per source row its node's memory, memory
+    time, mails (flattened over the slots) and mail times. Ids outside [0, num_nodes) give
+    zero rows (the reference raises; this is the convention of the GPU path)."""
+    ids = np.asarray(ids, dtype=np.int64)
+    n_nodes = state["node_memory"].shape[0]
+    ok = (ids >= 0) & (ids < n_nodes)
+    safe = np.where(ok, ids, 0)
+
+    def take(a):
+        out = a[safe].copy()
+        out[~ok] = 0
+        return out
+
+    mb = state["mailbox"]
+    return {"mem": take(state["node_memory"]), "mem_ts": take(state["node_memory_ts"]),
+            "mem_input": take(mb.reshape(mb.shape[0], -1)), "mail_ts": take(state["mailbox_ts"])}
+
+
+def recurrent_update(P: dict, mem_input, mem, ts, mem_ts, gru: bool = True,
+                     dtype=torch.float64) -> torch.Tensor:
+    """GRUMemeoryUpdater / RNNMemeoryUpdater.forward (memorys.py:286-293, 322-329) in
+    ``dtype``: the time features of ts - mem_ts (a float32 difference, as in the reference)
+    by ``time_encode``; x = [mem_input, time features]; then torch.nn.GRUCell's equations
+    with gate blocks (r, z, n) - r = s(gi_r + gh_r), z = s(gi_z + gh_z),
+    n = tanh(gi_n + r gh_n), h' = (1 - z) n + z h - or RNNCell's h' = tanh(gi + gh), where
+    gi = x W_ih^T + b_ih and gh = h W_hh^T + b_hh. P holds 'updater.weight_ih',
+    'updater.weight_hh', 'updater.bias_ih', 'updater.bias_hh' and, with time features,
+    'time_enc.w.weight' / 'time_enc.w.bias'. Differentiable in every P entry and in mem."""
+    cast = lambda t: torch.as_tensor(t).to(dtype)
+    x = cast(mem_input)
+    if "time_enc.w.weight" in P:
+        t = torch.as_tensor(ts).to(torch.float32) - torch.as_tensor(mem_ts).to(torch.float32)
+        tf = time_encode(t, P["time_enc.w.weight"].view(-1), P["time_enc.w.bias"], dtype)
+        x = torch.cat([x, tf], dim=1)
+    h = cast(mem)
+    gi = x @ cast(P["updater.weight_ih"]).t() + cast(P["updater.bias_ih"])
+    gh = h @ cast(P["updater.weight_hh"]).t() + cast(P["updater.bias_hh"])
+    if not gru:
+        return torch.tanh(gi + gh)
+    m = h.shape[1]
+    r = torch.sigmoid(gi[:, :m] + gh[:, :m])
+    z = torch.sigmoid(gi[:, m:2 * m] + gh[:, m:2 * m])
+    n = torch.tanh(gi[:, 2 * m:] + r * gh[:, 2 * m:])
+    return (1 - z) * n + z * h
+
+
+def combine_node_feature(P: dict, h, updated, dim_node_feat: int, dim_hid: int,
+                         dtype=torch.float64):
+    """memorys.py:297-304: the updated memory added to, mapped onto, or in place of the
+    node features."""
+    if dim_node_feat > 0:
+        if dim_node_feat == dim_hid:
+            return torch.as_tensor(h).to(dtype) + updated
+        return updated + (torch.as_tensor(h).to(dtype) @ P["node_feat_map.weight"].to(dtype).t()
+                          + P["node_feat_map.bias"].to(dtype))
+    return updated
+
+
+def _last_rows(ids: np.ndarray) -> np.ndarray:
+    """Row of the last occurrence of every distinct id (ascending ids)."""
+    rev = ids[::-1]
+    _, first = np.unique(rev, return_index=True)
+    return len(ids) - 1 - first
+
+
+def update_memory(state: dict, nid, memory, ts, root_count: int, neg_samples: int = 1) -> None:
+    """MailBox.update_memory (memorys.py:86-103): node_memory / node_memory_ts of the first
+    2n rows (n = root_count // (neg_samples + 2)), the last row of a repeated id winning (the
+    reference's device index_put leaves that winner unspecified)."""
+    k = root_count // (neg_samples + 2) * 2
+    nid = np.asarray(nid, dtype=np.int64)[:k]
+    memory = np.asarray(memory, dtype=np.float32)[:k]
+    ts = np.asarray(ts, dtype=np.float32)[:k]
+    rows = _last_rows(nid)
+    ok = (nid[rows] >= 0) & (nid[rows] < state["node_memory"].shape[0])
+    rows = rows[ok]
+    state["node_memory"][nid[rows]] = memory[rows]
+    state["node_memory_ts"][nid[rows]] = ts[rows]
+
+
+def update_mailbox(state: dict, memory, root_nodes, ts, edge_feats, neg_samples: int = 1) -> None:
+    """MailBox.update_mailbox for deliver_to 'self', mail_combine 'last' (memorys.py:113-139):
+    for the n = len(root_nodes) // (neg_samples + 2) true edges, source mail
+    [mem_src, mem_dst, ef] and destination mail [mem_dst, mem_src, ef], interleaved
+    (cat(dim=1).reshape); the interleaved row r is paired with ts[r]; unique node ids with
+    the last row of each (torch.unique + scatter_ of arange); slot next_mail_pos written and,
+    with more than one slot, advanced modulo the slot count."""
+    n = len(root_nodes) // (neg_samples + 2)
+    roots = np.asarray(root_nodes, dtype=np.int64)
+    memory = np.asarray(memory, dtype=np.float32)
+    mem_src, mem_dst = memory[:n], memory[n:2 * n]
+    parts_s, parts_d = [mem_src, mem_dst], [mem_dst, mem_src]
+    if edge_feats is not None and np.asarray(edge_feats).size:
+        ef = np.asarray(edge_feats, dtype=np.float32)[:n]
+        parts_s.append(ef)
+        parts_d.append(ef)
+    src_mail = np.concatenate(parts_s, axis=1)
+    dst_mail = np.concatenate(parts_d, axis=1)
+    mail = np.concatenate([src_mail, dst_mail], axis=1).reshape(2 * n, -1)
+    nid = np.stack([roots[:n], roots[n:2 * n]], axis=1).reshape(-1)
+    mail_ts = np.asarray(ts, dtype=np.float32)[:2 * n]
+    perm = _last_rows(nid)
+    nid, mail, mail_ts = nid[perm], mail[perm], mail_ts[perm]
+    ok = (nid >= 0) & (nid < state["mailbox"].shape[0])
+    nid, mail, mail_ts = nid[ok], mail[ok], mail_ts[ok]
+    slots = state["mailbox"].shape[1]
+    pos = state["next_mail_pos"][nid]
+    state["mailbox"][nid, pos] = mail
+    state["mailbox_ts"][nid, pos] = mail_ts
+    if slots > 1:
+        state["next_mail_pos"][nid] = (pos + 1) % slots

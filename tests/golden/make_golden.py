@@ -353,6 +353,113 @@ def mfg_case() -> dict:
     return {"results": results, "blocks": expect, "cnte": cnte, "rowptr": rowptr}
 
 
+# -------------------------------------------------------------------------------------
+# TGN node memory (memorys.py:6-304)
+# -------------------------------------------------------------------------------------
+def sigmoid(x: float) -> float:
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def memory_case() -> dict:
+    """MailBox.prep_input_mails (memorys.py:67-71), then two batches of update_mailbox
+    ('self', 'last': memorys.py:113-139) followed by update_memory (memorys.py:86-103), in the
+    order train.py:220-221 calls them, simulated row by row: the mails of edge k are
+    [mem_src, mem_dst, ef] for its source and [mem_dst, mem_src, ef] for its destination,
+    interleaved (source, destination, ...), the interleaved row r paired with ts[r]; per node
+    the last row wins and writes slot next_mail_pos (advanced modulo the slot count when
+    there is more than one slot); update_memory assigns rows 0..2n-1 in order. Roots repeat
+    within and across batches. A generator of its own."""
+    rng = random.Random(7002)
+    cases = []
+    for N, m, de, slots in ((12, 3, 2, 3), (9, 2, 0, 1)):
+        mail = 2 * m + de
+        st = {"node_memory": [[f32(rng.gauss(0, 1)) for _ in range(m)] for _ in range(N)],
+              "node_memory_ts": [f32(rng.random() * 100) for _ in range(N)],
+              "mailbox": [[[f32(rng.gauss(0, 1)) for _ in range(mail)] for _ in range(slots)]
+                          for _ in range(N)],
+              "mailbox_ts": [[f32(rng.random() * 100) for _ in range(slots)] for _ in range(N)],
+              "next_mail_pos": [rng.randrange(slots) for _ in range(N)]}
+        init = json.loads(json.dumps(st))
+        ids = [rng.randrange(N) for _ in range(15)]
+        prep = json.loads(json.dumps({
+            "ids": ids,
+            "mem": [st["node_memory"][i] for i in ids],
+            "mem_ts": [st["node_memory_ts"][i] for i in ids],
+            "mem_input": [[v for s_ in st["mailbox"][i] for v in s_] for i in ids],
+            "mail_ts": [st["mailbox_ts"][i] for i in ids]}))   # a copy: the batches below
+        # update the state's lists in place
+        batches = []
+        for _ in range(2):
+            n, neg = 5, 1
+            roots = [rng.randrange(N) for _ in range(n * (neg + 2))]
+            n_rows = len(roots) + 4
+            memory = [[f32(rng.gauss(0, 1)) for _ in range(m)] for _ in range(n_rows)]
+            lu_nid = roots + [rng.randrange(N) for _ in range(4)]
+            lu_ts = [f32(rng.random() * 1000) for _ in range(n_rows)]
+            ts = [f32(rng.random() * 1000) for _ in range(len(roots))]
+            ef = [[f32(rng.gauss(0, 1)) for _ in range(de)] for _ in range(n)]
+            rows = []
+            for k in range(n):
+                rows.append((roots[k], memory[k] + memory[n + k] + ef[k], ts[2 * k]))
+                rows.append((roots[n + k], memory[n + k] + memory[k] + ef[k], ts[2 * k + 1]))
+            last = {}
+            for r, (nid, _, _) in enumerate(rows):
+                last[nid] = r
+            for nid in sorted(last):
+                _, ml, mt = rows[last[nid]]
+                pos = st["next_mail_pos"][nid]
+                st["mailbox"][nid][pos] = list(ml)
+                st["mailbox_ts"][nid][pos] = mt
+                if slots > 1:
+                    st["next_mail_pos"][nid] = (pos + 1) % slots
+            for i in range(len(roots) // (neg + 2) * 2):
+                st["node_memory"][lu_nid[i]] = list(memory[i])
+                st["node_memory_ts"][lu_nid[i]] = lu_ts[i]
+            batches.append({"roots": roots, "neg": neg, "memory": memory, "nid": lu_nid,
+                            "lu_ts": lu_ts, "ts": ts, "edge_feats": ef,
+                            "after": json.loads(json.dumps(st))})
+        cases.append({"dims": [N, m, de, slots], "init": init, "prep": prep, "batches": batches})
+    return {"cases": cases}
+
+
+def recurrent_case() -> dict:
+    """GRUMemeoryUpdater / RNNMemeoryUpdater forward (memorys.py:286-293, 322-329) on three
+    rows: x = [mails, cos(w (ts - mem_ts) + b)] with the time argument rounded as the
+    reference's float32 Linear(1, dt) rounds it, then torch.nn.GRUCell's equations with gate
+    blocks (r, z, n): r = s(W_ir x + b_ir + W_hr h + b_hr), z likewise, n = tanh(W_in x +
+    b_in + r (W_hn h + b_hn)), h' = (1 - z) n + z h; and RNNCell's h' = tanh(W_ih x + b_ih +
+    W_hh h + b_hh)."""
+    rng = random.Random(7003)
+    rows, mail, dt, hid = 3, 4, 3, 2
+    din = mail + dt
+    g = lambda: f32(rng.gauss(0, 0.5))
+    P = {"w_ih": [[g() for _ in range(din)] for _ in range(3 * hid)],
+         "w_hh": [[g() for _ in range(hid)] for _ in range(3 * hid)],
+         "b_ih": [g() for _ in range(3 * hid)], "b_hh": [g() for _ in range(3 * hid)],
+         "r_ih": [[g() for _ in range(din)] for _ in range(hid)],
+         "r_hh": [[g() for _ in range(hid)] for _ in range(hid)],
+         "rb_ih": [g() for _ in range(hid)], "rb_hh": [g() for _ in range(hid)],
+         "tw": [f32(1 / 10 ** (j * 9 / (dt - 1))) for j in range(dt)], "tb": [g() for _ in range(dt)]}
+    mails = [[g() for _ in range(mail)] for _ in range(rows)]
+    h = [[g() for _ in range(hid)] for _ in range(rows)]
+    ts = [f32(rng.random() * 1e4) for _ in range(rows)]
+    mem_ts = [f32(rng.random() * 1e3) for _ in range(rows)]
+    gru, rnn = [], []
+    for i in range(rows):
+        t = f32(ts[i] - mem_ts[i])
+        x = mails[i] + [math.cos(f32(f32(t * P["tw"][j]) + P["tb"][j])) for j in range(dt)]
+        gi = linear(x, P["w_ih"], P["b_ih"])
+        gh = linear(h[i], P["w_hh"], P["b_hh"])
+        r = [sigmoid(gi[j] + gh[j]) for j in range(hid)]
+        z = [sigmoid(gi[hid + j] + gh[hid + j]) for j in range(hid)]
+        nn = [math.tanh(gi[2 * hid + j] + r[j] * gh[2 * hid + j]) for j in range(hid)]
+        gru.append([(1 - z[j]) * nn[j] + z[j] * h[i][j] for j in range(hid)])
+        ri = linear(x, P["r_ih"], P["rb_ih"])
+        rh = linear(h[i], P["r_hh"], P["rb_hh"])
+        rnn.append([math.tanh(ri[j] + rh[j]) for j in range(hid)])
+    return {"P": P, "mails": mails, "h": h, "ts": ts, "mem_ts": mem_ts, "gru": gru, "rnn": rnn}
+
+
 def main():
     rng = random.Random(20240611)
     fixtures = {
@@ -363,6 +470,8 @@ def main():
         "tgat_layer_tiny.json": tgat_case(rng),
         "time_weight.json": time_weight(),
         "mfg.json": mfg_case(),
+        "memory.json": memory_case(),
+        "recurrent.json": recurrent_case(),
     }
     for name, data in fixtures.items():
         with open(os.path.join(HERE, name), "w") as fh:

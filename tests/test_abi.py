@@ -221,3 +221,27 @@ def test_softmax_rejects_bad_arguments(lib):
     assert call(-1, 2, 2, 0) == FA_EINVAL
     assert call(0, 2, 2, 0) == FA_OK        # nothing to do: returns before any launch
     assert call(4, 0, 2, 0) == FA_OK
+
+
+def test_memory_entry_points_reject_bad_arguments(lib):
+    """The memory path's argument checks run before any launch (no device access)."""
+    vp, c = ctypes.c_void_p, ctypes.c_int64
+    one = ctypes.c_void_p(16)
+    # generation 0 and negative sizes
+    assert lib.fa_memory_update_f32(c(1), one, 1, one, c(4), 4, one, one, c(4), one, c(10), one,
+                                    ctypes.c_uint32(0), None) == -1
+    assert lib.fa_memory_update_f32(c(-1), one, 1, one, c(4), 4, one, one, c(4), one, c(10), one,
+                                    ctypes.c_uint32(1), None) == -1
+    # mailbox rows narrower than slots x (2m + de)
+    assert lib.fa_mailbox_update_f32(c(2), one, one, 1, one, c(4), 4, None, c(0), 0, one, one,
+                                     c(7), one, one, 2, c(10), one, ctypes.c_uint32(1), None) == -1
+    # gru: leading dimension below 3m; missing workspace
+    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(11), one, c(12), None, c(0), one, c(4), one, None) == -1
+    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(12), one, c(12), None, c(0), one, c(4), None, None) == -1
+    # time gradient without scratch
+    assert lib.fa_time_rows_grad_f32(c(3), one, None, one, one, 8, one, c(8), one, one, None,
+                                     ctypes.c_size_t(0), None) == -4
+    assert lib.fa_time_rows_grad_scratch_bytes(8) >= 2 * 8 * 4
+    # nothing to do is not an error
+    assert lib.fa_mail_gather_f32(c(0), None, 0, c(0), None, c(0), 0, None, None, c(0), c(0), None,
+                                  0, None, c(0), None, None, c(0), None, None) == 0

@@ -328,3 +328,72 @@ def test_split_rows_backward_fills_the_rows_in_front():
     assert torch.equal(out2, want)
     out3, _ = tgat._SplitRows.backward(Ctx(), None, g_src.clone())
     assert torch.equal(out3[:4], torch.zeros(4, 3)) and torch.equal(out3[4:], g_src)
+
+
+# ---------------------------------------------------------------------------------------
+# TGN node memory: host-side state and dispatch (no kernels)
+# ---------------------------------------------------------------------------------------
+def _mem_param(**kw):
+    p = {"type": "node", "dim_time": 100, "deliver_to": "self", "mail_combine": "last",
+         "memory_update": "gru", "mailbox_size": 2, "combine_node_feature": True, "dim_out": 100}
+    p.update(kw)
+    return p
+
+
+def test_mailbox_state_matches_the_reference_layout():
+    """memorys.py:13-18: the tensors, shapes and dtypes a MailBox holds, zero-initialised on
+    the host until moved."""
+    from fast_amd.memorys import MailBox
+
+    mb = MailBox(_mem_param(), 11, 172)
+    assert mb.node_memory.shape == (11, 100) and mb.node_memory.dtype == torch.float32
+    assert mb.node_memory_ts.shape == (11,)
+    assert mb.mailbox.shape == (11, 2, 372) and mb.mailbox_ts.shape == (11, 2)
+    assert mb.next_mail_pos.dtype == torch.long and mb.device.type == "cpu"
+    for t in (mb.node_memory, mb.mailbox, mb.mailbox_ts, mb.next_mail_pos):
+        assert not t.any()
+    with pytest.raises(NotImplementedError):
+        MailBox(_mem_param(type="none"), 3, 0)
+
+
+def test_mailbox_unsupported_modes_raise():
+    from fast_amd.memorys import MailBox
+
+    mb = MailBox(_mem_param(deliver_to="neighbors"), 4, 0)
+    with pytest.raises(NotImplementedError):
+        mb.update_mailbox(None, torch.zeros(3, 100), np.zeros(3, np.int32), np.zeros(3, np.float32),
+                          None, None)
+    mb = MailBox(_mem_param(mail_combine="mean"), 4, 0)
+    with pytest.raises(NotImplementedError):
+        mb.update_mailbox(None, torch.zeros(3, 100), np.zeros(3, np.int32), np.zeros(3, np.float32),
+                          None, None)
+
+
+def test_mailbox_write_tags_wrap_before_32_bits():
+    """The per-node tags of the write-back grow by one generation per call and restart
+    (with the tags cleared) before the generation would pass 32 bits."""
+    from fast_amd import memorys
+
+    mb = memorys.MailBox(_mem_param(), 5, 0)
+    last, g1 = mb._tags()
+    _, g2 = mb._tags()
+    assert (g1, g2) == (1, 2) and last.shape == (5,) and last.dtype == torch.int64
+    mb._gen = memorys._TAG_LIMIT - 1
+    last.fill_(7)
+    last2, g = mb._tags()
+    assert g == 1 and not last2.any()
+
+
+def test_updaters_keep_the_reference_parameters():
+    """GRUMemeoryUpdater / RNNMemeoryUpdater hold the reference's modules (state-dict keys
+    and shapes of memorys.py:270-282, 308-320)."""
+    from fast_amd.memorys import GRUMemeoryUpdater, RNNMemeoryUpdater
+
+    g = GRUMemeoryUpdater(_mem_param(), 372, 100, 100, 50)
+    sd = {k: tuple(v.shape) for k, v in g.state_dict().items()}
+    assert sd["updater.weight_ih"] == (300, 472) and sd["updater.weight_hh"] == (300, 100)
+    assert sd["time_enc.w.weight"] == (100, 1) and sd["node_feat_map.weight"] == (100, 50)
+    r = RNNMemeoryUpdater(_mem_param(), 372, 100, 0, 100)
+    sd = {k: tuple(v.shape) for k, v in r.state_dict().items()}
+    assert sd == {"updater.weight_ih": (100, 372), "updater.weight_hh": (100, 100),
+                  "updater.bias_ih": (100,), "updater.bias_hh": (100,)}

@@ -440,3 +440,99 @@ def test_dropout_mask_properties():
     # the high seed word matters as well
     c = C.dropout_mask(4000, 2, 1 + (1 << 32), 0.5)
     assert 0.4 < (a != c).mean() < 0.6
+
+
+# ---------------------------------------------------------------------------------------
+# TGN node memory (memorys.py)
+# ---------------------------------------------------------------------------------------
+def _state_from(d):
+    return {"node_memory": np.asarray(d["node_memory"], dtype=np.float32),
+            "node_memory_ts": np.asarray(d["node_memory_ts"], dtype=np.float32),
+            "mailbox": np.asarray(d["mailbox"], dtype=np.float32),
+            "mailbox_ts": np.asarray(d["mailbox_ts"], dtype=np.float32),
+            "next_mail_pos": np.asarray(d["next_mail_pos"], dtype=np.int64)}
+
+
+def _assert_state_equal(got, want):
+    for k in ("node_memory", "node_memory_ts", "mailbox", "mailbox_ts", "next_mail_pos"):
+        np.testing.assert_array_equal(got[k], np.asarray(want[k], dtype=got[k].dtype), err_msg=k)
+
+
+def test_memory_golden():
+    """mail_inputs, update_mailbox and update_memory against the row-by-row simulation of
+    memorys.py:67-71, 113-139, 86-103 (two batches, repeated roots, 3 slots / 1 slot, with
+    and without edge features): every value exact."""
+    for c in _load("memory.json")["cases"]:
+        N, m, de, slots = c["dims"]
+        st = _state_from(c["init"])
+        p = c["prep"]
+        got = ref_cpu.mail_inputs(st, p["ids"])
+        for k in ("mem", "mem_ts", "mem_input", "mail_ts"):
+            np.testing.assert_array_equal(got[k], np.asarray(p[k], dtype=np.float32), err_msg=k)
+        for b in c["batches"]:
+            ef = np.asarray(b["edge_feats"], dtype=np.float32).reshape(len(b["edge_feats"]), de)
+            ref_cpu.update_mailbox(st, b["memory"], b["roots"], b["ts"], ef if de else None, b["neg"])
+            ref_cpu.update_memory(st, b["nid"], b["memory"], b["lu_ts"], len(b["roots"]), b["neg"])
+            _assert_state_equal(st, b["after"])
+
+
+def test_mail_inputs_invalid_ids_give_zero_rows():
+    st = ref_cpu.mailbox_state(5, 2, 1, 2, seed=3)
+    got = ref_cpu.mail_inputs(st, [4, -1, 5, 0])
+    assert not got["mem"][1].any() and not got["mem"][2].any()
+    np.testing.assert_array_equal(got["mem_input"][0], st["mailbox"][4].reshape(-1))
+    np.testing.assert_array_equal(got["mail_ts"][3], st["mailbox_ts"][0])
+
+
+def test_update_mailbox_cycles_the_slots():
+    """A node that receives a mail in three consecutive batches fills slots p, p+1, p+2
+    (mod slots), each with that batch's mail."""
+    st = ref_cpu.mailbox_state(4, 1, 0, 3, seed=1)
+    st["next_mail_pos"][:] = 2
+    for step in range(3):
+        mem = np.array([[10.0 + step], [20.0 + step], [0.0]], dtype=np.float32)
+        ref_cpu.update_mailbox(st, mem, [1, 2, 3], [5.0 + step, 6.0 + step, 0.0], None, 1)
+    np.testing.assert_array_equal(st["mailbox"][1, :, 0], [11.0, 12.0, 10.0])
+    np.testing.assert_array_equal(st["mailbox"][2, :, 0], [21.0, 22.0, 20.0])
+    np.testing.assert_array_equal(st["mailbox"][1, :, 1], [21.0, 22.0, 20.0])
+    # row r of the interleaved mails takes ts[r]: node 1 (row 0) ts[0], node 2 (row 1) ts[1]
+    np.testing.assert_array_equal(st["mailbox_ts"][1], [6.0, 7.0, 5.0])
+    np.testing.assert_array_equal(st["mailbox_ts"][2], [7.0, 8.0, 6.0])
+    assert st["next_mail_pos"][1] == 2 and st["next_mail_pos"][0] == 2
+
+
+def _recurrent_params(c, gru):
+    P = c["P"]
+    t = lambda v: torch.tensor(v, dtype=torch.float64)
+    k = ("w_ih", "w_hh", "b_ih", "b_hh") if gru else ("r_ih", "r_hh", "rb_ih", "rb_hh")
+    return {"updater.weight_ih": t(P[k[0]]), "updater.weight_hh": t(P[k[1]]),
+            "updater.bias_ih": t(P[k[2]]), "updater.bias_hh": t(P[k[3]]),
+            "time_enc.w.weight": torch.tensor(P["tw"], dtype=torch.float32).view(-1, 1),
+            "time_enc.w.bias": torch.tensor(P["tb"], dtype=torch.float32)}
+
+
+@pytest.mark.parametrize("gru", [True, False])
+def test_recurrent_update_golden(gru):
+    c = _load("recurrent.json")
+    out = ref_cpu.recurrent_update(_recurrent_params(c, gru), c["mails"], c["h"],
+                                   torch.tensor(c["ts"]), torch.tensor(c["mem_ts"]), gru)
+    np.testing.assert_allclose(out.numpy(), np.asarray(c["gru" if gru else "rnn"]), rtol=1e-12,
+                               atol=1e-13)
+
+
+@pytest.mark.parametrize("gru", [True, False])
+def test_recurrent_update_matches_torch_cells(gru):
+    """The written-out cell equals torch.nn.GRUCell / RNNCell (float64) applied to
+    [mails, time features]."""
+    torch.manual_seed(5)
+    n, mail, dt, hid = 7, 10, 6, 5
+    cell = (torch.nn.GRUCell if gru else torch.nn.RNNCell)(mail + dt, hid).double()
+    P = {"updater." + k: v.detach() for k, v in cell.named_parameters()}
+    P["time_enc.w.weight"] = ref_cpu.time_encoding_weight(dt).view(-1, 1)
+    P["time_enc.w.bias"] = torch.randn(dt)
+    mails, h = torch.randn(n, mail, dtype=torch.float64), torch.randn(n, hid, dtype=torch.float64)
+    ts, mem_ts = torch.rand(n) * 1e5, torch.rand(n) * 1e4
+    tf = ref_cpu.time_encode(ts - mem_ts, P["time_enc.w.weight"].view(-1), P["time_enc.w.bias"])
+    want = cell(torch.cat([mails, tf], 1), h)
+    got = ref_cpu.recurrent_update(P, mails, h, ts, mem_ts, gru)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)

@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
-    ap.add_argument("--config", choices=("c3", "c4", "c5"), default="c3",
+    ap.add_argument("--config", choices=("c3", "c4", "c4m", "c5"), default="c3",
                     help="c3: the headline float32 2-layer workload; c4: the ragged TGN-style "
                          "layer; c5: bf16 tables of widths 413 / 186, 8 heads, hidden 256")
     ap.add_argument("--dropin", action="store_true",
@@ -204,6 +204,39 @@ def cpu_layer(n_dst, reps, seed, backward=True, ragged=False):
     return _median_time(call, reps), b.num_edges()
 
 
+def cpu_tgn_layer(n_dst, reps, seed):
+    """The oracle's float32 restatement of the TGN updater (memorys.py:286-293) over a ragged
+    block's source rows followed by one TGAT layer, forward and backward, on the host:
+    (seconds per call, edges)."""
+    import numpy as np
+    import torch
+
+    from fast_amd.memorys import GRUMemeoryUpdater
+    from fast_amd.tgat import TransfomerAttentionLayer
+    from fast_amd.workloads import ragged_degrees, single_layer
+    from oracle.ref_cpu import recurrent_update, tgat_layer
+
+    torch.manual_seed(seed)
+    layer = TransfomerAttentionLayer(100, 172, 100, 2, 0.0, 0.0, 100)
+    upd = GRUMemeoryUpdater(TGN_MEMORY, 372, 100, 100, 0)
+    inp = single_layer(n_dst, degrees=ragged_degrees(n_dst, seed), seed=seed)
+    b = inp.block
+    src, dst = b.edges()
+    n = b.num_src_nodes()
+    g = torch.Generator().manual_seed(seed)
+    mails, mem = torch.randn(n, 372, generator=g), torch.randn(n, 100, generator=g)
+    ts, mem_ts = torch.rand(n, generator=g) * 1e6, torch.rand(n, generator=g) * 1e5
+
+    def call():
+        Pu = {k: v.detach().float().requires_grad_(True) for k, v in upd.named_parameters()}
+        h = recurrent_update(Pu, mails, mem, ts, mem_ts, True, dtype=torch.float32)
+        out = tgat_layer(_cpu_params(layer), h, b.edata["f"], b.edata["dt"], src, dst, n_dst,
+                         dtype=torch.float32)
+        out.backward(inp.dout)
+
+    return _median_time(call, reps), b.num_edges()
+
+
 def cpu_baseline(config: str, reps: int, seed: int) -> dict:
     """The CPU restatement (oracle/ref_cpu.py, float32, torch on the host cores) of the same
     workload on a bounded sample; for c3 also the C1 forward and C2 forward + backward
@@ -219,6 +252,11 @@ def cpu_baseline(config: str, reps: int, seed: int) -> dict:
         t, edges, text = cpu_stack((413, 186, 100, 8, 256), 500, (1_000_000, 1_000_000), reps, seed,
                                    hot_frac=0.05, hot_share=0.8, dtype=torch.bfloat16, row_align=4)
         text += ", bf16 values widened, 500 of the 4000 roots"
+    elif config == "c4m":
+        t, edges = cpu_tgn_layer(20_000, reps, seed)
+        text = (f"TGN step sample: GRU memory updater over the source rows, then 1 ragged TGAT "
+                f"layer fwd+bwd, 20000 of the 200000 destinations (Zipf(1.5) degrees in [1, 20], "
+                f"5 % empty), {edges} edges, dense gathered rows")
     else:
         t, edges = cpu_layer(200_000, reps, seed, ragged=True)
         text = (f"1 ragged TGAT layer fwd+bwd, 200000 destinations (Zipf(1.5) degrees in [1, 20], "
@@ -297,6 +335,38 @@ def dropin_bench(reps: int = 20, seed: int = 0) -> None:
                           "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+TGN_MEMORY = {"type": "node", "dim_time": 100, "deliver_to": "self", "mail_combine": "last",
+              "memory_update": "gru", "mailbox_size": 1, "combine_node_feature": True,
+              "dim_out": 100}   # config/TGN.yml
+
+
+def tgn_step_module():
+    """nn.Module of one TGN step on a block: mails gathered, the GRU updater writing
+    srcdata['h'], the TGAT layer on it; ``after_step`` writes the roots' mails and memories
+    back (train.py:202-221)."""
+    import torch
+
+    class TgnStep(torch.nn.Module):
+        def __init__(self, updater, layer, mailbox, roots, ts, edge_feats):
+            super().__init__()
+            self.updater, self.layer = updater, layer
+            self.mailbox, self.roots, self.ts, self.edge_feats = mailbox, roots, ts, edge_feats
+
+        def forward(self, b):
+            self.mailbox.prep_input_mails([b])
+            self.updater([b])
+            return self.layer(b)
+
+        def after_step(self):
+            u = self.updater
+            self.mailbox.update_mailbox(u.last_updated_nid, u.last_updated_memory, self.roots,
+                                        self.ts, self.edge_feats, None)
+            self.mailbox.update_memory(u.last_updated_nid, u.last_updated_memory, self.roots,
+                                       u.last_updated_ts)
+
+    return TgnStep
+
+
 def build_workload(config: str, args, dev):
     """(module, list of blocks, upstream gradient, edges per step, description, dtype)."""
     import torch
@@ -305,6 +375,36 @@ def build_workload(config: str, args, dev):
     from fast_amd.workloads import ragged_layer, two_layer
 
     torch.manual_seed(args.seed)
+    if config == "c4m":
+        from fast_amd.memorys import GRUMemeoryUpdater, MailBox
+
+        layer = TransfomerAttentionLayer(100, 172, 100, 2, 0.2, 0.2, 100).to(dev)
+        updater = GRUMemeoryUpdater(TGN_MEMORY, 2 * 100 + 172, 100, 100, 0).to(dev)
+        inp = ragged_layer(200_000, seed=args.seed, device=dev)
+        blk = inp.block
+        nodes = blk.node_table.shape[0]
+        g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+        mailbox = MailBox(TGN_MEMORY, nodes, 172, _node_memory=blk.node_table,
+                          _node_memory_ts=torch.rand(nodes, generator=g, device=dev) * 1e5,
+                          _mailbox=torch.randn(nodes, 1, 372, generator=g, device=dev),
+                          _mailbox_ts=torch.rand(nodes, 1, generator=g, device=dev) * 1e5,
+                          _next_mail_pos=torch.zeros(nodes, dtype=torch.long, device=dev))
+        blk.node_table = None   # node rows: the updated memory in srcdata['h']
+        N = blk.num_dst_nodes()
+        _, dst = blk.edges()
+        t_dst = 1e5 + torch.rand(N, generator=g, device=dev) * 9e5
+        blk.srcdata["ts"] = torch.cat([t_dst, t_dst[dst] - blk.edata["dt"]])
+        n_true = N // 3
+        eids = torch.randint(0, blk.edge_table.shape[0], (n_true,), generator=g, device=dev)
+        model = tgn_step_module()(updater, layer, mailbox, blk.srcdata["ID"][:N],
+                                  blk.srcdata["ts"][:N], blk.edge_table[eids])
+        desc = ("C4 as a TGN step (config/TGN.yml memory: GRU updater, mailbox 1, memory 100): "
+                "mails and memory of all source rows gathered from a 1M-node MailBox, GRU "
+                "updater (torch GEMMs + gate kernels) into the node rows, ragged TGAT layer "
+                "fwd+bwd+Adam, mailbox and memory write-back of the batch's roots; 200000 "
+                "destinations with Zipf(1.5) degrees clipped to [1, 20] and 5% empty, edge rows "
+                "from a 10M x 172 table, time 100, 2 heads, hidden 100")
+        return model, [blk], inp.dout, [blk.num_edges()], desc, "f32"
     if config == "c5":
         dims = (413, 186, 100, 8, 256)
         enc = TGATEncoder(*dims, num_layers=2, dropout=0.1, att_dropout=0.1).to(dev)
@@ -359,6 +459,8 @@ def main():
         out = model(blocks) if len(blocks) > 1 else model(blocks[0])
         out.backward(dout)
         opt.step()
+        if hasattr(model, "after_step"):
+            model.after_step()
 
     progress(f"inputs resident: {len(blocks)} blocks, {edges} edges per step")
     for _ in range(args.warmup):

@@ -1127,7 +1127,7 @@ std::vector<at::Tensor> gru_fwd(at::Tensor gi, at::Tensor gh, std::optional<at::
   return {hy, ws};
 }
 
-// -> [dgi [n, 3m], dgh [n, 3m], dh [n, m] (dhy z; empty unless need_dh)]
+// -> [dgi [n, 3m], dgh [n, 3m], dh [n, m] (dhy z; empty unless need_dh), db_ih [3m], db_hh [3m]]
 std::vector<at::Tensor> gru_bwd(at::Tensor dhy, at::Tensor ws, std::optional<at::Tensor> h,
                                 bool need_dh) {
   check_f32(dhy, 2, "dhy");
@@ -1139,12 +1139,17 @@ std::vector<at::Tensor> gru_bwd(at::Tensor dhy, at::Tensor ws, std::optional<at:
   auto dgi = at::empty({n, 3 * m}, dhy.options());
   auto dgh = at::empty({n, 3 * m}, dhy.options());
   auto dh = need_dh ? at::empty({n, m}, dhy.options()) : at::empty({0}, dhy.options());
+  auto db_ih = at::empty({3 * m}, dhy.options());
+  auto db_hh = at::empty({3 * m}, dhy.options());
+  const size_t sb = fa_gru_bwd_scratch_bytes(n, static_cast<int32_t>(m));
+  auto scratch = at::empty({static_cast<int64_t>(sb / 4 + 1)}, dhy.options());
   const int st = fa_gru_bwd_f32(n, static_cast<int32_t>(m), dhy.data_ptr<float>(), m,
                                 ws.data_ptr<float>(), hp, m, dgi.data_ptr<float>(), 3 * m,
                                 dgh.data_ptr<float>(), 3 * m, need_dh ? dh.data_ptr<float>() : nullptr,
-                                m, stream_of(dhy));
+                                m, db_ih.data_ptr<float>(), db_hh.data_ptr<float>(),
+                                scratch.data_ptr<float>(), sb, stream_of(dhy));
   check_status(st, "gru_bwd");
-  return {dgi, dgh, dh};
+  return {dgi, dgh, dh, db_ih, db_hh};
 }
 
 at::Tensor rnn_fwd(at::Tensor gi, at::Tensor gh) {
@@ -1356,7 +1361,7 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("g"), py::arg("ts"), py::arg("mem_ts"), py::arg("w"), py::arg("b"));
   m.def("gru_fwd", &gru_fwd, "GRUCell gates from gi, gh (and h)", py::arg("gi"), py::arg("gh"),
         py::arg("h") = py::none());
-  m.def("gru_bwd", &gru_bwd, "GRUCell gate gradients", py::arg("dhy"), py::arg("workspace"),
+  m.def("gru_bwd", &gru_bwd, "GRUCell gate and bias gradients", py::arg("dhy"), py::arg("workspace"),
         py::arg("h") = py::none(), py::arg("need_dh") = false);
   m.def("rnn_fwd", &rnn_fwd, "RNNCell (tanh) from gi, gh", py::arg("gi"), py::arg("gh"));
   m.def("rnn_bwd", &rnn_bwd, "RNNCell (tanh) gradient of gi and gh", py::arg("dhy"), py::arg("hy"));

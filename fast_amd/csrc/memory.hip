@@ -149,40 +149,97 @@ __global__ __launch_bounds__(kEltBlock) void time_rows(const float* ts, const fl
   }
 }
 
-constexpr int kTimeGradBlocks = 2048;
-constexpr int kTimeGradThreads = 128;
+// Row-chunk kernels: workgroup b owns rows [b*per, min(n, (b+1)*per)); its 256 threads are
+// 128 column lanes x 2 row phases (phase p takes rows r0 + p, r0 + p + 2, ...), so each
+// row's columns are read and written contiguously. Column sums are kept per thread in row
+// order, the two phases added in a fixed order through LDS, and the workgroups' partials
+// summed by col_finish in a fixed order: the sums do not depend on scheduling.
+constexpr int kColLanes = 128;
+constexpr int kRowPhases = 2;
+constexpr int kColBlock = kColLanes * kRowPhases;
+constexpr int kMaxChunkBlocks = 4096;
+constexpr int kMinChunkRows = 64;
 
-// partial[blk][0][j] = sum over the block's rows of -sin(a_ij) t_i g_ij, [1][j] the same
-// without t_i; rows are split into gridDim.x equal chunks, each summed in row order.
-__global__ __launch_bounds__(kTimeGradThreads) void time_rows_grad(
+int chunk_blocks(int64_t n) {
+  const int64_t b = (n + kMinChunkRows - 1) / kMinChunkRows;
+  return static_cast<int>(b < 1 ? 1 : (b > kMaxChunkBlocks ? kMaxChunkBlocks : b));
+}
+
+struct RowChunk {
+  int64_t r0, r1;
+  int lane, phase;
+};
+
+__device__ __forceinline__ RowChunk row_chunk(int64_t n) {
+  const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+  RowChunk c;
+  c.r0 = static_cast<int64_t>(blockIdx.x) * per;
+  c.r1 = c.r0 + per < n ? c.r0 + per : n;
+  c.lane = threadIdx.x % kColLanes;
+  c.phase = threadIdx.x / kColLanes;
+  return c;
+}
+
+// out[b][col] = sum of the two phases' values v (phase 0 first); every thread of the
+// workgroup calls it with the same col0 (the column chunk), lanes past `cols` pass 0.
+template <int K>
+__device__ __forceinline__ void phase_sums(const float (&v)[K], const RowChunk& c, int64_t col,
+                                           int64_t cols, int64_t stride, float* out) {
+  __shared__ float red[kRowPhases][K][kColLanes];
+#pragma unroll
+  for (int k = 0; k < K; ++k) red[c.phase][k][c.lane] = v[k];
+  __syncthreads();
+  if (c.phase == 0 && col < cols) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) out[k * stride + col] = red[0][k][c.lane] + red[1][k][c.lane];
+  }
+  __syncthreads();
+}
+
+// partial[blk][0][j] = sum over the workgroup's rows of -sin(a_ij) t_i g_ij, [1][j] the same
+// without t_i.
+__global__ __launch_bounds__(kColBlock) void time_rows_grad(
     const float* ts, const float* mem_ts, int64_t n, const float* w, const float* b, int32_t dt,
     const float* g, int64_t ldg, float* partial) {
-  const int64_t per = (n + gridDim.x - 1) / gridDim.x;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * per;
-  const int64_t r1 = r0 + per < n ? r0 + per : n;
-  for (int j = threadIdx.x; j < dt; j += kTimeGradThreads) {
-    const float wj = w[j], bj = b[j];
-    float aw = 0.f, ab = 0.f;
-    for (int64_t i = r0; i < r1; ++i) {
-      const float t = mem_ts ? ts[i] - mem_ts[i] : ts[i];
-      const float d = -sin_time(t, wj, bj) * g[i * ldg + j];
-      aw = fmaf(d, t, aw);
-      ab += d;
+  const RowChunk c = row_chunk(n);
+  float* out = partial + static_cast<int64_t>(blockIdx.x) * 2 * dt;
+  for (int j0 = 0; j0 < dt; j0 += kColLanes) {
+    const int j = j0 + c.lane;
+    float v[2] = {0.f, 0.f};
+    if (j < dt) {
+      const float wj = w[j], bj = b[j];
+      for (int64_t i = c.r0 + c.phase; i < c.r1; i += kRowPhases) {
+        const float t = mem_ts ? ts[i] - mem_ts[i] : ts[i];
+        const float d = -sin_time(t, wj, bj) * g[i * ldg + j];
+        v[0] = fmaf(d, t, v[0]);
+        v[1] += d;
+      }
     }
-    partial[(static_cast<int64_t>(blockIdx.x) * 2 + 0) * dt + j] = aw;
-    partial[(static_cast<int64_t>(blockIdx.x) * 2 + 1) * dt + j] = ab;
+    phase_sums<2>(v, c, j, dt, dt, out);
   }
 }
 
-// dw[j] / db[j] = the partials summed in block order (one thread per output).
-__global__ __launch_bounds__(kEltBlock) void time_grad_finish(const float* partial, int blocks,
-                                                              int32_t dt, float* dw, float* db) {
-  const int c = blockIdx.x * kEltBlock + threadIdx.x;
-  if (c >= 2 * dt) return;
-  const int which = c / dt, j = c - which * dt;
+// Per output column c < cols: the sum over `blocks` partial rows [blocks][cols], one wave
+// per column (lane-strided, then the wave's fixed reduction tree). Column c goes to
+// out_a[c] when c < split, else out_b[c - split]; with dup > 0, columns c < dup also go to
+// out_b[c].
+__global__ __launch_bounds__(kRowBlock) void col_finish(const float* partial, int blocks,
+                                                        int64_t cols, int64_t split, float* out_a,
+                                                        float* out_b, int64_t dup) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * kRowWaves + threadIdx.x / kWave;
+  if (col >= cols) return;
+  const int lane = lane_id();
   float s = 0.f;
-  for (int k = 0; k < blocks; ++k) s += partial[(static_cast<int64_t>(k) * 2 + which) * dt + j];
-  (which == 0 ? dw : db)[j] = s;
+  for (int k = lane; k < blocks; k += kWave) s += partial[static_cast<int64_t>(k) * cols + col];
+  s = wave_sum(s);
+  if (lane == 0) {
+    if (col < split) {
+      out_a[col] = s;
+      if (col < dup) out_b[col] = s;
+    } else {
+      out_b[col - split + dup] = s;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -191,60 +248,68 @@ __global__ __launch_bounds__(kEltBlock) void time_grad_finish(const float* parti
 // gi = x W_ih^T + b_ih, gh = h W_hh^T + b_hh, gate blocks [r | z | n] (torch.nn.GRUCell):
 //   r = s(gi_r + gh_r), z = s(gi_z + gh_z), c = tanh(gi_n + r gh_n), h' = (1 - z) c + z h.
 // ws keeps [r | z | c | gh_n] per row for the backward.
-__global__ __launch_bounds__(kEltBlock) void gru_fwd(int64_t n, int32_t m, const float* gi,
+__global__ __launch_bounds__(kColBlock) void gru_fwd(int64_t n, int32_t m, const float* gi,
                                                      int64_t ldgi, const float* gh, int64_t ldgh,
                                                      const float* h, int64_t ldh, float* hy,
                                                      int64_t ldy, float* ws) {
-  const int64_t total = n * m;
-  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kEltBlock + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * kEltBlock) {
-    const int64_t i = idx / m;
-    const int j = static_cast<int>(idx - i * m);
-    const float* a = gi + i * ldgi;
-    const float* c = gh + i * ldgh;
-    const float r = sigmoid(a[j] + c[j]);
-    const float z = sigmoid(a[m + j] + c[m + j]);
-    const float hn = c[2 * m + j];
-    const float nc = tanhf(a[2 * m + j] + r * hn);
-    const float hv = h ? h[i * ldh + j] : 0.f;
-    hy[i * ldy + j] = (1.f - z) * nc + z * hv;
-    float* s = ws + i * 4 * m;
-    s[j] = r;
-    s[m + j] = z;
-    s[2 * m + j] = nc;
-    s[3 * m + j] = hn;
+  const RowChunk c = row_chunk(n);
+  for (int j = c.lane; j < m; j += kColLanes) {
+    for (int64_t i = c.r0 + c.phase; i < c.r1; i += kRowPhases) {
+      const float* a = gi + i * ldgi;
+      const float* q = gh + i * ldgh;
+      const float r = sigmoid(a[j] + q[j]);
+      const float z = sigmoid(a[m + j] + q[m + j]);
+      const float hn = q[2 * m + j];
+      const float nc = tanhf(a[2 * m + j] + r * hn);
+      const float hv = h ? h[i * ldh + j] : 0.f;
+      hy[i * ldy + j] = (1.f - z) * nc + z * hv;
+      float* s = ws + i * 4 * m;
+      s[j] = r;
+      s[m + j] = z;
+      s[2 * m + j] = nc;
+      s[3 * m + j] = hn;
+    }
   }
 }
 
 // dgi = [dr' | dz' | dn'], dgh = [dr' | dz' | dn' r] with dn' = dy (1 - z)(1 - c^2),
 // dz' = dy (h - c) z (1 - z), dr' = dn' gh_n r (1 - r); dh = dy z (the direct path; the
-// path through W_hh is the caller's product dgh W_hh).
-__global__ __launch_bounds__(kEltBlock) void gru_bwd(int64_t n, int32_t m, const float* dy,
+// path through W_hh is the caller's product dgh W_hh). With partial, the workgroup's column
+// sums of dr', dz', dn', dn' r go to partial[blk][4m] (the bias gradients).
+__global__ __launch_bounds__(kColBlock) void gru_bwd(int64_t n, int32_t m, const float* dy,
                                                      int64_t ldd, const float* ws, const float* h,
                                                      int64_t ldh, float* dgi, int64_t ldgi,
                                                      float* dgh, int64_t ldgh, float* dh,
-                                                     int64_t lddh) {
-  const int64_t total = n * m;
-  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kEltBlock + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * kEltBlock) {
-    const int64_t i = idx / m;
-    const int j = static_cast<int>(idx - i * m);
-    const float* s = ws + i * 4 * m;
-    const float r = s[j], z = s[m + j], nc = s[2 * m + j], hn = s[3 * m + j];
-    const float g = dy[i * ldd + j];
-    const float hv = h ? h[i * ldh + j] : 0.f;
-    const float dn = g * (1.f - z) * (1.f - nc * nc);
-    const float dz = g * (hv - nc) * z * (1.f - z);
-    const float dr = dn * hn * r * (1.f - r);
-    float* a = dgi + i * ldgi;
-    float* c = dgh + i * ldgh;
-    a[j] = dr;
-    a[m + j] = dz;
-    a[2 * m + j] = dn;
-    c[j] = dr;
-    c[m + j] = dz;
-    c[2 * m + j] = dn * r;
-    if (dh) dh[i * lddh + j] = g * z;
+                                                     int64_t lddh, float* partial) {
+  const RowChunk c = row_chunk(n);
+  for (int j0 = 0; j0 < m; j0 += kColLanes) {
+    const int j = j0 + c.lane;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j < m) {
+      for (int64_t i = c.r0 + c.phase; i < c.r1; i += kRowPhases) {
+        const float* s = ws + i * 4 * m;
+        const float r = s[j], z = s[m + j], nc = s[2 * m + j], hn = s[3 * m + j];
+        const float g = dy[i * ldd + j];
+        const float hv = h ? h[i * ldh + j] : 0.f;
+        const float dn = g * (1.f - z) * (1.f - nc * nc);
+        const float dz = g * (hv - nc) * z * (1.f - z);
+        const float dr = dn * hn * r * (1.f - r);
+        float* a = dgi + i * ldgi;
+        float* q = dgh + i * ldgh;
+        a[j] = dr;
+        a[m + j] = dz;
+        a[2 * m + j] = dn;
+        q[j] = dr;
+        q[m + j] = dz;
+        q[2 * m + j] = dn * r;
+        if (dh) dh[i * lddh + j] = g * z;
+        v[0] += dr;
+        v[1] += dz;
+        v[2] += dn;
+        v[3] += dn * r;
+      }
+    }
+    if (partial) phase_sums<4>(v, c, j, m, m, partial + static_cast<int64_t>(blockIdx.x) * 4 * m);
   }
 }
 
@@ -415,7 +480,7 @@ extern "C" int fa_time_rows_f32(int64_t n, const float* ts, const float* mem_ts,
 }
 
 extern "C" size_t fa_time_rows_grad_scratch_bytes(int32_t dt) {
-  return dt > 0 ? sizeof(float) * static_cast<size_t>(kTimeGradBlocks) * 2 * dt : 0;
+  return dt > 0 ? sizeof(float) * static_cast<size_t>(kMaxChunkBlocks) * 2 * dt : 0;
 }
 
 extern "C" int fa_time_rows_grad_f32(int64_t n, const float* ts, const float* mem_ts,
@@ -427,12 +492,12 @@ extern "C" int fa_time_rows_grad_f32(int64_t n, const float* ts, const float* me
   if (!w || !b || !dw || !db || (n > 0 && (!ts || !g))) return FA_EINVAL;
   if (!scratch || scratch_bytes < fa_time_rows_grad_scratch_bytes(dt)) return FA_ESCRATCH;
   float* partial = static_cast<float*>(scratch);
-  const int blocks = n > 0 ? (n < kTimeGradBlocks ? static_cast<int>(n) : kTimeGradBlocks) : 0;
+  const int blocks = n > 0 ? chunk_blocks(n) : 0;
   if (blocks > 0)
-    time_rows_grad<<<blocks, kTimeGradThreads, 0, stream>>>(ts, mem_ts, n, w, b, dt, g, ld_g,
-                                                            partial);
-  time_grad_finish<<<(2 * dt + kEltBlock - 1) / kEltBlock, kEltBlock, 0, stream>>>(partial, blocks,
-                                                                                 dt, dw, db);
+    time_rows_grad<<<blocks, kColBlock, 0, stream>>>(ts, mem_ts, n, w, b, dt, g, ld_g, partial);
+  const int64_t cols = 2 * static_cast<int64_t>(dt);
+  col_finish<<<static_cast<int>((cols + kRowWaves - 1) / kRowWaves), kRowBlock, 0, stream>>>(
+      partial, blocks, cols, dt, dw, db, 0);
   return launch_status();
 }
 
@@ -444,22 +509,42 @@ extern "C" int fa_gru_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_
     return FA_EINVAL;
   if (n == 0 || m == 0) return FA_OK;
   if (!gi || !gh || !hy || !workspace) return FA_EINVAL;
-  gru_fwd<<<elt_grid(n * m), kEltBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, h, ld_h, hy, ld_hy,
+  gru_fwd<<<chunk_blocks(n), kColBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, h, ld_h, hy, ld_hy,
                                                      workspace);
   return launch_status();
+}
+
+extern "C" size_t fa_gru_bwd_scratch_bytes(int64_t n, int32_t m) {
+  return n > 0 && m > 0 ? sizeof(float) * static_cast<size_t>(chunk_blocks(n)) * 4 * m : 0;
 }
 
 extern "C" int fa_gru_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy,
                               const float* workspace, const float* h, int64_t ld_h, float* dgi,
                               int64_t ld_dgi, float* dgh, int64_t ld_dgh, float* dh,
-                              int64_t ld_dh, hipStream_t stream) {
+                              int64_t ld_dh, float* db_ih, float* db_hh, void* scratch,
+                              size_t scratch_bytes, hipStream_t stream) {
   if (n < 0 || m < 0 || ld_dhy < m || ld_dgi < 3 * static_cast<int64_t>(m) ||
-      ld_dgh < 3 * static_cast<int64_t>(m) || (h && ld_h < m) || (dh && ld_dh < m))
+      ld_dgh < 3 * static_cast<int64_t>(m) || (h && ld_h < m) || (dh && ld_dh < m) ||
+      (!db_ih != !db_hh))
     return FA_EINVAL;
-  if (n == 0 || m == 0) return FA_OK;
-  if (!dhy || !workspace || !dgi || !dgh) return FA_EINVAL;
-  gru_bwd<<<elt_grid(n * m), kEltBlock, 0, stream>>>(n, m, dhy, ld_dhy, workspace, h, ld_h, dgi,
-                                                     ld_dgi, dgh, ld_dgh, dh, ld_dh);
+  if (m == 0) return FA_OK;
+  const bool sums = db_ih != nullptr;
+  if (sums && n > 0 && (!scratch || scratch_bytes < fa_gru_bwd_scratch_bytes(n, m)))
+    return FA_ESCRATCH;
+  if (n > 0) {
+    if (!dhy || !workspace || !dgi || !dgh) return FA_EINVAL;
+    gru_bwd<<<chunk_blocks(n), kColBlock, 0, stream>>>(n, m, dhy, ld_dhy, workspace, h, ld_h, dgi,
+                                                       ld_dgi, dgh, ld_dgh, dh, ld_dh,
+                                                       sums ? static_cast<float*>(scratch) : nullptr);
+  }
+  if (sums) {
+    // partial columns [dr' | dz' | dn' | dn' r]: db_ih = the first three, db_hh = the first
+    // two and the fourth
+    const int64_t cols = 4 * static_cast<int64_t>(m);
+    col_finish<<<static_cast<int>((cols + kRowWaves - 1) / kRowWaves), kRowBlock, 0, stream>>>(
+        static_cast<const float*>(scratch), n > 0 ? chunk_blocks(n) : 0, cols,
+        3 * static_cast<int64_t>(m), db_ih, db_hh, 2 * static_cast<int64_t>(m));
+  }
   return launch_status();
 }
 

@@ -27,9 +27,27 @@ import numpy as np
 import torch
 
 from . import fastAgg
+from . import tgat
 from .tgat import TimeEncode
 
 _TAG_LIMIT = 1 << 32
+
+
+def _timed(name, nbytes, fn, *args):
+    """fn(*args), timed (with its algorithmic bytes) when the kernel timer is set."""
+    return tgat._timed(name, nbytes, fn, *args)
+
+
+def _tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T b for a [n, p], b [n, q] over many rows (the cells' weight gradients): the per-head
+    weight-gradient kernel (split-bf16 matrix-core products, fixed-order sums) with a's
+    columns in G groups of at most 64 and every group reading the same rows of b."""
+    n, p = a.shape
+    q = b.shape[1]
+    G = next(g for g in range(1, p + 1) if p % g == 0 and p // g <= tgat.HEAD_KERNEL_MAX_J)
+    nb = 4 * (n * p + n * q + p * q)
+    y = b.unsqueeze(0).expand(G, n, q)
+    return _timed("cell_wgrad", nb, fastAgg.head_wgrad, a, y, G, False).reshape(p, q)
 
 
 def _as_device(x, device, dtype=None) -> torch.Tensor:
@@ -126,8 +144,11 @@ class MailBox:
         width = mail_w + self._time_dim()
         for b in mfg:
             ids = _ids(b.srcdata["ID"], self.device)
-            mem, mem_ts, rows, mail_ts = fastAgg.mail_gather(
-                ids, self.node_memory, self.node_memory_ts, self.mailbox, self.mailbox_ts, width)
+            n, m, slots = ids.numel(), self.node_memory.shape[1], self.mailbox.shape[1]
+            nbytes = n * (ids.element_size() + 2 * 4 * (m + 1 + mail_w + slots))
+            mem, mem_ts, rows, mail_ts = _timed(
+                "mail_gather", nbytes, fastAgg.mail_gather, ids, self.node_memory,
+                self.node_memory_ts, self.mailbox, self.mailbox_ts, width)
             b.srcdata["mem"] = mem
             b.srcdata["mem_ts"] = mem_ts
             b.srcdata["mem_input"] = rows[:, :mail_w]
@@ -161,7 +182,11 @@ class MailBox:
             mem = _as_device(memory[:k], self.device, torch.float32)
             t = _as_device(ts[:k], self.device, torch.float32)
             last, gen = self._tags()
-            fastAgg.memory_update_(ids, mem, t, self.node_memory, self.node_memory_ts, last, gen)
+            m = mem.shape[1]
+            # ids, rows and times read, one row and time written per distinct id (<= k)
+            nbytes = k * (ids.element_size() + 4 * m + 4 + 8) + k * (4 * m + 4)
+            _timed("memory_update", nbytes, fastAgg.memory_update_, ids, mem, t, self.node_memory,
+                   self.node_memory_ts, last, gen)
 
     def update_mailbox(self, nid, memory, root_nodes, ts, edge_feats, block, neg_samples=1):
         """memorys.py:105-182 for deliver_to 'self' with mail_combine 'last' (TGN, JODIE):
@@ -181,8 +206,13 @@ class MailBox:
             if self.dim_edge_feat > 0:
                 ef = _as_device(edge_feats[:n], self.device, torch.float32)
             last, gen = self._tags()
-            fastAgg.mailbox_update_(roots[:n].contiguous(), roots[n:2 * n].contiguous(), mem, ef, t,
-                                    self.mailbox, self.mailbox_ts, self.next_mail_pos, last, gen)
+            m, de = mem.shape[1], self.dim_edge_feat
+            # per write row: its id, two memory rows, the edge row, its time read; one mail,
+            # time and position written per distinct node (<= 2n)
+            nbytes = 2 * n * (roots.element_size() + 8 * m + 4 * de + 4 + 8) + 2 * n * (4 * (2 * m + de) + 12)
+            _timed("mailbox_update", nbytes, fastAgg.mailbox_update_, roots[:n].contiguous(),
+                   roots[n:2 * n].contiguous(), mem, ef, t, self.mailbox, self.mailbox_ts,
+                   self.next_mail_pos, last, gen)
 
     def update_next_mail_pos(self):
         """memorys.py:184-188."""
@@ -267,14 +297,16 @@ class _CellUpdate(torch.autograd.Function):
     @staticmethod
     def forward(ctx, rows, mail_w, ts, mem_ts, h, w_ih, w_hh, b_ih, b_hh, tw, tb, gru):
         dt = 0 if tw is None else tw.numel()
+        n, m = h.shape
         if dt:
-            fastAgg.time_rows_(rows, mail_w, ts, mem_ts, tw, tb)
+            _timed("time_rows", n * (8 + 4 * dt), fastAgg.time_rows_, rows, mail_w, ts, mem_ts, tw, tb)
         gi = torch.addmm(b_ih, rows, w_ih.t())
         gh = torch.addmm(b_hh, h, w_hh.t())
         if gru:
-            hy, saved = fastAgg.gru_fwd(gi, gh, h)
+            # gi, gh, h read; h' and the [r | z | c | gh_n] workspace written
+            hy, saved = _timed("cell_fwd", n * m * 48, fastAgg.gru_fwd, gi, gh, h)
         else:
-            hy = fastAgg.rnn_fwd(gi, gh)
+            hy = _timed("cell_fwd", n * m * 12, fastAgg.rnn_fwd, gi, gh)
             saved = hy
         ctx.gru, ctx.mail_w, ctx.dt = gru, mail_w, dt
         ctx.save_for_backward(rows, h, w_ih, w_hh, saved, ts, mem_ts, tw, tb)
@@ -285,19 +317,26 @@ class _CellUpdate(torch.autograd.Function):
         rows, h, w_ih, w_hh, saved, ts, mem_ts, tw, tb = ctx.saved_tensors
         dhy = dhy.contiguous()
         need_h = ctx.needs_input_grad[4]
+        n, m = dhy.shape
         if ctx.gru:
-            dgi, dgh, dh_direct = fastAgg.gru_bwd(dhy, saved, h, need_h)
+            # dhy, workspace, h read; dgi, dgh (and dh) written; the bias sums on the way
+            nb = n * m * (48 + (4 if need_h else 0))
+            dgi, dgh, dh_direct, d_bih, d_bhh = _timed("cell_bwd", nb, fastAgg.gru_bwd, dhy, saved,
+                                                       h, need_h)
         else:
-            dgi = dgh = fastAgg.rnn_bwd(dhy, saved)
+            dgi = dgh = _timed("cell_bwd", n * m * 12, fastAgg.rnn_bwd, dhy, saved)
+            d_bih = d_bhh = dgi.sum(0)
             dh_direct = None
-        d_wih = dgi.t().mm(rows) if ctx.needs_input_grad[5] else None
-        d_whh = dgh.t().mm(h) if ctx.needs_input_grad[6] else None
-        d_bih = dgi.sum(0) if ctx.needs_input_grad[7] else None
-        d_bhh = dgh.sum(0) if ctx.needs_input_grad[8] else None
+        d_wih = _tmm(dgi, rows) if ctx.needs_input_grad[5] else None
+        d_whh = _tmm(dgh, h) if ctx.needs_input_grad[6] else None
+        d_bih = d_bih if ctx.needs_input_grad[7] else None
+        d_bhh = d_bhh if ctx.needs_input_grad[8] else None
         d_tw = d_tb = None
         if ctx.dt and (ctx.needs_input_grad[9] or ctx.needs_input_grad[10]):
-            g_time = dgi.mm(w_ih[:, ctx.mail_w:])
-            d_tw, d_tb = fastAgg.time_rows_grad(g_time, ts, mem_ts, tw, tb)
+            # the time columns' gradient dgi W_ih[:, mail_w:]
+            g_time = tgat._rows_mm(dgi, w_ih[:, ctx.mail_w:].t(), "cell_reduce")
+            d_tw, d_tb = _timed("time_rows_grad", n * (8 + 4 * ctx.dt), fastAgg.time_rows_grad,
+                                g_time, ts, mem_ts, tw, tb)
             d_tw = d_tw.view_as(tw)
         dh = None
         if need_h:

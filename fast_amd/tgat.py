@@ -432,12 +432,12 @@ def _reduce_path(y, J: int) -> int:
     return int(fastAgg.head_reduce_supported(J, y.shape[2], y.stride(1), _rows16(y)))
 
 
-def _reduce(y, w):
+def _reduce(y, w, name: str = "head_reduce"):
     """[G, N, C] x [G, J, C]^T -> [N, G*J]; batched torch GEMMs where the head kernel does
-    not take the shape (heads wider than 64, or W[g] too large for LDS)."""
+    not take the shape (heads wider than 64, or W[g] too large for LDS). Timed as ``name``."""
     G, J, C = w.shape
     if _reduce_path(y, J):
-        return _timed("head_reduce", _head_bytes(y.shape[1], G, J, C, y.stride(0) != 0),
+        return _timed(name, _head_bytes(y.shape[1], G, J, C, y.stride(0) != 0),
                       fastAgg.head_reduce, y, w)
     z = torch.matmul(y, w.transpose(1, 2).contiguous())
     return z.transpose(0, 1).reshape(y.shape[1], G * J)
@@ -452,11 +452,12 @@ def _wgrad(x, y, groups: int, ones: bool):
     return _timed("head_wgrad", nb, fastAgg.head_wgrad, x, y, groups, ones)
 
 
-def _rows_mm(x, a):
+def _rows_mm(x, a, name: str = "head_reduce"):
     """x @ a^T for x [N, K] with many rows and a small a [M, K]: the per-head reduce kernel
     with every group reading the same rows of x (fastAgg.head_reduce with a zero group
     stride; M split into G groups of at most HEAD_KERNEL_MAX_J rows of a), used where its
-    split-bf16 form applies (rows of x in whole 16-byte chunks); torch's GEMM otherwise."""
+    split-bf16 form applies (rows of x in whole 16-byte chunks); torch's GEMM otherwise.
+    Timed as ``name``."""
     m, k = a.shape
     if x.dim() != 2 or x.stride(1) != 1 or k % 4 or x.stride(0) % 4 or x.data_ptr() % 16:
         return x @ a.t()
@@ -470,7 +471,7 @@ def _rows_mm(x, a):
     if g is None:
         return x @ a.t()
     a = a.contiguous()
-    return _reduce(x.unsqueeze(0).expand(g, x.shape[0], k), a.view(g, m // g, k))
+    return _reduce(x.unsqueeze(0).expand(g, x.shape[0], k), a.view(g, m // g, k), name)
 
 
 class _SplitRows(torch.autograd.Function):

@@ -413,10 +413,14 @@ int fa_gru_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const f
                    int64_t ld_gh, const float* h, int64_t ld_h, float* hy, int64_t ld_hy,
                    float* workspace, hipStream_t stream);
 /* dgi, dgh [n][3m] (the gradients of gi and gh) from dhy; dh (optional) = dhy z, the direct
- * path only (the caller adds dgh W_hh). */
+ * path only (the caller adds dgh W_hh). With db_ih and db_hh (both or neither) also the bias
+ * gradients db_ih = sum over rows of dgi, db_hh = the same of dgh (fixed-order sums,
+ * deterministic), through scratch of fa_gru_bwd_scratch_bytes(n, m). */
+size_t fa_gru_bwd_scratch_bytes(int64_t n, int32_t m);
 int fa_gru_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy, const float* workspace,
                    const float* h, int64_t ld_h, float* dgi, int64_t ld_dgi, float* dgh,
-                   int64_t ld_dgh, float* dh, int64_t ld_dh, hipStream_t stream);
+                   int64_t ld_dgh, float* dh, int64_t ld_dh, float* db_ih, float* db_hh,
+                   void* scratch, size_t scratch_bytes, hipStream_t stream);
 /* torch.nn.RNNCell with tanh (RNNMemeoryUpdater, memorys.py:332): hy = tanh(gi + gh); the
  * backward gives da = dhy (1 - hy^2), the gradient of both gi and gh. */
 int fa_rnn_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const float* gh,

@@ -605,8 +605,8 @@ constexpr int kPairDepth = FA_PAIR_DEPTH;
 
 template <int NS>
 struct PairCtx {
-  // byte offset of the lane's chunk in its node / edge row, or float offset of its chunk in
-  // the time-tile row (time, bias or zero chunk)
+  // byte offset of the lane's chunk in its node / edge row (0 for the other chunks, which
+  // read the row's first chunk and discard it)
   uint32_t off[NS];
   // float offset in the time-tile row of the lane's chunk: the chunk itself for time, bias
   // and padding chunks, the tile's zero chunk for row chunks (every lane reads one)
@@ -641,8 +641,8 @@ __device__ __forceinline__ void setup_pair(const TgatParams& P, PairCtx<NS>& L, 
     } else if (c == P.cn + P.ce + P.ct) {
       off = 4u * static_cast<uint32_t>(P.ct);
     }
-    L.off[k] = off;
     L.toff[k] = (L.is_node[k] || L.is_edge[k]) ? 4u * static_cast<uint32_t>(P.ct + 1) : off;
+    L.off[k] = (L.is_node[k] || L.is_edge[k]) ? off : 0u;
   }
 }
 
@@ -679,25 +679,31 @@ __device__ __forceinline__ float pick_flt(float v, int j) {
 // plain (non-const) global so that selecting between it and a table row keeps a global
 // pointer: a generic pointer would make the loads flat loads, which also count against the
 // LDS wait counter. Nothing writes it.
-__device__ __align__(16) float g_zero_chunk[4] = {0.f, 0.f, 0.f, 0.f};
+// A zero row as long as the longest row the pair kernels take (32 lanes x 4 slots of
+// 16-byte chunks), read in place of a missing row.
+constexpr int kPairZeroRowFloats = 4 * kHalf * 4;
+__device__ __align__(16) float g_zero_row[kPairZeroRowFloats];
 
 // Row chunks of one edge per half-wave, loaded as they are stored: float4 (BF = false) or
 // four bf16 words in x.x, x.y (BF = true, widened by pair_widen where the chunk is used).
-// Every lane issues its load with the whole wave active: a lane whose chunk is no row chunk,
-// or whose row is missing, reads the zero chunk. No branch and no conversion sits between a
-// load and the code that consumes it a step later, so the compiler can wait for exactly that
-// load (a conditional write into a register that still has a load in flight, or a branch
-// around the load, makes it wait for every load the wave has in flight).
+// Every lane issues its load with the whole wave active, from its node row or its edge row;
+// a missing row (or no edge table, or an edge past the staged ones) is the zero row, and a
+// lane whose chunk is no row chunk reads the first chunk of the edge row, which pair_widen
+// discards. No branch and no conversion sits between a load and the code that consumes it a
+// step later, so the compiler can wait for exactly that load (a conditional write into a
+// register that still has a load in flight, or a branch around the load, makes it wait for
+// every load the wave has in flight). Row strides are below 2^32 bytes, so each row address
+// is one 32 x 32 -> 64-bit multiply-add.
 template <int NS, bool BF>
 __device__ __forceinline__ void pair_load(const TgatParams& P, const PairCtx<NS>& L, uint32_t nid,
                                           uint32_t eid, bool ok, float4 (&x)[NS]) {
-  const bool nok = ok && nid != kNoRow, eok = ok && eid != kNoRow;
-  const char* nrow = P.node_tab + static_cast<uint64_t>(nok ? nid : 0u) * P.node_stride;
-  const char* erow = P.edge_tab + static_cast<uint64_t>(eok ? eid : 0u) * P.edge_stride;
-  const char* zero = reinterpret_cast<const char*>(g_zero_chunk);
+  const bool nok = ok && nid != kNoRow && P.dn > 0, eok = ok && eid != kNoRow && P.de > 0;
+  const char* zero = reinterpret_cast<const char*>(g_zero_row);
+  const char* nrow = nok ? P.node_tab + static_cast<uint64_t>(nid) * static_cast<uint32_t>(P.node_stride) : zero;
+  const char* erow = eok ? P.edge_tab + static_cast<uint64_t>(eid) * static_cast<uint32_t>(P.edge_stride) : zero;
 #pragma unroll
   for (int k = 0; k < NS; ++k) {
-    const char* a = (L.is_node[k] && nok) ? nrow + L.off[k] : ((L.is_edge[k] && eok) ? erow + L.off[k] : zero);
+    const char* a = (L.is_node[k] ? nrow : erow) + L.off[k];
     if constexpr (BF) {
       const uint2 w = *reinterpret_cast<const uint2*>(a);
       x[k] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), 0.f, 0.f);

@@ -1,5 +1,8 @@
-// Sum aggregation of source rows into destination rows: COO edge scatter (run-reduced)
-// and CSR segment sum.
+// Sum aggregation of source rows into destination rows: COO edge scatter and CSR segment
+// sum. The COO scatter checks on the device whether the output index is sorted; if it is,
+// every output row is the sum of one run of edges and is written with plain stores by the
+// run's owner (atomic-free, deterministic, every row of the output written); if not, the
+// output is zero-filled and runs of equal consecutive indices are added with atomics.
 //
 // Rows are read through buffer descriptors sized to the row (a row id out of range has an
 // empty descriptor and reads as zeros), as float4 chunks when every row start is 16-byte
@@ -153,7 +156,8 @@ __device__ __forceinline__ void flush_run(const AggParams& P, int64_t row, const
 // run of at most 64 edges reaches its output row as at most two partial sums (whose sum does
 // not depend on their order).
 template <int NS, bool VEC>
-__global__ __launch_bounds__(kBlock) void edge_scatter_sum(AggParams P) {
+__global__ __launch_bounds__(kBlock) void edge_scatter_sum(AggParams P, const int* flag) {
+  if (flag[0] == 0) return;  // sorted: run_scatter wrote the output
   __shared__ __attribute__((aligned(16))) float stage_all[kWavesPerBlock][4 * kWave * NS];
   float* stage = stage_all[threadIdx.x / kWave];
   const int lane = lane_id();
@@ -198,6 +202,174 @@ __global__ __launch_bounds__(kBlock) void edge_scatter_sum(AggParams P) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Sorted output index: run owners, plain stores
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void flag_clear(int* flag) {
+  if (threadIdx.x == 0) flag[0] = 0;
+}
+
+
+// The edges taken: all, or the range the CSR segments cover (indptr[0] .. indptr[n_seg]).
+__device__ __forceinline__ void edge_range(const AggParams& P, int64_t& lo, int64_t& hi) {
+  lo = 0;
+  hi = P.n_edges;
+  if (P.indptr) {
+    lo = P.indptr[0] < 0 ? 0 : P.indptr[0];
+    hi = P.indptr[P.n_seg] < hi ? P.indptr[P.n_seg] : hi;
+    hi = hi < lo ? lo : hi;
+  }
+}
+
+// flag |= 1 when dst[e] < dst[e-1] for some lo < e < hi.
+__global__ __launch_bounds__(kBlock) void check_sorted(AggParams P, int* flag) {
+  int64_t lo, hi;
+  edge_range(P, lo, hi);
+  bool bad = false;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t e = lo + 1 + static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < hi;
+       e += stride)
+    bad |= P.dst[e] < P.dst[e - 1];
+  const uint64_t any = __ballot(bad);
+  if (any && lane_id() == __builtin_ctzll(any)) atomicOr(flag, 1);
+}
+
+// The value of lane `src` (any lane, per lane).
+__device__ __forceinline__ int64_t lane_i64_from(int64_t v, int src) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v & 0xffffffff)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v >> 32)));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Zero rows [r0, r1) of out (clamped to [0, n_out)) by a half-wave.
+template <int NS, bool VEC>
+__device__ __forceinline__ void zero_rows(const AggParams& P, int64_t r0, int64_t r1, int hl) {
+  r0 = r0 < 0 ? 0 : r0;
+  r1 = r1 > P.n_out ? P.n_out : r1;
+  for (int64_t r = r0; r < r1; ++r) {
+    const rsrc_t orow = row_rsrc(P.out + r * P.ldo, 4u * static_cast<uint32_t>(P.dim));
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int c = hl + k * kHalf;
+      if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), f4_zero());
+    }
+  }
+}
+
+constexpr int64_t kNoIndex = INT64_MIN;   // "no previous index"
+constexpr int kRunRows = 4;               // rows in flight per half-wave
+
+// One wave per 64 consecutive edges of [lo, hi); the wave owns the runs (maximal ranges of
+// equal output index) that start in its edges and takes them two at a time, one per
+// half-wave. A run's owner sums its rows (lane hl holds chunks hl, hl+32, ...; the run's
+// source ids loaded 32 at a time, four rows in flight), stores the output row, and zeroes
+// the output rows between the previous run's index and its own. The rows before the first
+// index and after the last are zeroed by the whole grid. Indices outside [0, n_out) are not
+// written. With an unsorted index (flag set) the kernel zero-fills the output instead, for
+// the atomic kernel that follows.
+template <int NS, bool VEC>
+__global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* flag) {
+  const int lane = lane_id();
+  const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
+  const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+  int64_t lo, hi;
+  edge_range(P, lo, hi);
+  if (flag[0] != 0 || hi <= lo) {  // unsorted, or no edge: zero-fill by half-waves
+    for (int64_t r = w0 * 2 + half; r < P.n_out; r += waves * 2) zero_rows<NS, VEC>(P, r, r + 1, hl);
+    return;
+  }
+  {  // the rows before the first index and after the last, by every half-wave of the grid
+    const int64_t first = P.dst[lo], last = P.dst[hi - 1];
+    const int64_t head = first < 0 ? 0 : (first > P.n_out ? P.n_out : first);
+    const int64_t tail = last < 0 ? 0 : (last + 1 > P.n_out ? P.n_out : last + 1);
+    for (int64_t r = w0 * 2 + half; r < head; r += waves * 2) zero_rows<NS, VEC>(P, r, r + 1, hl);
+    for (int64_t r = tail + w0 * 2 + half; r < P.n_out; r += waves * 2)
+      zero_rows<NS, VEC>(P, r, r + 1, hl);
+  }
+  for (int64_t w = w0; lo + w * kWave < hi; w += waves) {
+    const int64_t e0 = lo + w * kWave;
+    const int cnt = static_cast<int>(hi - e0 < kWave ? hi - e0 : kWave);
+    const int64_t my = P.dst[e0 + (lane < cnt ? lane : cnt - 1)];
+    const int64_t prev_tile = e0 > lo ? P.dst[e0 - 1] : kNoIndex;
+    const int64_t up = lane_i64_from(my, lane > 0 ? lane - 1 : 0);
+    const bool start = lane < cnt && (lane == 0 ? (e0 == lo || my != prev_tile) : my != up);
+    uint64_t m = __ballot(start);
+    while (m) {
+      // two runs: bit b0 for the first half-wave, b1 (if any) for the second
+      const int b0 = __builtin_ctzll(m);
+      m &= m - 1;
+      const int b1 = m ? __builtin_ctzll(m) : -1;
+      if (m) m &= m - 1;
+      const int b = half ? b1 : b0;
+      const int nb = half ? (m ? __builtin_ctzll(m) : -1) : b1;  // the next run's start bit
+      // lane reads with the whole wave active (a permute from an inactive lane reads zero)
+      const int bs = b < 0 ? 0 : b;
+      const int64_t row = lane_i64_from(my, bs);
+      const int64_t before_v = lane_i64_from(my, bs > 0 ? bs - 1 : 0);
+      if (b < 0) continue;
+      const int64_t before = b == 0 ? prev_tile : before_v;
+      int64_t end;
+      if (nb >= 0) {
+        end = e0 + nb;
+      } else {  // the tile's last run: scan past the tile for its end
+        end = e0 + cnt;
+        while (end < hi) {
+          const int64_t e = end + hl;
+          const int64_t v = e < hi ? P.dst[e] : row + 1;  // past the end: a different index
+          const uint32_t diff = static_cast<uint32_t>(__ballot(v != row) >> (half * kHalf));
+          if (diff) {
+            end += __builtin_ctz(diff);
+            break;
+          }
+          end += kHalf;
+        }
+        end = end > hi ? hi : end;
+      }
+      if (before != kNoIndex) zero_rows<NS, VEC>(P, before + 1, row, hl);  // the gap below
+      if (row >= 0 && row < P.n_out) {
+        float4 acc[NS];
+#pragma unroll
+        for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
+        for (int64_t eb = e0 + b; eb < end; eb += kHalf) {
+          const int n = static_cast<int>(end - eb < kHalf ? end - eb : kHalf);
+          const int64_t ids = P.src[eb + (hl < n ? hl : 0)];  // this half's next 32 source ids
+          for (int j = 0; j < n; j += kRunRows) {
+            float4 r[kRunRows][NS];
+#pragma unroll
+            for (int q = 0; q < kRunRows; ++q) {
+              // permutes stay inside this half-wave, whose lanes are all active
+              const int64_t sidx = lane_i64_from(ids, half * kHalf + (j + q < n ? j + q : 0));
+              const bool ok = j + q < n && sidx >= 0 && sidx < P.n_x;
+              const rsrc_t rr = row_rsrc(P.x + (ok ? sidx : 0) * P.ldx, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+#pragma unroll
+              for (int k = 0; k < NS; ++k) {
+                const int c = hl + k * kHalf;
+                r[q][k] = c < P.chunks ? load_chunk<VEC>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
+              }
+            }
+#pragma unroll
+            for (int q = 0; q < kRunRows; ++q)
+#pragma unroll
+              for (int k = 0; k < NS; ++k) {
+                acc[k].x += r[q][k].x;
+                acc[k].y += r[q][k].y;
+                acc[k].z += r[q][k].z;
+                acc[k].w += r[q][k].w;
+              }
+          }
+        }
+        const rsrc_t orow = row_rsrc(P.out + row * P.ldo, 4u * static_cast<uint32_t>(P.dim));
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+          const int c = hl + k * kHalf;
+          if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
+        }
+      }
+    }
+  }
+}
+
 constexpr int kAggMaxBlocks = 4096;
 
 int agg_grid(int64_t waves) {
@@ -215,29 +387,57 @@ bool vec_ok(const AggParams& P) {
 
 using namespace fa;
 
+extern "C" size_t fa_edge_scatter_sum_scratch_bytes(void) { return 16; }
+
 extern "C" int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_edges,
                                        const int32_t* indptr, int64_t n_seg, const float* x,
                                        int64_t ldx, int64_t n_x, int32_t dim, float* out,
-                                       int64_t ldo, int64_t n_out, hipStream_t stream) {
+                                       int64_t ldo, int64_t n_out, void* scratch,
+                                       size_t scratch_bytes, hipStream_t stream) {
   if (n_edges < 0 || n_x < 0 || dim < 0 || n_out < 0 || n_seg < 0) return FA_EINVAL;
-  if (n_edges == 0 || dim == 0 || n_out == 0) return FA_OK;
-  if (!dst || !src || !out || (n_x > 0 && !x) || ldx < dim || ldo < dim) return FA_EINVAL;
+  if (dim == 0 || n_out == 0) return FA_OK;
+  if (!out || ldo < dim || (n_edges > 0 && (!dst || !src || (n_x > 0 && !x) || ldx < dim)))
+    return FA_EINVAL;
   if (dim > 4 * kWave * kMaxSlots) return FA_EUNSUPPORTED;
+  if (!scratch || scratch_bytes < fa_edge_scatter_sum_scratch_bytes()) return FA_ESCRATCH;
+  int* flag = static_cast<int*>(scratch);
   AggParams P{dst, src, n_edges, indptr, n_seg, x, ldx, n_x, dim, static_cast<int>(ceil_div(dim, 4)),
               out, ldo, n_out};
-  const dim3 grid(agg_grid(ceil_div(n_edges, kWave)));
+  const dim3 grid(agg_grid(ceil_div(n_edges > 0 ? n_edges : 1, kWave)));
   const int ns = static_cast<int>(ceil_div(P.chunks, kWave));
+  const int ns_half = static_cast<int>(ceil_div(P.chunks, kHalf));
   const bool vec = vec_ok(P);
-#define FA_AGG_LAUNCH(NSV)                                                                      \
-  if (vec) hipLaunchKernelGGL((edge_scatter_sum<NSV, true>), grid, dim3(kBlock), 0, stream, P); \
-  else hipLaunchKernelGGL((edge_scatter_sum<NSV, false>), grid, dim3(kBlock), 0, stream, P);
-  switch (ns) {
-    case 1: FA_AGG_LAUNCH(1) break;
-    case 2: FA_AGG_LAUNCH(2) break;
-    case 3: FA_AGG_LAUNCH(3) break;
-    default: FA_AGG_LAUNCH(4) break;
+  hipLaunchKernelGGL(flag_clear, dim3(1), dim3(64), 0, stream, flag);
+  if (n_edges > 1)
+    hipLaunchKernelGGL(check_sorted, grid, dim3(kBlock), 0, stream, P, flag);
+#define FA_RUN_LAUNCH(NSV)                                                                       \
+  if (vec) hipLaunchKernelGGL((run_scatter<NSV, true>), grid, dim3(kBlock), 0, stream, P,        \
+                              static_cast<const int*>(flag));                                    \
+  else hipLaunchKernelGGL((run_scatter<NSV, false>), grid, dim3(kBlock), 0, stream, P,           \
+                          static_cast<const int*>(flag));
+  switch (ns_half) {
+    case 1: FA_RUN_LAUNCH(1) break;
+    case 2: FA_RUN_LAUNCH(2) break;
+    case 3: FA_RUN_LAUNCH(3) break;
+    case 4: FA_RUN_LAUNCH(4) break;
+    case 5: case 6: FA_RUN_LAUNCH(6) break;
+    default: FA_RUN_LAUNCH(8) break;
   }
+#undef FA_RUN_LAUNCH
+  if (n_edges > 0) {
+#define FA_AGG_LAUNCH(NSV)                                                                       \
+    if (vec) hipLaunchKernelGGL((edge_scatter_sum<NSV, true>), grid, dim3(kBlock), 0, stream, P,  \
+                                static_cast<const int*>(flag));                                  \
+    else hipLaunchKernelGGL((edge_scatter_sum<NSV, false>), grid, dim3(kBlock), 0, stream, P,     \
+                            static_cast<const int*>(flag));
+    switch (ns) {
+      case 1: FA_AGG_LAUNCH(1) break;
+      case 2: FA_AGG_LAUNCH(2) break;
+      case 3: FA_AGG_LAUNCH(3) break;
+      default: FA_AGG_LAUNCH(4) break;
+    }
 #undef FA_AGG_LAUNCH
+  }
   return launch_status();
 }
 

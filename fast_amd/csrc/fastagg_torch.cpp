@@ -66,7 +66,8 @@ at::Tensor softmax_fwd_impl(const at::Tensor& indptr, const at::Tensor& x, int64
   TORCH_CHECK(heads >= 0 && heads <= x.size(1), op, ": num_heads (", heads,
               ") must lie in [0, input_feat.size(1)=", x.size(1), "]");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
-  auto y = at::zeros({x.size(0), heads}, x.options());
+  // every entry is written: softmax values in the segments, zeros outside them
+  auto y = at::empty({x.size(0), heads}, x.options());
   const int64_t S = num_segments(indptr);
   int st;
   if (x.scalar_type() == at::kFloat)
@@ -94,7 +95,10 @@ at::Tensor softmax_bwd_impl(const at::Tensor& indptr, const at::Tensor& dy, cons
   TORCH_CHECK(heads >= 0 && heads <= dy.size(1), op, ": num_heads (", heads,
               ") must lie in [0, d_output.size(1)=", dy.size(1), "]");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(dy.device());
-  auto dx = at::zeros({dy.size(0), dy.size(1)}, dy.options());
+  // the kernels write the first num_heads columns of every row (zeros outside the
+  // segments); wider outputs keep zeros in the other columns
+  auto dx = heads == dy.size(1) ? at::empty({dy.size(0), dy.size(1)}, dy.options())
+                                : at::zeros({dy.size(0), dy.size(1)}, dy.options());
   const int64_t S = num_segments(indptr);
   int st;
   if (dy.scalar_type() == at::kFloat)
@@ -234,6 +238,20 @@ void check_edge_pair(const at::Tensor& a, const at::Tensor& b, const at::Tensor&
   CHECK_SAME_DEVICE(b, x);
 }
 
+// out [n_out, x.size(1)] = the scatter sum of x rows src[e] into rows dst[e] (every row written).
+at::Tensor scatter_sum(const at::Tensor& dst, const at::Tensor& src, const int32_t* indptr,
+                       int64_t n_seg, const at::Tensor& x, int64_t n_out, const char* op) {
+  auto out = at::empty({n_out, x.size(1)}, x.options());
+  auto scratch = at::empty({static_cast<int64_t>(fa_edge_scatter_sum_scratch_bytes())},
+                           x.options().dtype(at::kByte));
+  const int st = fa_edge_scatter_sum_f32(
+      dst.data_ptr<int64_t>(), src.data_ptr<int64_t>(), dst.numel(), indptr, n_seg,
+      x.data_ptr<float>(), x.size(1), x.size(0), static_cast<int32_t>(x.size(1)),
+      out.data_ptr<float>(), out.size(1), n_out, scratch.data_ptr(), scratch.numel(), stream_of(x));
+  check_status(st, op);
+  return out;
+}
+
 // forward_tgat (operators.cpp:146-165): out[src_edges[e]] += input_feat[dst_edges[e]]
 // for every edge (the reference argument names: src_edges holds destination ids).
 std::vector<at::Tensor> forward_tgat(at::Tensor src_edges, at::Tensor dst_edges,
@@ -247,14 +265,7 @@ std::vector<at::Tensor> forward_tgat(at::Tensor src_edges, at::Tensor dst_edges,
   check_edge_pair(src_edges, dst_edges, input_feat);
   TORCH_CHECK(dst_num >= 0, "dst_num must be >= 0");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(input_feat.device());
-  auto out = at::zeros({dst_num, input_feat.size(1)}, input_feat.options());
-  const int st = fa_edge_scatter_sum_f32(
-      src_edges.data_ptr<int64_t>(), dst_edges.data_ptr<int64_t>(), src_edges.numel(), nullptr, 0,
-      input_feat.data_ptr<float>(), input_feat.size(1), input_feat.size(0),
-      static_cast<int32_t>(input_feat.size(1)), out.data_ptr<float>(), out.size(1), dst_num,
-      stream_of(input_feat));
-  check_status(st, "forward_tgat");
-  return {out};
+  return {scatter_sum(src_edges, dst_edges, nullptr, 0, input_feat, dst_num, "forward_tgat")};
 }
 
 // backward_tgat (operators.cpp:364-384): d_out[dst_edges[e]] += d_input[src_edges[e]].
@@ -268,14 +279,7 @@ std::vector<at::Tensor> backward_tgat(at::Tensor src_edges, at::Tensor dst_edges
   check_edge_pair(src_edges, dst_edges, d_input);
   TORCH_CHECK(src_num >= 0, "src_num must be >= 0");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(d_input.device());
-  auto out = at::zeros({src_num, d_input.size(1)}, d_input.options());
-  const int st = fa_edge_scatter_sum_f32(
-      dst_edges.data_ptr<int64_t>(), src_edges.data_ptr<int64_t>(), src_edges.numel(), nullptr, 0,
-      d_input.data_ptr<float>(), d_input.size(1), d_input.size(0),
-      static_cast<int32_t>(d_input.size(1)), out.data_ptr<float>(), out.size(1), src_num,
-      stream_of(d_input));
-  check_status(st, "backward_tgat");
-  return {out};
+  return {scatter_sum(dst_edges, src_edges, nullptr, 0, d_input, src_num, "backward_tgat")};
 }
 
 // forward_tgat_shd (operators.cpp:120-145): CSR segment sum written to the segment's dst.
@@ -323,15 +327,9 @@ std::vector<at::Tensor> backward_tgat_shd(at::Tensor indptr, at::Tensor indices,
   check_edge_pair(dst_edges, src_edges, d_input);
   TORCH_CHECK(src_nodes >= 0, "src_nodes must be >= 0");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(d_input.device());
-  auto out = at::zeros({src_nodes, d_input.size(1)}, d_input.options());
   const int64_t S = num_segments(indptr);
-  const int st = fa_edge_scatter_sum_f32(
-      src_edges.data_ptr<int64_t>(), dst_edges.data_ptr<int64_t>(), src_edges.numel(),
-      S > 0 ? indptr.data_ptr<int32_t>() : nullptr, S, d_input.data_ptr<float>(),
-      d_input.size(1), d_input.size(0), static_cast<int32_t>(d_input.size(1)),
-      out.data_ptr<float>(), out.size(1), src_nodes, stream_of(d_input));
-  check_status(st, "backward_tgat_shd");
-  return {out};
+  return {scatter_sum(src_edges, dst_edges, S > 0 ? indptr.data_ptr<int32_t>() : nullptr, S,
+                      d_input, src_nodes, "backward_tgat_shd")};
 }
 
 // ----------------------------------------------------------------------------------

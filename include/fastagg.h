@@ -79,9 +79,12 @@ int fa_rowptr_from_sorted_dst_i64(const int64_t* dst, int64_t n_edges, int64_t n
 /* For each segment s < n_seg (edges indptr[s]..indptr[s+1]) and head h < heads:
  *   mode 0 (reciprocal): y = exp(x - max) * (1 / sum)   forward_edge_softmax
  *   mode 1 (division)  : y = exp(x - max) / sum         forward_csr_edge_softmax
- * with max seeded at -1e38, sum over the segment in edge order. Entries outside every
- * segment are not written. Replaces forward_edge_softmax_cuda (edge_softmax.cu:55-78,
- * 255-293) and forward_csr_edge_softmax_cuda (edge_softmax.cu:178-206, 450-518). */
+ * with max seeded at -1e38. Entries of edges outside every segment are set to zero (the
+ * reference's zero-initialised output). float32 rows of exactly `heads` values with heads in
+ * {1, 2, 4, 8, 16} run one 16-lane row per segment (coalesced, max and sum combined in a
+ * tree); other shapes and float64 one thread per (segment, head), summing in edge order.
+ * Replaces forward_edge_softmax_cuda (edge_softmax.cu:55-78, 255-293) and
+ * forward_csr_edge_softmax_cuda (edge_softmax.cu:178-206, 450-518). */
 int fa_edge_softmax_fwd_f32(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
                             const float* x, int64_t ldx, int32_t heads, float* y, int64_t ldy,
                             int32_t mode, hipStream_t stream);
@@ -89,7 +92,8 @@ int fa_edge_softmax_fwd_f64(const int32_t* indptr, int64_t n_seg, int64_t n_edge
                             const double* x, int64_t ldx, int32_t heads, double* y,
                             int64_t ldy, int32_t mode, hipStream_t stream);
 
-/* dx = y * (dy - sum_segment(y * dy)) per segment and head h < heads.
+/* dx = y * (dy - sum_segment(y * dy)) per segment and head h < heads; the first `heads`
+ * values of rows outside every segment are set to zero (same kernels as the forward).
  * Replaces backward_edge_softmax_cuda (edge_softmax.cu:79-106, 295-329) and
  * backward_csr_edge_softmax_cuda (edge_softmax.cu:207-235, 520-577). */
 int fa_edge_softmax_bwd_f32(const int32_t* indptr, int64_t n_seg, int64_t n_edges,
@@ -116,20 +120,23 @@ int fa_group_softmax_bwd_f32(const int64_t* batch_ptr, int64_t n_batch, const in
  * Sum aggregation over edges (drop-in kernels of aggregate_*_kernel.cu)
  * ------------------------------------------------------------------------------- */
 
-/* out[dst[e], :] += x[src[e], :] for e < n_edges (COO, any order; ids outside
- * [0, n_out) / [0, n_x) are skipped). When indptr is not NULL only the edges
- * indptr[0] <= e < indptr[n_seg] are used. out must be zeroed by the caller. Runs of equal
- * consecutive dst are reduced in registers, so for dst-sorted input the output row of a
- * run of at most 64 edges receives at most two partial sums (deterministic).
- * dim <= 1024 (FA_EUNSUPPORTED beyond).
- * Replaces computation_aware_forward_tgat_cuda (aggregate_acc_kernel.cu:36-94), with
- * every edge covered. Also the backward of forward_tgat / forward_tgat_shd with the
- * roles of dst and src swapped (aggregate_acc_kernel.cu:97-161,
- * aggregate_shd_kernel.cu:212-368). */
+/* out[r, :] = sum of x[src[e], :] over the edges e with dst[e] = r, for e < n_edges (COO, any
+ * order; ids outside [0, n_out) / [0, n_x) are skipped; x rows outside [0, n_x) read as zero).
+ * When indptr is not NULL only the edges indptr[0] <= e < indptr[n_seg] are used. Every row
+ * of out (dim values) is written: rows no edge reaches get zeros. The kernels check on the
+ * device whether dst is sorted (non-decreasing): if so, each output row is the sum of one run
+ * of edges, summed in edge order by the run's owner and written with plain stores
+ * (deterministic, no atomics); otherwise out is zero-filled and runs of equal consecutive dst
+ * are added with atomics (the result may then depend on the order of the additions).
+ * dim <= 1024 (FA_EUNSUPPORTED beyond). scratch: fa_edge_scatter_sum_scratch_bytes().
+ * Replaces computation_aware_forward_tgat_cuda (aggregate_acc_kernel.cu:36-94), with every
+ * edge covered. Also the backward of forward_tgat / forward_tgat_shd with the roles of dst
+ * and src swapped (aggregate_acc_kernel.cu:97-161, aggregate_shd_kernel.cu:212-368). */
+size_t fa_edge_scatter_sum_scratch_bytes(void);
 int fa_edge_scatter_sum_f32(const int64_t* dst, const int64_t* src, int64_t n_edges,
                             const int32_t* indptr, int64_t n_seg, const float* x, int64_t ldx,
                             int64_t n_x, int32_t dim, float* out, int64_t ldo, int64_t n_out,
-                            hipStream_t stream);
+                            void* scratch, size_t scratch_bytes, hipStream_t stream);
 
 /* CSR segment sum: for segment s, out[dst[indptr[s]], :] = sum_e x[src[e], :] over the
  * segment (edges of a segment share one destination). Rows of out outside every segment

@@ -219,8 +219,10 @@ def test_softmax_rejects_bad_arguments(lib):
     assert call(4, 2, 2, 2) == FA_EINVAL    # unknown mode
     assert call(4, 2, 1, 0) == FA_EINVAL    # leading dimension below the head count
     assert call(-1, 2, 2, 0) == FA_EINVAL
-    assert call(0, 2, 2, 0) == FA_OK        # nothing to do: returns before any launch
-    assert call(4, 0, 2, 0) == FA_OK
+    assert call(4, 0, 2, 0) == FA_OK        # nothing to do: returns before any launch
+    # no edges: nothing to write (with edges but no segment the output is zero-filled, a launch)
+    assert f(P, ctypes.c_int64(0), ctypes.c_int64(0), P, ctypes.c_int64(2), ctypes.c_int32(2), P,
+             ctypes.c_int64(2), ctypes.c_int32(0), None) == FA_OK
 
 
 def test_memory_entry_points_reject_bad_arguments(lib):

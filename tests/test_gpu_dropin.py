@@ -200,6 +200,70 @@ def test_tgat_aggregation_unsorted(fa, dev):
     assert_rel(out, C.edge_scatter_sum(dst, src, x, N), FP32_TOL, "unsorted forward_tgat")
 
 
+@pytest.mark.parametrize("case", ["gaps", "out_of_range", "one_long_run", "tile_sorted_only",
+                                  "no_edges", "csr_subrange"])
+@pytest.mark.parametrize("dim", [7, 100])
+def test_tgat_aggregation_sorted_edge_cases(fa, dev, case, dim):
+    """The run-owner path of the scatter (sorted output index, plain stores, every output row
+    written) and its switch to the atomic path: rows before, between and after the runs come
+    out zero, indices outside [0, n_out) are skipped, a run spanning many 64-edge tiles is one
+    sum, an index sorted inside every tile but not across tiles takes the atomic path; against
+    the C restatement (which starts from zeros)."""
+    rng = np.random.default_rng(dim + len(case))
+    n_out, indptr = 40, None
+    if case == "gaps":
+        dst = np.repeat([3, 4, 9, 30], [2, 70, 1, 5])
+    elif case == "out_of_range":
+        dst = np.array([-3, -3, -1, 0, 0, 5, 5, 5, 39, 40, 40, 41, 100])
+    elif case == "one_long_run":
+        dst = np.full(1000, 17)
+    elif case == "tile_sorted_only":
+        dst = np.concatenate([np.repeat([20, 21], 32), np.repeat([2, 3], 32), np.full(64, 20)])
+    elif case == "no_edges":
+        dst = np.zeros(0)
+    else:
+        dst = np.repeat(np.arange(0, 40, 3), 7)
+        indptr = np.array([5, 20, 20, 61], dtype=np.int32)   # edges 5..60 only
+    dst = dst.astype(np.int64)
+    E = dst.size
+    src = rng.integers(0, 300, size=E).astype(np.int64)
+    x = rng.standard_normal((300, dim)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    ref = C.edge_scatter_sum(dst, src, x, n_out, indptr)
+    if indptr is None:
+        out = fa.forward_tgat(t(dst), t(src), t(x), n_out, 8, 128)[0]
+        what = f"forward_tgat {case}"
+    else:
+        # backward_tgat_shd(indptr, indices, dst_edges, src_edges, d_input, src_nodes, ...)
+        # scatters d_input[dst_edges[e]] into rows src_edges[e] over the CSR-covered edges
+        out = fa.backward_tgat_shd(t(indptr), t(indptr), t(src), t(dst), t(x), n_out, 8, 32)[0]
+        what = f"backward_tgat_shd {case}"
+    assert_rel(out, ref, FP32_TOL, what)
+    hit = np.zeros(n_out, bool)
+    lo, hi = (0, E) if indptr is None else (int(indptr[0]), int(indptr[-1]))
+    hit[[d for d in dst[lo:hi] if 0 <= d < n_out]] = True
+    assert torch.count_nonzero(out[torch.from_numpy(~hit).to(dev)]) == 0, "rows without edges"
+
+
+def test_edge_softmax_rows_outside_segments_are_zero(fa, dev):
+    """Edges before the first segment and after the last one get zeros (the outputs are not
+    zero-filled beforehand); both the row kernels (2 heads) and the per-thread kernel
+    (3 heads) are covered, forward and backward."""
+    indptr = np.array([3, 5, 5, 9], dtype=np.int32)
+    for heads in (2, 3):
+        x = np.random.default_rng(heads).standard_normal((12, heads)).astype(np.float32)
+        dy = np.random.default_rng(heads + 1).standard_normal((12, heads)).astype(np.float32)
+        ti = torch.from_numpy(indptr).to(dev)
+        for _ in range(2):   # a second call reuses freed memory that is not zero
+            y = fa.forward_edge_softmax(ti, ti, torch.from_numpy(x).to(dev), 512, heads)[0]
+            dx = fa.backward_edge_softmax(ti, ti, torch.from_numpy(dy).to(dev), y, 512, heads)[0]
+        y_ref = C.edge_softmax_fwd(indptr, x, heads, 0)
+        assert_rel(y, y_ref, 1e-6, f"forward, {heads} heads")
+        assert not y[:3].any() and not y[9:].any()
+        assert_rel(dx, C.edge_softmax_bwd(indptr, dy, y.cpu().numpy(), heads), 1e-6, "backward")
+        assert not dx[:3].any() and not dx[9:].any()
+
+
 # ---------------------------------------------------------------------------------------
 # fused LeakyReLU + softmax + dropout + aggregation
 # ---------------------------------------------------------------------------------------

@@ -1235,7 +1235,10 @@ __device__ __forceinline__ float4 pick_f4(const float4& v, int j) {
 }
 
 // Waves per SIMD the register budget is sized for (three leave 168 registers for the widest).
-constexpr int pair_bwd_min_waves(int H, int NS) { return H * NS >= 6 ? 3 : 4; }
+#ifndef FA_PAIR_BWD_WAVES
+#define FA_PAIR_BWD_WAVES 3
+#endif
+constexpr int pair_bwd_min_waves(int H, int NS) { return H * NS >= 6 ? FA_PAIR_BWD_WAVES : 4; }
 
 template <int H, int NS, bool BF>
 __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pair(TgatParams P) {

@@ -45,6 +45,11 @@ __device__ __forceinline__ f4 ld4(rsrc_t r, uint32_t off) {
   return f4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
             __uint_as_float(v[3])};
 }
+using f2 = __attribute__((ext_vector_type(2))) float;
+__device__ __forceinline__ f2 ld2(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0);
+  return f2{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
 __device__ __forceinline__ void st4(rsrc_t r, uint32_t off, f4 v) {
   typedef unsigned int u4 __attribute__((ext_vector_type(4)));
   u4 u;
@@ -337,7 +342,8 @@ struct WgradParams {
   const float* y; int64_t yg; int64_t ldy;   // Y[g][n][c] = y[g*yg + n*ldy + c]
   float* part;                               // [chunks][g][jr][c]
   int64_t rows;                              // rows per chunk (multiple of 16)
-  int ncw4, njg;                             // column workgroups, 64-row j groups per head
+  int ncw4, njg;                             // column and j workgroups per head (the fp32
+                                             // kernel's j workgroups are 64-row j groups)
   int vec;                                   // Y rows 16-byte aligned and c % 4 == 0
 };
 
@@ -554,37 +560,66 @@ __device__ __forceinline__ f4 mfma_bf(const u4_t& a, const u4_t& b, f4 c) {
 constexpr int kBfStage = 32;  // rows per stage: one k-block of the bf16 product
 constexpr int kBfXp = 40;     // bf16 per LDS row of the transposed X parts (32 rows + 8)
 
-// Workgroup as head_wgrad. X staged in LDS already split and transposed, [part][j][row], so
-// a lane's A operand of a tile and part is one 16-byte LDS read; each lane's Y values of a
-// stage are eight float4 rows (rows 8*(l/16) + s, columns cw + 4*(l%16) .. +3), split in
-// registers into the B operands of its four column tiles. The next stage's X and Y are
-// loaded while the current one is multiplied.
-template <int NJT, int NW>
-__global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
+// Column tiles (16 columns) per wave of the split-bf16 wgrad, and waves per workgroup at
+// most: 32-column waves small enough (about 110 VGPRs) for four per SIMD.
+constexpr int kWbCt = 2;
+constexpr int kWbCols = 16 * kWbCt;
+#ifndef FA_WB_MAXW
+#define FA_WB_MAXW 12
+#endif
+#ifndef FA_WB_SIMDW
+#define FA_WB_SIMDW 3
+#endif
+constexpr int kWbMaxWaves = FA_WB_MAXW;
+// LDS of the split-bf16 wgrad's X stages, and the waves per SIMD it is held to (its launch
+// bound): FA_WB_SIMDW (3: about 170 VGPRs a wave), less where the LDS keeps fewer resident
+// (asking for more than the LDS allows would void the bound).
+constexpr int wgrad_bf_lds(int njg) { return 2 * 3 * 64 * njg * kBfXp * 2; }
+constexpr int wgrad_bf_min_waves(int waves, int njg) {
+  const int per_simd = (160 * 1024 / wgrad_bf_lds(njg)) * waves / 4;
+  return per_simd >= FA_WB_SIMDW ? FA_WB_SIMDW : (per_simd >= 1 ? per_simd : 1);
+}
+
+// The workgroup covers NJG 64-row j groups of a head (wave jl*NW + w: j group jl, 32
+// columns) so that every X element is staged once per workgroup and every Y element is
+// fetched from HBM once per workgroup (the NJG waves of one column read it through the L1).
+// X staged in LDS already split and transposed, [part][j][row], so a lane's A operand of a
+// tile and part is one 16-byte LDS read; each lane's Y values of a stage are eight float2
+// rows (rows 8*(l/16) + s, columns cw + 2*(l%16), +1), split in registers into the B
+// operands of its two column tiles. Two stages of X and Y are in flight: a stage's
+// registers are reloaded with the stage after next as soon as they are consumed (Y split
+// into B operands, X stored into LDS).
+template <int NJT, int NW, int NJG>
+__global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)) void head_wgrad_bf(WgradParams P) {
   constexpr int SR = kBfStage;
-  constexpr int XE = (SR + NW - 1) / NW;       // X elements per thread and stage
-  __shared__ __align__(16) uint16_t xp[2][3][64][kBfXp];
+  constexpr int CT = kWbCt;
+  constexpr int XC = 64 * NJG;                 // X columns the workgroup stages
+  constexpr int XE = (SR + NW - 1) / NW;       // X elements per thread and stage (rows step NW)
+  __shared__ __align__(16) uint16_t xp[2][3][XC][kBfXp];
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = uniform(tid / kWave);
-  const int per_g = P.njg * P.ncw4;
+  const int jl = wave / NW;
+  const int per_g = P.njg * P.ncw4;            // j workgroups x column workgroups per head
   const int g = blockIdx.y / per_g;
   const int rem = blockIdx.y - g * per_g;
-  const int jg = rem / P.ncw4;
-  const int cw = ((rem - jg * P.ncw4) * NW + wave) * kWcols;
-  const bool active = cw < P.c;
-  const int j0 = jg * 64;
+  const int jw = rem / P.ncw4;
+  const int cw = ((rem - jw * P.ncw4) * NW + (wave - jl * NW)) * kWbCols;
+  const int jbase = jw * XC;                   // first j of the workgroup
+  const int j0 = jbase + 64 * jl;              // first j of the wave
+  const bool active = cw < P.c && j0 < P.jr;
   const int li = lane & 15, lq = lane >> 4;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * P.rows;
   const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
   const float* xbase = P.x + g * P.xg;
   const float* ybase = P.y + g * P.yg;
-  // X elements of this thread: column `lane` of the j group, stage rows wave + NW*i
-  const int xj = j0 + lane;
-  const uint32_t xo = xj < P.j ? 4u * static_cast<uint32_t>(wave * P.ldx + xj) : kOob;
+  // X elements of this thread: column xc of the workgroup's j range, stage rows xr + NW*i
+  const int xc = tid % XC, xr = tid / XC;
+  const int xj = jbase + xc;
+  const uint32_t xo = xj < P.j ? 4u * static_cast<uint32_t>(xr * P.ldx + xj) : kOob;
   const uint32_t xstep = 4u * static_cast<uint32_t>(NW * P.ldx);
   const bool xones = xj >= P.j && xj < P.jr;   // this thread's column is the ones row
-  const int cl = cw + 4 * li;                  // first of this lane's four B columns
+  const int cl = cw + CT * li;                 // first of this lane's CT B columns
   const uint32_t yo =
       (active && cl < P.c) ? 4u * static_cast<uint32_t>(8 * lq * P.ldy + cl) : kOob;
   const uint32_t ystep = 4u * static_cast<uint32_t>(P.ldy);   // one row
@@ -592,89 +627,94 @@ __global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
     const int64_t rows = r1 - nb < SR ? r1 - nb : SR;
     return rsrc(base + nb * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
   };
-  float xv[XE];
-  auto xload = [&](int64_t nb) {
+  auto xload = [&](float (&xv)[XE], int64_t nb) {
     const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
 #pragma unroll
     for (int i = 0; i < XE; ++i)
-      xv[i] = ld1(rx, (xo == kOob || wave + NW * i >= SR) ? kOob : xo + i * xstep);
+      xv[i] = ld1(rx, (xo == kOob || xr + NW * i >= SR) ? kOob : xo + i * xstep);
   };
-  auto xstore = [&](int b, int64_t nb) {
+  auto xstore = [&](int b, const float (&xv)[XE], int64_t nb) {
     const int64_t left = r1 - nb;
     const int valid = left < SR ? static_cast<int>(left) : SR;
 #pragma unroll
     for (int i = 0; i < XE; i += 2) {
-      const int ra = wave + NW * i, rb = wave + NW * (i + 1);
+      const int ra = xr + NW * i, rb = xr + NW * (i + 1);
       const float va = xo == kOob ? ((xones && ra < valid) ? 1.f : 0.f) : xv[i];
       const float vb = i + 1 < XE ? (xo == kOob ? ((xones && rb < valid) ? 1.f : 0.f) : xv[i + 1]) : 0.f;
       uint32_t part[3];
       split3(va, vb, part);
 #pragma unroll
       for (int q = 0; q < 3; ++q) {
-        if (ra < SR) xp[b][q][lane][ra] = static_cast<uint16_t>(part[q] & 0xffffu);
-        if (i + 1 < XE && rb < SR) xp[b][q][lane][rb] = static_cast<uint16_t>(part[q] >> 16);
+        if (ra < SR) xp[b][q][xc][ra] = static_cast<uint16_t>(part[q] & 0xffffu);
+        if (i + 1 < XE && rb < SR) xp[b][q][xc][rb] = static_cast<uint16_t>(part[q] >> 16);
       }
     }
   };
-  f4 raw[8];
-  auto yload = [&](int64_t nb) {
+  auto yload = [&](f2 (&raw)[8], int64_t nb) {
     const rsrc_t ry = stage_rsrc(ybase, nb, P.ldy, P.c);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) raw[s] = ld4(ry, yo == kOob ? kOob : yo + s * ystep);
+    for (int s = 0; s < 8; ++s) raw[s] = ld2(ry, yo == kOob ? kOob : yo + s * ystep);
   };
-  f4 acc[NJT][4];
+  f4 acc[NJT][CT];
 #pragma unroll
   for (int a = 0; a < NJT; ++a)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[a][t] = f4{0.f, 0.f, 0.f, 0.f};
-  int64_t nb = r0;
-  xload(nb);
-  yload(nb);
-  xstore(0, nb);
+    for (int t = 0; t < CT; ++t) acc[a][t] = f4{0.f, 0.f, 0.f, 0.f};
+  float xa[XE], xb[XE];
+  f2 ra[8], rb[8];
+  xload(xa, r0);
+  yload(ra, r0);
+  xload(xb, r0 + SR);
+  yload(rb, r0 + SR);
+  xstore(0, xa, r0);
   __syncthreads();
-  int b = 0;
-  for (; nb < r1; nb += SR) {
+  int buf = 0;
+  auto step = [&](f2 (&rc)[8], float (&xc_)[XE], const float (&xn)[XE], int64_t at) {
     // this stage's B operands: tile t, part q, k-slots s = rows 8*(l/16) + s
-    u4_t bp[3][4];
+    u4_t bp[3][CT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < CT; ++t) {
 #pragma unroll
       for (int s = 0; s < 8; s += 2) {
         uint32_t part[3];
-        split3(raw[s][t], raw[s + 1][t], part);
+        split3(rc[s][t], rc[s + 1][t], part);
 #pragma unroll
         for (int q = 0; q < 3; ++q) bp[q][t][s / 2] = part[q];
       }
     }
-    xload(nb + SR);
-    yload(nb + SR);
+    xload(xc_, at + 2 * SR);
+    yload(rc, at + 2 * SR);
     pin();
     if (active) {
-      u4_t ap[3][NJT];
+      // the six part products by A part (A0 x B0..B2, A1 x B0..B1, A2 x B0), each over
+      // every (a, t): consecutive products go to different accumulators
 #pragma unroll
-      for (int q = 0; q < 3; ++q)
+      for (int qa = 0; qa < 3; ++qa) {
+        u4_t ap[NJT];
 #pragma unroll
         for (int a = 0; a < NJT; ++a)
-          ap[q][a] = *reinterpret_cast<const u4_t*>(&xp[b][q][16 * a + li][8 * lq]);
-      // the six part products, each over every (a, t): consecutive products go to
-      // different accumulators
-      constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
-      constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
+          ap[a] = *reinterpret_cast<const u4_t*>(&xp[buf][qa][64 * jl + 16 * a + li][8 * lq]);
 #pragma unroll
-      for (int pr = 0; pr < 6; ++pr) {
+        for (int qb = 0; qb < 3 - qa; ++qb) {
 #pragma unroll
-        for (int a = 0; a < NJT; ++a) {
+          for (int a = 0; a < NJT; ++a) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc[a][t] = mfma_bf(ap[kPa[pr]][a], bp[kPb[pr]][t], acc[a][t]);
+            for (int t = 0; t < CT; ++t) acc[a][t] = mfma_bf(ap[a], bp[qb][t], acc[a][t]);
+          }
         }
       }
     }
-    xstore(b ^ 1, nb + SR);
+    xstore(buf ^ 1, xn, at + SR);
     __syncthreads();
-    b ^= 1;
+    buf ^= 1;
+  };
+  for (int64_t nb = r0; nb < r1; nb += 2 * SR) {
+    step(ra, xa, xb, nb);
+    if (nb + SR >= r1) break;
+    step(rb, xb, xa, nb + SR);
   }
   if (!active) return;
-  // D[i][m] of tile t: row j0 + 16a + 4lq + r, column cw + 4*li + t
+  // D[i][m] of tile t: row j0 + 16a + 4lq + r, column cw + CT*li + t
   float* part = P.part + (static_cast<int64_t>(blockIdx.x) * P.g + g) * P.jr * P.c;
 #pragma unroll
   for (int a = 0; a < NJT; ++a) {
@@ -683,7 +723,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
       const int jj = j0 + 16 * a + 4 * lq + r;
       if (jj < P.jr) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < CT; ++t)
           if (cl + t < P.c) part[static_cast<int64_t>(jj) * P.c + cl + t] = acc[a][t][r];
       }
     }
@@ -694,16 +734,16 @@ __global__ __launch_bounds__(NW * kWave, 2) void head_wgrad_bf(WgradParams P) {
 #ifndef FA_RB_WAVES
 #define FA_RB_WAVES 12
 #endif
-#ifndef FA_RB_TILES
-#define FA_RB_TILES 2
-#endif
 #ifndef FA_RB_MINW
 #define FA_RB_MINW 3
 #endif
 constexpr int kRbWaves = FA_RB_WAVES;  // waves per workgroup (one per CU: W's parts fill LDS)
 constexpr int kRbBlock = kRbWaves * kWave;
-constexpr int kRbTiles = FA_RB_TILES;  // 16-row tiles per wave step (share the B operands)
-constexpr int kRbDepth = 2;    // k-blocks of Y in flight ahead of the one multiplied
+#ifndef FA_RB_DEPTH
+#define FA_RB_DEPTH 4
+#endif
+constexpr int kRbDepth = FA_RB_DEPTH;  // k-blocks of Y in flight ahead of the one multiplied
+constexpr int kRbQuads = 4;    // W quads per thread in flight while W is staged in LDS
 
 // LDS row (bf16) of the split W[g]: the k-blocks, plus 8 so that the rows of a 16-lane read
 // start 4 banks apart.
@@ -713,11 +753,12 @@ size_t reduce_bf_lds_bytes(int j, int c) {
 }
 
 // head_reduce with the split-bf16 product (see head_wgrad_bf): W[g]'s three parts in LDS
-// ([part][J+1][cp], row J zero); each wave takes two 16-row tiles of Y at a time (the B
-// operands read from LDS serve both) and runs over all C columns, 32 at a time. k-slot s of
-// lane l stands for column 32kb + 4*(l/16) + s (s < 4) or 32kb + 16 + 4*(l/16) + s - 4, so
-// that a lane's A values are two float4 loads whose 16 lanes of a row read 64 contiguous
-// bytes; W is stored in LDS in that order.
+// ([part][J+1][cp], row J zero). Each wave streams its 16-row tiles as one sequence of
+// (tile, k-block) steps, kRbDepth k-blocks of Y in flight across tile ends; its first loads
+// are issued before W is staged. k-slot s
+// of lane l stands for column 32kb + 4*(l/16) + s (s < 4) or 32kb + 16 + 4*(l/16) + s - 4,
+// so that a lane's A values are two float4 loads whose 16 lanes of a row read 64
+// contiguous bytes; W is stored in LDS in that order.
 template <int JT>
 __global__ __launch_bounds__(kRbBlock, FA_RB_MINW) void head_reduce_bf(ReduceParams P) {
   extern __shared__ __align__(16) uint16_t wlb[];
@@ -726,107 +767,141 @@ __global__ __launch_bounds__(kRbBlock, FA_RB_MINW) void head_reduce_bf(ReducePar
   const int wave = uniform(tid / kWave);
   const int g = blockIdx.y;
   const int cp = P.cp, rows = P.j + 1;
-  const float* w = P.w + g * P.wg;
-  for (int i = tid; i < rows * cp; i += kRbBlock) {
-    const int jr = i / cp, cc = i - jr * cp;
-    const int kb = cc >> 5, q = (cc >> 3) & 3, s = cc & 7;
-    const int src = 32 * kb + (s < 4 ? 4 * q + s : 16 + 4 * q + s - 4);
-    const float v = (jr < P.j && cc < 32 * P.kb && src < P.c) ? w[jr * P.ldw + src] : 0.f;
-    uint32_t part[3];
-    split3(v, 0.f, part);
+  const int li = lane & 15, lq = lane >> 4;
+  const float* ybase = P.y + g * P.yg;
+  // this wave's 16-row tiles: gw, gw + (all waves), ... with the waves dealt to the
+  // workgroups first, so that a launch with fewer tiles than resident waves still spreads
+  // them over every CU (and the tiles in flight at one time are neighbours in memory)
+  const int64_t gw = static_cast<int64_t>(wave) * gridDim.x + blockIdx.x;
+  const int64_t nw_all = static_cast<int64_t>(gridDim.x) * kRbWaves;
+  const int64_t t16 = (P.n + 15) / 16;
+  const int tiles = gw < t16 ? static_cast<int>((t16 - gw + nw_all - 1) / nw_all) : 0;
+  auto tile_row = [&](int t) { return (gw + t * nw_all) * 16; };
+  auto tile_end = [&](int64_t n0) { return P.n < n0 + 16 ? P.n : n0 + 16; };
+  const int64_t rb = tile_row(0);
+  const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
+  auto range_rsrc = [&](int t) {
+    const int64_t n0 = tile_row(t);
+    const int64_t left = tile_end(n0) - n0;
+    const int64_t rr = left < 16 ? left : 16;
+    return rsrc(ybase + (rr > 0 ? n0 : 0) * P.ldy, rr > 0 ? 4 * ((rr - 1) * P.ldy + P.c) : 0);
+  };
+  // load cursor: tile lt, k-block lk (wave-uniform)
+  int lt = 0, lk = 0;
+  rsrc_t lr = range_rsrc(0);
+  auto ly = [&](f4 (&v)[2]) {
+    const int c0 = 32 * lk + 4 * lq, c1 = c0 + 16;
+    const bool in = lt < tiles;
+    const uint32_t o0 = in && c0 < P.c ? yrow + 4u * c0 : kOob;
+    const uint32_t o1 = in && c1 < P.c ? yrow + 4u * c1 : kOob;
+    v[0] = ld4(lr, o0);
+    v[1] = ld4(lr, o1);
+    if (++lk == P.kb) {
+      lk = 0;
+      ++lt;
+      lr = range_rsrc(lt);
+    }
+  };
+  // issued in order: ya[0] is the oldest; kRbDepth k-blocks in flight
+  f4 ya[kRbDepth][2];
 #pragma unroll
-    for (int pp = 0; pp < 3; ++pp) wlb[(pp * rows + jr) * cp + cc] = static_cast<uint16_t>(part[pp] & 0xffffu);
+  for (int d = 0; d < kRbDepth; ++d) {
+    ly(ya[d]);
+    pin();
+  }
+  const float* w = P.w + g * P.wg;
+  {
+    // W[g] in quads of LDS columns: LDS columns 4i..4i+3 of a row hold four consecutive
+    // columns of W (k-slots 0-3 or 4-7 of one lane group), so each quad is four loads issued
+    // together and one 8-byte LDS store per part; kRbQuads quads per thread in flight.
+    const int cq = cp >> 2, quads = rows * cq;
+    for (int q0 = tid; q0 < quads; q0 += kRbBlock * kRbQuads) {
+      float v[kRbQuads][4];
+#pragma unroll
+      for (int u = 0; u < kRbQuads; ++u) {
+        const int i = q0 + u * kRbBlock;
+        const int jr = i / cq, cc = 4 * (i - jr * cq);
+        const int src = 32 * (cc >> 5) + ((cc & 4) ? 16 : 0) + 4 * ((cc >> 3) & 3);
+        const bool ok = i < quads && jr < P.j && cc < 32 * P.kb && src < P.c;
+        const float* wp = w + static_cast<int64_t>(ok ? jr : 0) * P.ldw + (ok ? src : 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = ok ? wp[e] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kRbQuads; ++u) {
+        const int i = q0 + u * kRbBlock;
+        if (i < quads) {
+          const int jr = i / cq, cc = 4 * (i - jr * cq);
+          uint32_t lo[3], hi[3];
+          split3(v[u][0], v[u][1], lo);
+          split3(v[u][2], v[u][3], hi);
+#pragma unroll
+          for (int pp = 0; pp < 3; ++pp)
+            *reinterpret_cast<uint2*>(&wlb[(pp * rows + jr) * cp + cc]) = make_uint2(lo[pp], hi[pp]);
+        }
+      }
+    }
   }
   __syncthreads();
-  const int li = lane & 15, lq = lane >> 4;
   int wrow[JT];
 #pragma unroll
   for (int jt = 0; jt < JT; ++jt) wrow[jt] = (16 * jt + li < P.j ? 16 * jt + li : P.j) * cp + 8 * lq;
   const int plane = rows * cp;
-  const float* ybase = P.y + g * P.yg;
-  const int64_t pairs = (P.n + 16 * kRbTiles - 1) / (16 * kRbTiles);
-  const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
-  for (int64_t pr = static_cast<int64_t>(blockIdx.x) * kRbWaves + wave; pr < pairs;
-       pr += static_cast<int64_t>(gridDim.x) * kRbWaves) {
-    const int64_t n0 = pr * 16 * kRbTiles;
-    rsrc_t ry[kRbTiles];
+  f4 acc[JT];
 #pragma unroll
-    for (int u = 0; u < kRbTiles; ++u) ry[u] = tile_rsrc(ybase, P.n, n0 + 16 * u, P.ldy, P.c);
-    // the two float4 of each tile for k-block kb (columns past C read 0)
-    auto ly = [&](int kb, f4 (&v)[kRbTiles][2]) {
-      const int c0 = 32 * kb + 4 * lq, c1 = c0 + 16;
-      const uint32_t o0 = c0 < P.c ? yrow + 4u * c0 : kOob, o1 = c1 < P.c ? yrow + 4u * c1 : kOob;
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = f4{0.f, 0.f, 0.f, 0.f};
+  auto mm = [&](int kb, const f4 (&v)[2]) {
+    u4_t ap[3];
 #pragma unroll
-      for (int u = 0; u < kRbTiles; ++u) {
-        v[u][0] = ld4(ry[u], o0);
-        v[u][1] = ld4(ry[u], o1);
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        uint32_t part[3];
+        split3(v[h][e], v[h][e + 1], part);
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp) ap[pp][2 * h + e / 2] = part[pp];
       }
-    };
-    f4 acc[kRbTiles][JT];
+    }
+    u4_t bp[3][JT];
 #pragma unroll
-    for (int u = 0; u < kRbTiles; ++u)
+    for (int pp = 0; pp < 3; ++pp)
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) acc[u][jt] = f4{0.f, 0.f, 0.f, 0.f};
-    auto mm = [&](int kb, const f4 (&v)[kRbTiles][2]) {
-      u4_t ap[kRbTiles][3];
+      for (int jt = 0; jt < JT; ++jt)
+        bp[pp][jt] = *reinterpret_cast<const u4_t*>(&wlb[pp * plane + wrow[jt] + 32 * kb]);
+    constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
+    constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
 #pragma unroll
-      for (int u = 0; u < kRbTiles; ++u) {
+    for (int q = 0; q < 6; ++q) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            uint32_t part[3];
-            split3(v[u][h][e], v[u][h][e + 1], part);
-#pragma unroll
-            for (int pp = 0; pp < 3; ++pp) ap[u][pp][2 * h + e / 2] = part[pp];
-          }
-        }
-      }
-      u4_t bp[3][JT];
-#pragma unroll
-      for (int pp = 0; pp < 3; ++pp)
-#pragma unroll
-        for (int jt = 0; jt < JT; ++jt)
-          bp[pp][jt] = *reinterpret_cast<const u4_t*>(&wlb[pp * plane + wrow[jt] + 32 * kb]);
-      constexpr int kPa[6] = {0, 0, 1, 0, 2, 1};
-      constexpr int kPb[6] = {0, 1, 0, 2, 0, 1};
-#pragma unroll
-      for (int q = 0; q < 6; ++q) {
-#pragma unroll
-        for (int u = 0; u < kRbTiles; ++u) {
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt) acc[u][jt] = mfma_bf(ap[u][kPa[q]], bp[kPb[q]][jt], acc[u][jt]);
-        }
-      }
-    };
-    // issued in order: ya[0] is the oldest; kRbDepth k-blocks in flight
-    f4 ya[kRbDepth][kRbTiles][2];
+      for (int jt = 0; jt < JT; ++jt) acc[jt] = mfma_bf(ap[kPa[q]], bp[kPb[q]][jt], acc[jt]);
+    }
+  };
+  int kb = 0, ct = 0;
+  int64_t n0 = rb;
+  const int steps = tiles * P.kb;   // a multiple of kRbDepth (P.kb is)
+  for (int st = 0; st < steps; st += kRbDepth) {
 #pragma unroll
     for (int d = 0; d < kRbDepth; ++d) {
-      ly(d, ya[d]);
+      mm(kb + d, ya[d]);
+      pin();
+      ly(ya[d]);
       pin();
     }
-    for (int kb = 0; kb < P.kb; kb += kRbDepth) {   // kb is a multiple of kRbDepth
-#pragma unroll
-      for (int d = 0; d < kRbDepth; ++d) {
-        mm(kb + d, ya[d]);
-        pin();
-        ly(kb + d + kRbDepth, ya[d]);
-        pin();
-      }
-    }
-    // D row 4lq + r of tile u, column 16jt + li
-#pragma unroll
-    for (int u = 0; u < kRbTiles; ++u) {
+    kb += kRbDepth;
+    if (kb == P.kb) {
+      // D row 4lq + r of the tile, column 16jt + li
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) {
         const int jj = 16 * jt + li;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int64_t row = n0 + 16 * u + 4 * lq + r;
-          if (jj < P.j && row < P.n) P.z[row * P.ldz + g * P.zg + jj] = acc[u][jt][r];
+          const int64_t row = n0 + 4 * lq + r;
+          if (jj < P.j && row < tile_end(n0)) P.z[row * P.ldz + g * P.zg + jj] = acc[jt][r];
         }
+        acc[jt] = f4{0.f, 0.f, 0.f, 0.f};
       }
+      kb = 0;
+      n0 = tile_row(++ct);
     }
   }
 }
@@ -1084,14 +1159,44 @@ WgradKernel wgrad_kernel(int njt, int nw, bool vec, int xv) {
   return nullptr;
 }
 
-// The split-bf16 wgrad kernel for njt 16-row j tiles and nw waves per workgroup.
-WgradKernel wgrad_bf_kernel(int njt, int nw) {
-#define FA_WGB_NW(NJ, NWV) \
-  if (njt == NJ && nw == NWV) return head_wgrad_bf<NJ, NWV>;
-#define FA_WGB(NJ) FA_WGB_NW(NJ, 1) FA_WGB_NW(NJ, 2) FA_WGB_NW(NJ, 3) FA_WGB_NW(NJ, 4)
-  FA_WGB(1) FA_WGB(2) FA_WGB(3) FA_WGB(4)
+// The split-bf16 wgrad launch shape: njg 64-row j groups and nw 32-column waves per
+// workgroup (nw one of the compiled counts, at least the waves the columns need), njw j
+// workgroups and ncwg column workgroups per head, njt 16-row j tiles per wave.
+struct WgradBfShape {
+  int njg, nw, njw, ncwg, njt;
+};
+
+WgradBfShape wgrad_bf_shape(int jr, int c) {
+  WgradBfShape s;
+  const int jg = static_cast<int>(ceil_div(jr, 64));
+  s.njg = jg < 4 ? jg : 4;
+  s.njw = static_cast<int>(ceil_div(jg, s.njg));
+  const int ncw = static_cast<int>(ceil_div(c, kWbCols));
+  static const int kCounts[] = {2, 4, 6, 8, 12};
+  int cap = 0;   // the most column waves a workgroup of njg j groups takes
+  for (int v : kCounts)
+    if (v * s.njg <= kWbMaxWaves) cap = v;
+  s.ncwg = static_cast<int>(ceil_div(ncw, cap));
+  const int need = static_cast<int>(ceil_div(ncw, s.ncwg));
+  s.nw = cap;
+  for (int v : kCounts)
+    if (v >= need && v < s.nw) s.nw = v;
+  s.njt = jg == 1 ? static_cast<int>(ceil_div(jr, 16)) : 4;
+  return s;
+}
+
+// The split-bf16 wgrad kernel for a launch shape.
+WgradKernel wgrad_bf_kernel(const WgradBfShape& s) {
+#define FA_WGB(NJ, NWV, NG) \
+  if (s.njt == NJ && s.nw == NWV && s.njg == NG) return head_wgrad_bf<NJ, NWV, NG>;
+#define FA_WGB1(NJ) FA_WGB(NJ, 2, 1) FA_WGB(NJ, 4, 1) FA_WGB(NJ, 6, 1) FA_WGB(NJ, 8, 1) \
+  FA_WGB(NJ, 12, 1)
+  FA_WGB1(1) FA_WGB1(2) FA_WGB1(3) FA_WGB1(4)
+  FA_WGB(4, 2, 2) FA_WGB(4, 4, 2) FA_WGB(4, 6, 2)
+  FA_WGB(4, 2, 3) FA_WGB(4, 4, 3)
+  FA_WGB(4, 2, 4)
+#undef FA_WGB1
 #undef FA_WGB
-#undef FA_WGB_NW
   return nullptr;
 }
 
@@ -1110,9 +1215,15 @@ constexpr bool kWgradBf = FA_WGRAD_BF != 0;
 // rows.
 int64_t wgrad_plan_chunks(int64_t n, int j, int c, int groups, int ones, bool bf) {
   const int jr = j + (ones ? 1 : 0);
+  if (bf) {
+    const WgradBfShape s = wgrad_bf_shape(jr, c);
+    const WgradKernel k = wgrad_bf_kernel(s);
+    const int64_t resident =
+        k ? resident_blocks(reinterpret_cast<const void*>(k), 0, s.njg * s.nw * kWave) : 1;
+    return wgrad_chunks(n, groups * s.njw * s.ncwg, resident);
+  }
   const int nw = wgrad_waves(c);
-  const WgradKernel k = bf ? wgrad_bf_kernel(wgrad_njt(jr), nw)
-                           : wgrad_kernel(wgrad_njt(jr), nw, true, 1);
+  const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, true, 1);
   const int64_t resident =
       k ? resident_blocks(reinterpret_cast<const void*>(k), 0, nw * kWave) : 1;
   return wgrad_chunks(n, wgrad_groups(j, c, groups, ones), resident);
@@ -1228,9 +1339,9 @@ extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t group
     if (hipFuncSetAttribute(kp, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess)
       return launch_status();
-    const int64_t pairs = ceil_div(n, 16 * kRbTiles);
+    const int64_t tiles = ceil_div(n, 16);
     int64_t gx = resident_blocks(kp, lds, kRbBlock) / groups;
-    if (gx > ceil_div(pairs, kRbWaves)) gx = ceil_div(pairs, kRbWaves);
+    if (gx > tiles) gx = tiles;
     if (gx < 1) gx = 1;
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(groups)),
                        dim3(kRbBlock), lds, stream, P);
@@ -1289,10 +1400,22 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.x = x; P.ldx = ldx; P.xg = xg; P.y = y; P.yg = yg; P.ldy = ldy;
   P.vec = aligned16(y) && !(ldy & 3) && !(yg & 3) && !(c & 3);
   const int nw = wgrad_waves(c);
-  P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), nw));
-  P.njg = static_cast<int>(ceil_div(jr, 64));
-  const int gy = wgrad_groups(j, c, groups, ones);
   const bool bf = kWgradBf && P.vec && nw >= 2;   // one-wave shapes (c <= 64) stay fp32
+  WgradKernel k = nullptr;
+  int gy = 0, threads = 0;
+  if (bf) {
+    const WgradBfShape s = wgrad_bf_shape(jr, c);
+    P.ncw4 = s.ncwg;
+    P.njg = s.njw;
+    gy = groups * s.njw * s.ncwg;
+    threads = s.njg * s.nw * kWave;
+    k = wgrad_bf_kernel(s);
+  } else {
+    P.ncw4 = static_cast<int>(ceil_div(ceil_div(c, kWcols), nw));
+    P.njg = static_cast<int>(ceil_div(jr, 64));
+    gy = wgrad_groups(j, c, groups, ones);
+    threads = nw * kWave;
+  }
   const int64_t chunks = wgrad_plan_chunks(n, j, c, groups, ones, bf);
   P.rows = round_up(ceil_div(n, chunks), bf ? kBfStage : kWgradStage);
   // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
@@ -1308,10 +1431,9 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
     xv = 4;
   else if (!(j & 1) && !(ldx & 1) && !(xg & 1) && !(reinterpret_cast<uintptr_t>(x) & 7))
     xv = 2;
-  const WgradKernel k =
-      bf ? wgrad_bf_kernel(wgrad_njt(jr), nw) : wgrad_kernel(wgrad_njt(jr), nw, P.vec != 0, xv);
+  if (!bf) k = wgrad_kernel(wgrad_njt(jr), nw, P.vec != 0, xv);
   if (!k) return FA_EUNSUPPORTED;
-  hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(nw * kWave)), 0, stream, P);
+  hipLaunchKernelGGL(k, grid, dim3(static_cast<unsigned>(threads)), 0, stream, P);
   if (!(out & 3) && aligned16(dw) && aligned16(scratch)) {
     hipLaunchKernelGGL(chunk_sums4, dim3(static_cast<unsigned>(ceil_div(out, 4 * kSumOut4))), dim3(kBlock), 0,
                        stream, static_cast<const float*>(P.part), static_cast<int>(used), out, dw);

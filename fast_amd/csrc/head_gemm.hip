@@ -594,7 +594,12 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
   constexpr int SR = kBfStage;
   constexpr int CT = kWbCt;
   constexpr int XC = 64 * NJG;                 // X columns the workgroup stages
-  constexpr int XE = (SR + NW - 1) / NW;       // X elements per thread and stage (rows step NW)
+  // X staging: thread t takes column t % XC of the workgroup's j range and the 8-row groups
+  // t / XC, t / XC + NT / XC, ... of a stage (written to LDS as one 16-byte run per part)
+  constexpr int NT = NJG * NW * kWave;
+  constexpr int XG = NT / XC < 4 ? 4 / (NT / XC) : 1;   // 8-row groups per thread
+  constexpr int XE = 8 * XG;                   // X elements per thread and stage
+  static_assert(NT / XC >= 4 || 4 % (NT / XC) == 0, "X row groups must cover the stage");
   __shared__ __align__(16) uint16_t xp[2][3][XC][kBfXp];
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -613,12 +618,13 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
   const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
   const float* xbase = P.x + g * P.xg;
   const float* ybase = P.y + g * P.yg;
-  // X elements of this thread: column xc of the workgroup's j range, stage rows xr + NW*i
-  const int xc = tid % XC, xr = tid / XC;
+  const int xc = tid % XC, xg0 = tid / XC;     // column, first 8-row group
+  const bool xbusy = xg0 < 4;                  // threads past the stage's four groups idle
   const int xj = jbase + xc;
-  const uint32_t xo = xj < P.j ? 4u * static_cast<uint32_t>(xr * P.ldx + xj) : kOob;
-  const uint32_t xstep = 4u * static_cast<uint32_t>(NW * P.ldx);
-  const bool xones = xj >= P.j && xj < P.jr;   // this thread's column is the ones row
+  const uint32_t xo = xbusy && xj < P.j ? 4u * static_cast<uint32_t>(8 * xg0 * P.ldx + xj) : kOob;
+  const uint32_t xrow = 4u * static_cast<uint32_t>(P.ldx);                       // next row
+  const uint32_t xgrp = 4u * static_cast<uint32_t>(8 * (NT / XC) * P.ldx);      // next group
+  const bool xones = xbusy && xj >= P.j && xj < P.jr;   // this thread's column is the ones row
   const int cl = cw + CT * li;                 // first of this lane's CT B columns
   const uint32_t yo =
       (active && cl < P.c) ? 4u * static_cast<uint32_t>(8 * lq * P.ldy + cl) : kOob;
@@ -630,23 +636,31 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
   auto xload = [&](float (&xv)[XE], int64_t nb) {
     const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
 #pragma unroll
-    for (int i = 0; i < XE; ++i)
-      xv[i] = ld1(rx, (xo == kOob || xr + NW * i >= SR) ? kOob : xo + i * xstep);
+    for (int k = 0; k < XG; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        xv[8 * k + e] = ld1(rx, (xo == kOob || xg0 + k * (NT / XC) >= 4) ? kOob : xo + k * xgrp + e * xrow);
   };
   auto xstore = [&](int b, const float (&xv)[XE], int64_t nb) {
     const int64_t left = r1 - nb;
     const int valid = left < SR ? static_cast<int>(left) : SR;
 #pragma unroll
-    for (int i = 0; i < XE; i += 2) {
-      const int ra = xr + NW * i, rb = xr + NW * (i + 1);
-      const float va = xo == kOob ? ((xones && ra < valid) ? 1.f : 0.f) : xv[i];
-      const float vb = i + 1 < XE ? (xo == kOob ? ((xones && rb < valid) ? 1.f : 0.f) : xv[i + 1]) : 0.f;
-      uint32_t part[3];
-      split3(va, vb, part);
+    for (int k = 0; k < XG; ++k) {
+      const int grp = xg0 + k * (NT / XC);
+      if (grp < 4) {
+        u4_t part4[3];
 #pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        if (ra < SR) xp[b][q][xc][ra] = static_cast<uint16_t>(part[q] & 0xffffu);
-        if (i + 1 < XE && rb < SR) xp[b][q][xc][rb] = static_cast<uint16_t>(part[q] >> 16);
+        for (int e = 0; e < 8; e += 2) {
+          const int ra = 8 * grp + e;
+          const float va = xo == kOob ? ((xones && ra < valid) ? 1.f : 0.f) : xv[8 * k + e];
+          const float vb = xo == kOob ? ((xones && ra + 1 < valid) ? 1.f : 0.f) : xv[8 * k + e + 1];
+          uint32_t part[3];
+          split3(va, vb, part);
+#pragma unroll
+          for (int q = 0; q < 3; ++q) part4[q][e / 2] = part[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q) *reinterpret_cast<u4_t*>(&xp[b][q][xc][8 * grp]) = part4[q];
       }
     }
   };
@@ -781,6 +795,7 @@ __global__ __launch_bounds__(kRbBlock, FA_RB_MINW) void head_reduce_bf(ReducePar
   const int64_t rb = tile_row(0);
   const uint32_t yrow = 4u * static_cast<uint32_t>(li * P.ldy);
   auto range_rsrc = [&](int t) {
+    if (t >= tiles) return rsrc(ybase, 0);   // past the wave's last tile: reads zeros
     const int64_t n0 = tile_row(t);
     const int64_t left = tile_end(n0) - n0;
     const int64_t rr = left < 16 ? left : 16;

@@ -540,8 +540,10 @@ class HeadReduce(torch.autograd.Function):
     def backward(ctx, dz):
         y, w, z = ctx.saved_tensors
         dz = dz.contiguous()
-        dy = _proj(dz, w, None) if ctx.needs_input_grad[0] else None
+        # the weight gradient first: dy, written last, is what the next kernel (the fused
+        # backward) reads, so its most recent part is still in the last-level cache
         dw = _wgrad(dz, y, w.shape[0], False) if ctx.needs_input_grad[1] else None
+        dy = _proj(dz, w, None) if ctx.needs_input_grad[0] else None
         if ctx.link is not None and dy is not None:
             ctx.link.tdot = fastAgg.row_group_dots(dz, z, w.shape[0])
         return dy, dw, None

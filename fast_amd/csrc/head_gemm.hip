@@ -574,14 +574,17 @@ constexpr int kWbMaxWaves = FA_WB_MAXW;
 // LDS of the split-bf16 wgrad's X stages, and the waves per SIMD it is held to (its launch
 // bound): FA_WB_SIMDW (3: about 170 VGPRs a wave), less where the LDS keeps fewer resident
 // (asking for more than the LDS allows would void the bound).
-constexpr int wgrad_bf_lds(int njg) { return 2 * 3 * 64 * njg * kBfXp * 2; }
-constexpr int wgrad_bf_min_waves(int waves, int njg) {
-  const int per_simd = (160 * 1024 / wgrad_bf_lds(njg)) * waves / 4;
-  return per_simd >= FA_WB_SIMDW ? FA_WB_SIMDW : (per_simd >= 1 ? per_simd : 1);
+constexpr int wgrad_bf_span(int njt) { return njt > 4 ? 128 : 64; }   // j rows of a wave
+constexpr int wgrad_bf_lds(int njg, int njt) { return 2 * 3 * wgrad_bf_span(njt) * njg * kBfXp * 2; }
+constexpr int wgrad_bf_min_waves(int waves, int njg, int njt) {
+  const int per_simd = (160 * 1024 / wgrad_bf_lds(njg, njt)) * waves / 4;
+  const int want = njt > 4 ? 2 : FA_WB_SIMDW;   // 128-row waves: about 250 VGPRs
+  return per_simd >= want ? want : (per_simd >= 1 ? per_simd : 1);
 }
 
-// The workgroup covers NJG 64-row j groups of a head (wave jl*NW + w: j group jl, 32
-// columns) so that every X element is staged once per workgroup and every Y element is
+// The workgroup covers NJG j groups of a head (wave jl*NW + w: j group jl, 32 columns; a j
+// group is 64 rows, or 128 for a single group of more than four 16-row tiles) so that every
+// X element is staged once per workgroup and every Y element is
 // fetched from HBM once per workgroup (the NJG waves of one column read it through the L1).
 // X staged in LDS already split and transposed, [part][j][row], so a lane's A operand of a
 // tile and part is one 16-byte LDS read; each lane's Y values of a stage are eight float2
@@ -590,10 +593,12 @@ constexpr int wgrad_bf_min_waves(int waves, int njg) {
 // registers are reloaded with the stage after next as soon as they are consumed (Y split
 // into B operands, X stored into LDS).
 template <int NJT, int NW, int NJG>
-__global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)) void head_wgrad_bf(WgradParams P) {
+__global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG, NJT)) void head_wgrad_bf(WgradParams P) {
   constexpr int SR = kBfStage;
   constexpr int CT = kWbCt;
-  constexpr int XC = 64 * NJG;                 // X columns the workgroup stages
+  constexpr int JW = wgrad_bf_span(NJT);       // j rows of a wave
+  static_assert(NJT <= 4 || NJG == 1, "128-row j groups come one to a workgroup");
+  constexpr int XC = JW * NJG;                 // X columns the workgroup stages
   // X staging: thread t takes column t % XC of the workgroup's j range and the 8-row groups
   // t / XC, t / XC + NT / XC, ... of a stage (written to LDS as one 16-byte run per part)
   constexpr int NT = NJG * NW * kWave;
@@ -611,14 +616,15 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
   const int jw = rem / P.ncw4;
   const int cw = ((rem - jw * P.ncw4) * NW + (wave - jl * NW)) * kWbCols;
   const int jbase = jw * XC;                   // first j of the workgroup
-  const int j0 = jbase + 64 * jl;              // first j of the wave
+  const int j0 = jbase + JW * jl;              // first j of the wave
   const bool active = cw < P.c && j0 < P.jr;
   const int li = lane & 15, lq = lane >> 4;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * P.rows;
   const int64_t r1 = P.n < r0 + P.rows ? P.n : r0 + P.rows;
   const float* xbase = P.x + g * P.xg;
   const float* ybase = P.y + g * P.yg;
-  const int xc = tid % XC, xg0 = tid / XC;     // column, first 8-row group
+  const int xc = tid % XC;                     // column
+  const int xg0 = uniform(tid / XC);           // first 8-row group (XC is a multiple of 64)
   const bool xbusy = xg0 < 4;                  // threads past the stage's four groups idle
   const int xj = jbase + xc;
   const uint32_t xo = xbusy && xj < P.j ? 4u * static_cast<uint32_t>(8 * xg0 * P.ldx + xj) : kOob;
@@ -633,13 +639,15 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
     const int64_t rows = r1 - nb < SR ? r1 - nb : SR;
     return rsrc(base + nb * ld, rows > 0 ? 4 * ((rows - 1) * ld + w) : 0);
   };
+  // one offset expression per element, no select: a thread without X (column past j, or
+  // idle) starts at kOob, and its offsets stay past every range without wrapping (the
+  // stage offsets are below 2^31, checked on the host); the thread's groups are all < 4
   auto xload = [&](float (&xv)[XE], int64_t nb) {
     const rsrc_t rx = stage_rsrc(xbase, nb, P.ldx, P.j);
 #pragma unroll
     for (int k = 0; k < XG; ++k)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        xv[8 * k + e] = ld1(rx, (xo == kOob || xg0 + k * (NT / XC) >= 4) ? kOob : xo + k * xgrp + e * xrow);
+      for (int e = 0; e < 8; ++e) xv[8 * k + e] = ld1(rx, xo + k * xgrp + e * xrow);
   };
   auto xstore = [&](int b, const float (&xv)[XE], int64_t nb) {
     const int64_t left = r1 - nb;
@@ -707,7 +715,7 @@ __global__ __launch_bounds__(NJG * NW * kWave, wgrad_bf_min_waves(NJG * NW, NJG)
         u4_t ap[NJT];
 #pragma unroll
         for (int a = 0; a < NJT; ++a)
-          ap[a] = *reinterpret_cast<const u4_t*>(&xp[buf][qa][64 * jl + 16 * a + li][8 * lq]);
+          ap[a] = *reinterpret_cast<const u4_t*>(&xp[buf][qa][JW * jl + 16 * a + li][8 * lq]);
 #pragma unroll
         for (int qb = 0; qb < 3 - qa; ++qb) {
 #pragma unroll
@@ -1184,19 +1192,23 @@ struct WgradBfShape {
 WgradBfShape wgrad_bf_shape(int jr, int c) {
   WgradBfShape s;
   const int jg = static_cast<int>(ceil_div(jr, 64));
-  s.njg = jg < 4 ? jg : 4;
-  s.njw = static_cast<int>(ceil_div(jg, s.njg));
+  const bool wide = jg == 2;   // 65..128 rows: one 128-row j group (5 to 8 tiles a wave)
+  s.njg = wide ? 1 : (jg < 4 ? jg : 4);
+  s.njw = wide ? 1 : static_cast<int>(ceil_div(jg, s.njg));
   const int ncw = static_cast<int>(ceil_div(c, kWbCols));
+  // column-wave counts compiled (128-row groups: 4 or 8, two waves per SIMD)
   static const int kCounts[] = {2, 4, 6, 8, 12};
+  static const int kWideCounts[] = {4, 4, 8, 8, 8};
+  const int* counts = wide ? kWideCounts : kCounts;
   int cap = 0;   // the most column waves a workgroup of njg j groups takes
-  for (int v : kCounts)
-    if (v * s.njg <= kWbMaxWaves) cap = v;
+  for (int i = 0; i < 5; ++i)
+    if (counts[i] * s.njg <= kWbMaxWaves) cap = counts[i];
   s.ncwg = static_cast<int>(ceil_div(ncw, cap));
   const int need = static_cast<int>(ceil_div(ncw, s.ncwg));
   s.nw = cap;
-  for (int v : kCounts)
-    if (v >= need && v < s.nw) s.nw = v;
-  s.njt = jg == 1 ? static_cast<int>(ceil_div(jr, 16)) : 4;
+  for (int i = 0; i < 5; ++i)
+    if (counts[i] >= need && counts[i] < s.nw) s.nw = counts[i];
+  s.njt = jg == 1 || wide ? static_cast<int>(ceil_div(jr, 16)) : 4;
   return s;
 }
 
@@ -1207,6 +1219,8 @@ WgradKernel wgrad_bf_kernel(const WgradBfShape& s) {
 #define FA_WGB1(NJ) FA_WGB(NJ, 2, 1) FA_WGB(NJ, 4, 1) FA_WGB(NJ, 6, 1) FA_WGB(NJ, 8, 1) \
   FA_WGB(NJ, 12, 1)
   FA_WGB1(1) FA_WGB1(2) FA_WGB1(3) FA_WGB1(4)
+  FA_WGB(5, 4, 1) FA_WGB(5, 8, 1) FA_WGB(6, 4, 1) FA_WGB(6, 8, 1)
+  FA_WGB(7, 4, 1) FA_WGB(7, 8, 1) FA_WGB(8, 4, 1) FA_WGB(8, 8, 1)
   FA_WGB(4, 2, 2) FA_WGB(4, 4, 2) FA_WGB(4, 6, 2)
   FA_WGB(4, 2, 3) FA_WGB(4, 4, 3)
   FA_WGB(4, 2, 4)

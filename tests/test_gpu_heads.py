@@ -69,11 +69,13 @@ def test_head_reduce(dev, shape):
     assert torch.equal(got2, got)
 
 
-# wider heads for the weight gradient (rows_mm's single head of up to D rows): two, three
-# and four 64-row j groups in one workgroup, more than four (two j workgroups), and column
-# workgroups of those; the ones row can open a j group of its own (j = 64, 256)
+# wider heads for the weight gradient (rows_mm's single head of up to D rows): one 128-row
+# j group (65 to 128 rows, also with two column workgroups), three and four 64-row j groups
+# in one workgroup, more than four (two j workgroups), and column workgroups of those; the
+# ones row can open a j group of its own (j = 64, 256)
 WGRAD_SHAPES = SHAPES + [(500, 1, 100, 100), (300, 1, 150, 100), (260, 1, 256, 256),
-                         (333, 1, 200, 600), (97, 2, 64, 132)]
+                         (333, 1, 200, 600), (97, 2, 64, 132), (700, 1, 127, 376),
+                         (90, 1, 80, 68)]
 
 
 @pytest.mark.parametrize("shape", WGRAD_SHAPES)

@@ -1249,7 +1249,12 @@ int64_t wgrad_plan_chunks(int64_t n, int j, int c, int groups, int ones, bool bf
     const WgradKernel k = wgrad_bf_kernel(s);
     const int64_t resident =
         k ? resident_blocks(reinterpret_cast<const void*>(k), 0, s.njg * s.nw * kWave) : 1;
-    return wgrad_chunks(n, groups * s.njw * s.ncwg, resident);
+    int64_t chunks = wgrad_chunks(n, groups * s.njw * s.ncwg, resident);
+    // a multiple of the 8 XCDs (workgroups go to XCDs in turn by linear id), so that the
+    // workgroups of one chunk (its heads, j and column blocks, which read the same rows)
+    // share one XCD's L2
+    if (chunks >= 16) chunks -= chunks % 8;
+    return chunks;
   }
   const int nw = wgrad_waves(c);
   const WgradKernel k = wgrad_kernel(wgrad_njt(jr), nw, true, 1);
@@ -1449,7 +1454,9 @@ extern "C" int fa_head_wgrad_f32(int64_t n, int32_t j, int32_t c, int32_t groups
   P.rows = round_up(ceil_div(n, chunks), bf ? kBfStage : kWgradStage);
   // byte offsets inside a chunk (and its one-block prefetch) stay below the marker
   if ((P.rows + 64) * (ldx > ldy ? ldx : ldy) * 4 >= static_cast<int64_t>(kOob)) return FA_EUNSUPPORTED;
-  const int64_t used = ceil_div(n, P.rows);
+  // the split-bf16 grid keeps every planned chunk (trailing ones past n add zeros), so that
+  // its width stays a multiple of 8
+  const int64_t used = bf ? chunks : ceil_div(n, P.rows);
   if (!scratch || scratch_bytes < fa_head_wgrad_scratch_bytes(n, j, c, groups, ones))
     return FA_ESCRATCH;
   P.part = static_cast<float*>(scratch);

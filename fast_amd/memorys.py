@@ -41,10 +41,11 @@ def _timed(name, nbytes, fn, *args):
 def _tmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """a^T b for a [n, p], b [n, q] over many rows (the cells' weight gradients): the per-head
     weight-gradient kernel (split-bf16 matrix-core products, fixed-order sums) with a's
-    columns in G groups of at most 64 and every group reading the same rows of b."""
+    columns in G groups of at most 128 (one j group of the kernel's workgroup each) and
+    every group reading the same rows of b."""
     n, p = a.shape
     q = b.shape[1]
-    G = next(g for g in range(1, p + 1) if p % g == 0 and p // g <= tgat.HEAD_KERNEL_MAX_J)
+    G = next(g for g in range(1, p + 1) if p % g == 0 and p // g <= 128)
     nb = 4 * (n * p + n * q + p * q)
     y = b.unsqueeze(0).expand(G, n, q)
     return _timed("cell_wgrad", nb, fastAgg.head_wgrad, a, y, G, False).reshape(p, q)

@@ -1109,18 +1109,21 @@ std::vector<at::Tensor> time_rows_grad(at::Tensor g, at::Tensor ts, std::optiona
 }
 
 // -> [hy [n, m], workspace [n, 4m]]
-std::vector<at::Tensor> gru_fwd(at::Tensor gi, at::Tensor gh, std::optional<at::Tensor> h) {
+std::vector<at::Tensor> gru_fwd(at::Tensor gi, at::Tensor gh, std::optional<at::Tensor> h,
+                                std::optional<at::Tensor> b_ih, std::optional<at::Tensor> b_hh) {
   check_f32(gi, 2, "gi");
   check_f32(gh, 2, "gh");
   const int64_t n = gi.size(0), m = gi.size(1) / 3;
   TORCH_CHECK(gi.size(1) == 3 * m && gh.sizes() == gi.sizes(), "gru_fwd: gi, gh must be [n, 3m]");
   const float* hp = opt_ptr(h, n * m, "h");
+  const float* bi = opt_ptr(b_ih, 3 * m, "b_ih");
+  const float* bh = opt_ptr(b_hh, 3 * m, "b_hh");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gi.device());
   auto hy = at::empty({n, m}, gi.options());
   auto ws = at::empty({n, 4 * m}, gi.options());
   const int st = fa_gru_fwd_f32(n, static_cast<int32_t>(m), gi.data_ptr<float>(), 3 * m,
-                                gh.data_ptr<float>(), 3 * m, hp, m, hy.data_ptr<float>(), m,
-                                ws.data_ptr<float>(), stream_of(gi));
+                                gh.data_ptr<float>(), 3 * m, hp, m, bi, bh, hy.data_ptr<float>(),
+                                m, ws.data_ptr<float>(), stream_of(gi));
   check_status(st, "gru_fwd");
   return {hy, ws};
 }
@@ -1150,15 +1153,19 @@ std::vector<at::Tensor> gru_bwd(at::Tensor dhy, at::Tensor ws, std::optional<at:
   return {dgi, dgh, dh, db_ih, db_hh};
 }
 
-at::Tensor rnn_fwd(at::Tensor gi, at::Tensor gh) {
+at::Tensor rnn_fwd(at::Tensor gi, at::Tensor gh, std::optional<at::Tensor> b_ih,
+                   std::optional<at::Tensor> b_hh) {
   check_f32(gi, 2, "gi");
   check_f32(gh, 2, "gh");
   TORCH_CHECK(gh.sizes() == gi.sizes(), "rnn_fwd: gi, gh must have one shape");
   const int64_t n = gi.size(0), m = gi.size(1);
+  const float* bi = opt_ptr(b_ih, m, "b_ih");
+  const float* bh = opt_ptr(b_hh, m, "b_hh");
   c10::hip::HIPGuardMasqueradingAsCUDA guard(gi.device());
   auto hy = at::empty({n, m}, gi.options());
   const int st = fa_rnn_fwd_f32(n, static_cast<int32_t>(m), gi.data_ptr<float>(), m,
-                                gh.data_ptr<float>(), m, hy.data_ptr<float>(), m, stream_of(gi));
+                                gh.data_ptr<float>(), m, bi, bh, hy.data_ptr<float>(), m,
+                                stream_of(gi));
   check_status(st, "rnn_fwd");
   return hy;
 }
@@ -1357,11 +1364,13 @@ PYBIND11_MODULE(fastAgg, m) {
         py::arg("col"), py::arg("ts"), py::arg("mem_ts"), py::arg("w"), py::arg("b"));
   m.def("time_rows_grad", &time_rows_grad, "dw, db of time_rows_ for the column gradient g",
         py::arg("g"), py::arg("ts"), py::arg("mem_ts"), py::arg("w"), py::arg("b"));
-  m.def("gru_fwd", &gru_fwd, "GRUCell gates from gi, gh (and h)", py::arg("gi"), py::arg("gh"),
-        py::arg("h") = py::none());
+  m.def("gru_fwd", &gru_fwd, "GRUCell gates from gi, gh (and h; the biases when gi, gh lack them)",
+        py::arg("gi"), py::arg("gh"), py::arg("h") = py::none(), py::arg("b_ih") = py::none(),
+        py::arg("b_hh") = py::none());
   m.def("gru_bwd", &gru_bwd, "GRUCell gate and bias gradients", py::arg("dhy"), py::arg("workspace"),
         py::arg("h") = py::none(), py::arg("need_dh") = false);
-  m.def("rnn_fwd", &rnn_fwd, "RNNCell (tanh) from gi, gh", py::arg("gi"), py::arg("gh"));
+  m.def("rnn_fwd", &rnn_fwd, "RNNCell (tanh) from gi, gh (the biases when gi, gh lack them)",
+        py::arg("gi"), py::arg("gh"), py::arg("b_ih") = py::none(), py::arg("b_hh") = py::none());
   m.def("rnn_bwd", &rnn_bwd, "RNNCell (tanh) gradient of gi and gh", py::arg("dhy"), py::arg("hy"));
   m.def("memory_update_", &memory_update_, "node memory write-back, last row of an id wins",
         py::arg("ids"), py::arg("mem"), py::arg("ts"), py::arg("node_memory"),

@@ -1375,6 +1375,9 @@ extern "C" int fa_head_reduce_f32(int64_t n, int32_t j, int32_t c, int32_t group
       return launch_status();
     const int64_t tiles = ceil_div(n, 16);
     int64_t gx = resident_blocks(kp, lds, kRbBlock) / groups;
+    // heads that share Y rows: a multiple of the 8 XCDs, so that the workgroups of one grid
+    // column (the same tiles) run on one XCD and its L2 serves the other heads' reads
+    if (groups > 1 && gx >= 16) gx -= gx % 8;
     if (gx > tiles) gx = tiles;
     if (gx < 1) gx = 1;
     hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(groups)),

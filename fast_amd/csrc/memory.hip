@@ -247,20 +247,26 @@ __global__ __launch_bounds__(kRowBlock) void col_finish(const float* partial, in
 // ---------------------------------------------------------------------------------
 // gi = x W_ih^T + b_ih, gh = h W_hh^T + b_hh, gate blocks [r | z | n] (torch.nn.GRUCell):
 //   r = s(gi_r + gh_r), z = s(gi_z + gh_z), c = tanh(gi_n + r gh_n), h' = (1 - z) c + z h.
+// With bi / bh the products come without their biases, added here (per column).
 // ws keeps [r | z | c | gh_n] per row for the backward.
 __global__ __launch_bounds__(kColBlock) void gru_fwd(int64_t n, int32_t m, const float* gi,
                                                      int64_t ldgi, const float* gh, int64_t ldgh,
-                                                     const float* h, int64_t ldh, float* hy,
-                                                     int64_t ldy, float* ws) {
+                                                     const float* h, int64_t ldh, const float* bi,
+                                                     const float* bh, float* hy, int64_t ldy,
+                                                     float* ws) {
   const RowChunk c = row_chunk(n);
   for (int j = c.lane; j < m; j += kColLanes) {
+    // the biases of this column's three gates (0 without)
+    const float br = (bi ? bi[j] : 0.f) + (bh ? bh[j] : 0.f);
+    const float bz = (bi ? bi[m + j] : 0.f) + (bh ? bh[m + j] : 0.f);
+    const float bin = bi ? bi[2 * m + j] : 0.f, bhn = bh ? bh[2 * m + j] : 0.f;
     for (int64_t i = c.r0 + c.phase; i < c.r1; i += kRowPhases) {
       const float* a = gi + i * ldgi;
       const float* q = gh + i * ldgh;
-      const float r = sigmoid(a[j] + q[j]);
-      const float z = sigmoid(a[m + j] + q[m + j]);
-      const float hn = q[2 * m + j];
-      const float nc = tanhf(a[2 * m + j] + r * hn);
+      const float r = sigmoid(a[j] + q[j] + br);
+      const float z = sigmoid(a[m + j] + q[m + j] + bz);
+      const float hn = q[2 * m + j] + bhn;
+      const float nc = tanhf(a[2 * m + j] + bin + r * hn);
       const float hv = h ? h[i * ldh + j] : 0.f;
       hy[i * ldy + j] = (1.f - z) * nc + z * hv;
       float* s = ws + i * 4 * m;
@@ -313,16 +319,19 @@ __global__ __launch_bounds__(kColBlock) void gru_bwd(int64_t n, int32_t m, const
   }
 }
 
-// torch.nn.RNNCell (tanh): h' = tanh(gi + gh); backward da = dy (1 - h'^2).
+// torch.nn.RNNCell (tanh): h' = tanh(gi + gh) (+ the biases bi, bh when the products come
+// without them); backward da = dy (1 - h'^2).
 __global__ __launch_bounds__(kEltBlock) void rnn_fwd(int64_t n, int32_t m, const float* gi,
                                                      int64_t ldgi, const float* gh, int64_t ldgh,
-                                                     float* hy, int64_t ldy) {
+                                                     const float* bi, const float* bh, float* hy,
+                                                     int64_t ldy) {
   const int64_t total = n * m;
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kEltBlock + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * kEltBlock) {
     const int64_t i = idx / m;
     const int j = static_cast<int>(idx - i * m);
-    hy[i * ldy + j] = tanhf(gi[i * ldgi + j] + gh[i * ldgh + j]);
+    const float b = (bi ? bi[j] : 0.f) + (bh ? bh[j] : 0.f);
+    hy[i * ldy + j] = tanhf(gi[i * ldgi + j] + gh[i * ldgh + j] + b);
   }
 }
 
@@ -503,14 +512,15 @@ extern "C" int fa_time_rows_grad_f32(int64_t n, const float* ts, const float* me
 
 extern "C" int fa_gru_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi,
                               const float* gh, int64_t ld_gh, const float* h, int64_t ld_h,
-                              float* hy, int64_t ld_hy, float* workspace, hipStream_t stream) {
+                              const float* b_ih, const float* b_hh, float* hy, int64_t ld_hy,
+                              float* workspace, hipStream_t stream) {
   if (n < 0 || m < 0 || ld_gi < 3 * static_cast<int64_t>(m) || ld_gh < 3 * static_cast<int64_t>(m) ||
       ld_hy < m || (h && ld_h < m))
     return FA_EINVAL;
   if (n == 0 || m == 0) return FA_OK;
   if (!gi || !gh || !hy || !workspace) return FA_EINVAL;
-  gru_fwd<<<chunk_blocks(n), kColBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, h, ld_h, hy, ld_hy,
-                                                     workspace);
+  gru_fwd<<<chunk_blocks(n), kColBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, h, ld_h, b_ih, b_hh,
+                                                     hy, ld_hy, workspace);
   return launch_status();
 }
 
@@ -549,12 +559,13 @@ extern "C" int fa_gru_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld
 }
 
 extern "C" int fa_rnn_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi,
-                              const float* gh, int64_t ld_gh, float* hy, int64_t ld_hy,
-                              hipStream_t stream) {
+                              const float* gh, int64_t ld_gh, const float* b_ih, const float* b_hh,
+                              float* hy, int64_t ld_hy, hipStream_t stream) {
   if (n < 0 || m < 0 || ld_gi < m || ld_gh < m || ld_hy < m) return FA_EINVAL;
   if (n == 0 || m == 0) return FA_OK;
   if (!gi || !gh || !hy) return FA_EINVAL;
-  rnn_fwd<<<elt_grid(n * m), kEltBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, hy, ld_hy);
+  rnn_fwd<<<elt_grid(n * m), kEltBlock, 0, stream>>>(n, m, gi, ld_gi, gh, ld_gh, b_ih, b_hh, hy,
+                                                     ld_hy);
   return launch_status();
 }
 

@@ -7,9 +7,11 @@ kernels of libfastagg_hip.so.
   room for the updater's time features, so the updater never concatenates.
 * ``GRUMemeoryUpdater`` / ``RNNMemeoryUpdater`` keep ``torch.nn.GRUCell`` / ``RNNCell`` as
   the parameter holders (same state-dict keys). Their forward is one autograd node: the time
-  columns (``fastAgg.time_rows_``), the two input products as torch GEMMs, the gate
-  arithmetic (``fastAgg.gru_fwd`` / ``rnn_fwd``); the backward runs the gate gradients, the
-  weight GEMMs and the time-encoder gradient (``fastAgg.time_rows_grad``).
+  columns (``fastAgg.time_rows_``), the two input products on the split-bf16 reduce kernel
+  (``fastAgg.head_reduce``, without their biases), the gate arithmetic with the biases
+  (``fastAgg.gru_fwd`` / ``rnn_fwd``); the backward runs the gate gradients, the weight
+  gradients (``fastAgg.head_wgrad``) and the time-encoder gradient
+  (``fastAgg.time_rows_grad``).
 * ``update_memory`` / ``update_mailbox`` (deliver_to 'self', mail_combine 'last') write back
   with one winner per node id, the row that comes last in the reference's order
   (``fastAgg.memory_update_`` / ``mailbox_update_``). For ``update_memory`` the reference's
@@ -301,13 +303,15 @@ class _CellUpdate(torch.autograd.Function):
         n, m = h.shape
         if dt:
             _timed("time_rows", n * (8 + 4 * dt), fastAgg.time_rows_, rows, mail_w, ts, mem_ts, tw, tb)
-        gi = torch.addmm(b_ih, rows, w_ih.t())
-        gh = torch.addmm(b_hh, h, w_hh.t())
+        # the input and hidden products on the split-bf16 reduce kernel (torch's GEMM where
+        # it does not take the shape), without their biases, which the gate kernel adds
+        gi = tgat._rows_mm(rows, w_ih, "cell_proj")
+        gh = tgat._rows_mm(h, w_hh, "cell_proj")
         if gru:
             # gi, gh, h read; h' and the [r | z | c | gh_n] workspace written
-            hy, saved = _timed("cell_fwd", n * m * 48, fastAgg.gru_fwd, gi, gh, h)
+            hy, saved = _timed("cell_fwd", n * m * 48, fastAgg.gru_fwd, gi, gh, h, b_ih, b_hh)
         else:
-            hy = _timed("cell_fwd", n * m * 12, fastAgg.rnn_fwd, gi, gh)
+            hy = _timed("cell_fwd", n * m * 12, fastAgg.rnn_fwd, gi, gh, b_ih, b_hh)
             saved = hy
         ctx.gru, ctx.mail_w, ctx.dt = gru, mail_w, dt
         ctx.save_for_backward(rows, h, w_ih, w_hh, saved, ts, mem_ts, tw, tb)

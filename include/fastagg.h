@@ -415,10 +415,12 @@ int fa_time_rows_grad_f32(int64_t n, const float* ts, const float* mem_ts, const
 /* Elementwise part of torch.nn.GRUCell (memorys.py:291): gi = x W_ih^T + b_ih and
  * gh = h W_hh^T + b_hh with gate blocks [r | z | n], each m wide; hy = (1 - z) c + z h with
  * r = sigmoid(gi_r + gh_r), z = sigmoid(gi_z + gh_z), c = tanh(gi_n + r gh_n) (h NULL => 0).
- * workspace [n][4m] keeps r, z, c, gh_n for fa_gru_bwd_f32. */
+ * b_ih / b_hh [3m] (each optional): gi / gh come without that bias, which is added here.
+ * workspace [n][4m] keeps r, z, c, gh_n (with its bias) for fa_gru_bwd_f32. */
 int fa_gru_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const float* gh,
-                   int64_t ld_gh, const float* h, int64_t ld_h, float* hy, int64_t ld_hy,
-                   float* workspace, hipStream_t stream);
+                   int64_t ld_gh, const float* h, int64_t ld_h, const float* b_ih,
+                   const float* b_hh, float* hy, int64_t ld_hy, float* workspace,
+                   hipStream_t stream);
 /* dgi, dgh [n][3m] (the gradients of gi and gh) from dhy; dh (optional) = dhy z, the direct
  * path only (the caller adds dgh W_hh). With db_ih and db_hh (both or neither) also the bias
  * gradients db_ih = sum over rows of dgi, db_hh = the same of dgh (fixed-order sums,
@@ -428,10 +430,12 @@ int fa_gru_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy, const
                    const float* h, int64_t ld_h, float* dgi, int64_t ld_dgi, float* dgh,
                    int64_t ld_dgh, float* dh, int64_t ld_dh, float* db_ih, float* db_hh,
                    void* scratch, size_t scratch_bytes, hipStream_t stream);
-/* torch.nn.RNNCell with tanh (RNNMemeoryUpdater, memorys.py:332): hy = tanh(gi + gh); the
- * backward gives da = dhy (1 - hy^2), the gradient of both gi and gh. */
+/* torch.nn.RNNCell with tanh (RNNMemeoryUpdater, memorys.py:332): hy = tanh(gi + gh), plus
+ * b_ih / b_hh [m] (each optional) where gi / gh come without them; the backward gives
+ * da = dhy (1 - hy^2), the gradient of both gi and gh. */
 int fa_rnn_fwd_f32(int64_t n, int32_t m, const float* gi, int64_t ld_gi, const float* gh,
-                   int64_t ld_gh, float* hy, int64_t ld_hy, hipStream_t stream);
+                   int64_t ld_gh, const float* b_ih, const float* b_hh, float* hy, int64_t ld_hy,
+                   hipStream_t stream);
 int fa_rnn_bwd_f32(int64_t n, int32_t m, const float* dhy, int64_t ld_dhy, const float* hy,
                    int64_t ld_hy, float* da, int64_t ld_da, hipStream_t stream);
 

@@ -238,8 +238,10 @@ def test_memory_entry_points_reject_bad_arguments(lib):
     assert lib.fa_mailbox_update_f32(c(2), one, one, 1, one, c(4), 4, None, c(0), 0, one, one,
                                      c(7), one, one, 2, c(10), one, ctypes.c_uint32(1), None) == -1
     # gru: leading dimension below 3m; missing workspace
-    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(11), one, c(12), None, c(0), one, c(4), one, None) == -1
-    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(12), one, c(12), None, c(0), one, c(4), None, None) == -1
+    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(11), one, c(12), None, c(0), None, None, one, c(4),
+                              one, None) == -1
+    assert lib.fa_gru_fwd_f32(c(2), 4, one, c(12), one, c(12), None, c(0), None, None, one, c(4),
+                              None, None) == -1
     # time gradient without scratch
     assert lib.fa_time_rows_grad_f32(c(3), one, None, one, one, 8, one, c(8), one, one, None,
                                      ctypes.c_size_t(0), None) == -4

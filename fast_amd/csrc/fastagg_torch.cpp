@@ -409,12 +409,15 @@ std::vector<at::Tensor> backward_fused_attn(at::Tensor d_output, at::Tensor V_va
   const int64_t E = output.size(0), H = num_heads, dh = V_val.size(2);
   auto d_input = at::zeros({E, H}, output.options());
   auto grad_V = at::zeros({E, H, dh}, output.options());
+  const size_t sb = fa_fused_attn_bwd_scratch_bytes();
+  auto scratch = at::empty({static_cast<int64_t>(sb)}, output.options().dtype(at::kByte));
   const int st = fa_fused_attn_bwd_f32(
       indptr.data_ptr<int32_t>(), num_segments(indptr), dst_eid.data_ptr<int64_t>(),
       src_eid.data_ptr<int64_t>(), E, d_output.size(0), node_num, d_output.data_ptr<float>(),
       V_val.data_ptr<float>(), output.data_ptr<float>(), edge_mask.data_ptr<float>(),
       static_cast<int32_t>(H), static_cast<int32_t>(dh), static_cast<float>(attn_drop),
-      d_input.data_ptr<float>(), grad_V.data_ptr<float>(), stream_of(output));
+      d_input.data_ptr<float>(), grad_V.data_ptr<float>(), scratch.data_ptr(), sb,
+      stream_of(output));
   check_status(st, "backward_fused_attn");
   debug_nan(d_input, "backward_fused_attn");
   return {d_input, grad_V};

@@ -189,6 +189,7 @@ struct FaParams {
   int dh, dim, chunks;
   float slope, p;
   float* attn; float* out; float* d_act; float* grad_V;
+  const int* own;   // backward: nonzero when every V row belongs to its own edge (row e)
 };
 
 // Per-lane head of each component of its NS chunks (H = number of heads).
@@ -315,6 +316,138 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_k(FaParams P) {
   }
 }
 
+// Forward for rows of at most 32 float4 chunks (dim <= 128): the two half-waves take
+// alternate edges of the segment and each lane one chunk of its half's V row, so one load
+// instruction reads two rows (25 of each half's 32 lanes carry data at D = 100, against 25
+// of 64 with one row per wave); the halves' sums are added once per segment. Statistics,
+// attention and dropout weights as fused_attn_fwd_k.
+template <int H, bool VEC>
+__global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
+  const int lane = lane_id();
+  const int half = lane >> 5, hl = lane & (kHalf - 1);
+  int hc[4];   // head of each component of this lane's chunk (-1 past dim)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int col = 4 * hl + i;
+    hc[i] = col < P.dim ? col / P.dh : -1;
+  }
+  const uint32_t coff = 16u * static_cast<uint32_t>(hl);   // past the row for hl >= chunks
+  static_assert(kWave % (2 * kRows) == 0, "pairs stay inside a 64-edge block");
+  // V chunks of this half's edges of pairs j/2 .. j/2 + kRows - 1 of a block (entry
+  // j + 2b + half; j + 2b is even, so a pair's lanes lie in the block; entries past cnt get
+  // an empty descriptor)
+  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kRows]) {
+#pragma unroll
+    for (int b = 0; b < kRows; ++b) {
+      const int j0 = j + 2 * b;
+      const int64_t s0 = lane_i64(my_src, j0), s1 = lane_i64(my_src, j0 + 1);
+      const int64_t row = (half ? s1 : s0) - P.n_dst;
+      const bool ok = j0 + half < cnt && row >= 0 && row < P.n_v;
+      const rsrc_t rr = row_rsrc(P.V + (ok ? row : 0) * P.dim, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+      r[b] = chunk_load<VEC>(rr, coff);
+    }
+  };
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       s < P.n_seg; s += total) {
+    int64_t lb = P.indptr[s], le = P.indptr[s + 1];
+    lb = lb < 0 ? 0 : lb;
+    le = le > P.n_edges ? P.n_edges : le;
+    if (le <= lb) continue;
+    const int64_t d = P.dst[lb];
+    const bool write_out = d >= 0 && d < P.n_dst && P.dim > 0;
+    // the first 64-edge block in registers, and its first V rows in flight while the
+    // softmax statistics are formed
+    const int cnt0 = static_cast<int>(le - lb < kWave ? le - lb : kWave);
+    const bool in0 = lane < cnt0;
+    const int64_t e00 = lb + (in0 ? lane : 0);
+    float l0[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) l0[h] = in0 ? leaky(P.score[e00 * H + h], P.slope) : kMaxSeed;
+    const int64_t src0 = P.src[e00];
+    float4 r[kRows];
+    if (write_out) issue(src0, 0, cnt0, r);
+    float mx[H], sm[H];
+    if (le - lb <= kWave) {   // one block: the statistics from the registers
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        mx[h] = wave_max(l0[h]);
+        sm[h] = wave_sum(in0 ? expf(l0[h] - mx[h]) : 0.f);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < H; ++h) { mx[h] = kMaxSeed; sm[h] = 0.f; }
+      for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+        const bool in = e0 + lane < le;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+          const float l = in ? leaky(P.score[(e0 + lane) * H + h], P.slope) : kMaxSeed;
+          mx[h] = fmaxf(mx[h], wave_max(l));
+        }
+      }
+      for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+        const bool in = e0 + lane < le;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+          const float v = in ? expf(leaky(P.score[(e0 + lane) * H + h], P.slope) - mx[h]) : 0.f;
+          sm[h] += wave_sum(v);
+        }
+      }
+    }
+    float4 acc = f4_zero();
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const bool first = e0 == lb;
+      const int cnt = static_cast<int>(le - e0 < kWave ? le - e0 : kWave);
+      const bool in = lane < cnt;
+      const int64_t e = e0 + (in ? lane : 0);
+      float w[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const float l = first ? l0[h] : leaky(P.score[e * H + h], P.slope);
+        const float a = expf(l - mx[h]) / sm[h];
+        if (in) P.attn[e * H + h] = a;
+        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p) : a;
+        w[h] = in ? w[h] : 0.f;
+      }
+      if (!write_out) continue;
+      const int64_t my_src = first ? src0 : P.src[e];
+      for (int j = 0; j < cnt; j += 2 * kRows) {
+        if (!(first && j == 0)) issue(my_src, j, cnt, r);
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          if (j + 2 * b >= cnt) break;
+          const int j0 = j + 2 * b;
+          float wb[H];
+#pragma unroll
+          for (int h = 0; h < H; ++h) {
+            const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[h]), j0));
+            const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[h]), j0 + 1));
+            wb[h] = half ? w1 : w0;   // a missing entry has weight 0 and a zero row
+          }
+          acc.x = fmaf(pick<H>(wb, hc[0]), r[b].x, acc.x);
+          acc.y = fmaf(pick<H>(wb, hc[1]), r[b].y, acc.y);
+          acc.z = fmaf(pick<H>(wb, hc[2]), r[b].z, acc.z);
+          acc.w = fmaf(pick<H>(wb, hc[3]), r[b].w, acc.w);
+        }
+      }
+    }
+    if (!write_out) continue;
+    // the two halves' sums of each chunk (edge order within a half, then the halves)
+    acc.x += __shfl_xor(acc.x, kHalf, kWave);
+    acc.y += __shfl_xor(acc.y, kHalf, kWave);
+    acc.z += __shfl_xor(acc.z, kHalf, kWave);
+    acc.w += __shfl_xor(acc.w, kHalf, kWave);
+    if (half == 0) {
+      float* o = P.out + d * P.dim;
+      const int c4 = 4 * hl;
+      if (c4 < P.dim) o[c4] = acc.x;
+      if (c4 + 1 < P.dim) o[c4 + 1] = acc.y;
+      if (c4 + 2 < P.dim) o[c4 + 2] = acc.z;
+      if (c4 + 3 < P.dim) o[c4 + 3] = acc.w;
+    }
+  }
+}
+
 template <int H, int NS, bool VEC>
 __global__ __launch_bounds__(kBlock) void fused_attn_bwd_k(FaParams P) {
   __shared__ __attribute__((aligned(16))) float stage_all[kWavesPerBlock][4 * kWave * NS];
@@ -423,6 +556,183 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_k(FaParams P) {
   }
 }
 
+// The own-rows flag: set to 1, then cleared by any edge whose V row is in range and is not
+// row e (a row that two edges may add to); plain stores of a single value, any order.
+__global__ __launch_bounds__(64) void own_flag_set(int* flag) {
+  if (threadIdx.x == 0) flag[0] = 1;
+}
+
+__global__ __launch_bounds__(kBlock) void check_own_rows(const int64_t* src, int64_t n_edges,
+                                                         int64_t n_dst, int64_t n_v,
+                                                         int64_t n_src, int* flag) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < n_edges;
+       e += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t sr = src[e];
+    const int64_t row = sr - n_dst;
+    if (row >= 0 && row < n_v && sr < n_src && row != e) flag[0] = 0;
+  }
+}
+
+// Backward for rows of at most 32 float4 chunks, in the half-wave layout of
+// fused_attn_fwd_half: the halves take alternate edges; per edge its half forms the grad_V
+// chunk a*keep*dout and the partial dots keep*dout.V per head (a half-wave sum), adds the
+// grad_V row with lane-consecutive atomics through its LDS staging row, and the per-edge
+// dots land in the lane of their edge. A segment of at most 64 edges keeps them in
+// registers and writes d_act once; longer ones finish in a second pass as fused_attn_bwd_k.
+template <int H, bool VEC>
+__global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
+  __shared__ __attribute__((aligned(16))) float stage_all[kWavesPerBlock][2][4 * kHalf];
+  const int lane = lane_id();
+  const int half = lane >> 5, hl = lane & (kHalf - 1);
+  float* stage = stage_all[threadIdx.x / kWave][half];
+  int hc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int col = 4 * hl + i;
+    hc[i] = col < P.dim ? col / P.dh : -1;
+  }
+  const uint32_t coff = 16u * static_cast<uint32_t>(hl);
+  const float keep = static_cast<float>(1.0 / (1.0 - static_cast<double>(P.p)));
+  const bool own = P.own && P.own[0] != 0;
+  static_assert(kWave % (2 * kRows) == 0, "pairs stay inside a 64-edge block");
+  // this half's row of pair entry j0 (-1 when missing or out of range)
+  auto row_of = [&](int64_t my_src, int j0, int cnt) -> int64_t {
+    const int64_t s0 = lane_i64(my_src, j0), s1 = lane_i64(my_src, j0 + 1);
+    const int64_t sr = half ? s1 : s0;
+    const int64_t row = sr - P.n_dst;
+    return (j0 + half < cnt && row >= 0 && row < P.n_v && sr < P.n_src) ? row : -1;
+  };
+  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kRows]) {
+#pragma unroll
+    for (int b = 0; b < kRows; ++b) {
+      const int64_t row = row_of(my_src, j + 2 * b, cnt);
+      const rsrc_t rr = row_rsrc(P.V + (row >= 0 ? row : 0) * P.dim, row >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+      r[b] = chunk_load<VEC>(rr, coff);
+    }
+  };
+  const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + uniform(threadIdx.x / kWave);
+       s < P.n_seg; s += total) {
+    int64_t lb = P.indptr[s], le = P.indptr[s + 1];
+    lb = lb < 0 ? 0 : lb;
+    le = le > P.n_edges ? P.n_edges : le;
+    if (le <= lb) continue;
+    const int64_t d = P.dst[lb];
+    if (d < 0 || d >= P.n_dst) continue;
+    const bool one = le - lb <= kWave;
+    float4 g;   // this lane's chunk of the destination's dout row
+    {
+      const rsrc_t dr = row_rsrc(P.dout + d * P.dim, 4u * static_cast<uint32_t>(P.dim));
+      g = chunk_load<VEC>(dr, coff);
+    }
+    float tsum[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) tsum[h] = 0.f;
+    float a[H], da[H];   // lane j: entry j of the current block
+    int cnt = 0;
+    int64_t e = lb;
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      cnt = static_cast<int>(le - e0 < kWave ? le - e0 : kWave);
+      const bool in = lane < cnt;
+      e = e0 + (in ? lane : 0);
+      float kf[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        a[h] = in ? P.attn_in[e * H + h] : 0.f;
+        kf[h] = P.mask ? (P.mask[e * H + h] > P.p ? keep : 0.f) : 1.f;
+        da[h] = 0.f;
+      }
+      const int64_t my_src = P.src[e];
+      float4 r[kRows];
+      for (int j = 0; j < cnt; j += 2 * kRows) {
+        issue(my_src, j, cnt, r);
+#pragma unroll
+        for (int b = 0; b < kRows; ++b) {
+          if (j + 2 * b >= cnt) break;
+          const int j0 = j + 2 * b;
+          float ab[H], kb[H], part[H];
+#pragma unroll
+          for (int h = 0; h < H; ++h) {
+            const float a0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[h]), j0));
+            const float a1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[h]), j0 + 1));
+            const float k0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kf[h]), j0));
+            const float k1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kf[h]), j0 + 1));
+            ab[h] = half ? a1 : a0;
+            kb[h] = half ? k1 : k0;
+            part[h] = 0.f;
+          }
+          const float gx[4] = {g.x, g.y, g.z, g.w};
+          const float vx[4] = {r[b].x, r[b].y, r[b].z, r[b].w};
+          float cx[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            cx[i] = pick<H>(ab, hc[i]) * pick<H>(kb, hc[i]) * gx[i];
+#pragma unroll
+            for (int h = 0; h < H; ++h) part[h] = hc[i] == h ? fmaf(gx[i], vx[i], part[h]) : part[h];
+          }
+          // the per-edge dots: half 0's into lane j0, half 1's into lane j0 + 1
+#pragma unroll
+          for (int h = 0; h < H; ++h) {
+            const float v = kb[h] * half_sum(part[h]);
+            const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+            const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), kHalf));
+            da[h] = lane == j0 ? v0 : (lane == j0 + 1 ? v1 : da[h]);
+          }
+          // grad_V row of this half's edge: stored as float4 chunks when every row is its own
+          // edge's (the caller's zeros overwritten once), else added lane-consecutively with
+          // atomics
+          const int64_t row = row_of(my_src, j0, cnt);
+          const float4 gv = make_float4(cx[0], cx[1], cx[2], cx[3]);
+          if (own) {
+            const rsrc_t wr = row_rsrc(P.grad_V + (row >= 0 ? row : 0) * P.dim,
+                                       row >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+            if (VEC) {
+              typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+              u4 w4;
+              w4[0] = __float_as_uint(gv.x);
+              w4[1] = __float_as_uint(gv.y);
+              w4[2] = __float_as_uint(gv.z);
+              w4[3] = __float_as_uint(gv.w);
+              __builtin_amdgcn_raw_buffer_store_b128(w4, wr, static_cast<int>(coff), 0, 0);
+            } else {
+              const int o = static_cast<int>(coff);
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.x), wr, o, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.y), wr, o + 4, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.z), wr, o + 8, 0, 0);
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.w), wr, o + 12, 0, 0);
+            }
+          } else {
+            *reinterpret_cast<float4*>(stage + 4 * hl) = gv;
+            lds_sync();
+            if (row >= 0)
+              for (int c = hl; c < P.dim; c += kHalf) atomicAdd(P.grad_V + row * P.dim + c, stage[c]);
+            lds_sync();
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        if (in && !one) P.d_act[e * H + h] = da[h];
+        tsum[h] += wave_sum(in ? a[h] * da[h] : 0.f);
+      }
+    }
+    if (one) {   // the block is still in registers
+      if (lane < cnt) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) P.d_act[e * H + h] = a[h] * (da[h] - tsum[h]);
+      }
+      continue;
+    }
+    for (int64_t e0 = lb; e0 < le; e0 += kWave) {
+      const int64_t ee = e0 + lane;
+      if (ee < le) {
+#pragma unroll
+        for (int h = 0; h < H; ++h) P.d_act[ee * H + h] = P.attn_in[ee * H + h] * (P.d_act[ee * H + h] - tsum[h]);
+      }
+    }
+  }
+}
+
 constexpr int kFaMaxBlocks = 4096;
 
 int fa_grid(int64_t n_seg) {
@@ -442,6 +752,16 @@ int launch_fa(const FaParams& P, bool bwd, hipStream_t stream) {
   } else {                                                                                    \
     if (vec) hipLaunchKernelGGL((fused_attn_fwd_k<H, NSV, true>), grid, dim3(kBlock), 0, stream, P); \
     else hipLaunchKernelGGL((fused_attn_fwd_k<H, NSV, false>), grid, dim3(kBlock), 0, stream, P);    \
+  }
+  if (P.chunks <= kHalf) {   // rows of at most 128 values: the half-wave kernels
+    if (bwd) {
+      if (vec) hipLaunchKernelGGL((fused_attn_bwd_half<H, true>), grid, dim3(kBlock), 0, stream, P);
+      else hipLaunchKernelGGL((fused_attn_bwd_half<H, false>), grid, dim3(kBlock), 0, stream, P);
+    } else {
+      if (vec) hipLaunchKernelGGL((fused_attn_fwd_half<H, true>), grid, dim3(kBlock), 0, stream, P);
+      else hipLaunchKernelGGL((fused_attn_fwd_half<H, false>), grid, dim3(kBlock), 0, stream, P);
+    }
+    return launch_status();
   }
   switch (ns) {
     case 0:
@@ -480,7 +800,7 @@ extern "C" int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const
   if (static_cast<int64_t>(heads) * dh <= 4 * kWave * 4) {
     FaParams P{indptr, n_seg, dst, src, n_edges, n_dst, 0, n_edges, score, V, mask, nullptr,
                nullptr, dh, heads * dh, static_cast<int>(ceil_div(heads * dh, 4)), slope, p,
-               attn, out, nullptr, nullptr};
+               attn, out, nullptr, nullptr, nullptr};
     const int st = launch_fa_heads(P, heads, false, stream);
     if (st != -1000) return st;
   }
@@ -490,21 +810,33 @@ extern "C" int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const
   return launch_status();
 }
 
+extern "C" size_t fa_fused_attn_bwd_scratch_bytes(void) { return 16; }
+
 extern "C" int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
                                      const int64_t* src, int64_t n_edges, int64_t n_dst,
                                      int64_t n_src, const float* dout, const float* V,
                                      const float* attn, const float* mask, int32_t heads,
                                      int32_t dh, float p, float* d_act, float* grad_V,
-                                     hipStream_t stream) {
+                                     void* scratch, size_t scratch_bytes, hipStream_t stream) {
   if (n_seg < 0 || n_edges < 0 || n_dst < 0 || heads < 0 || dh < 0) return FA_EINVAL;
   if (heads > kWave) return FA_EUNSUPPORTED;
+  if (scratch && scratch_bytes < fa_fused_attn_bwd_scratch_bytes()) return FA_ESCRATCH;
   if (n_seg == 0 || heads == 0) return FA_OK;
   if (!indptr || !dst || !src || !attn || !d_act || (dh > 0 && (!V || !dout || !grad_V)))
     return FA_EINVAL;
   if (static_cast<int64_t>(heads) * dh <= 4 * kWave * 4) {
+    int* own = nullptr;
+    if (scratch && dh > 0 && heads * dh <= 4 * kHalf) {   // the half-wave backward reads it
+      own = static_cast<int*>(scratch);
+      hipLaunchKernelGGL(own_flag_set, dim3(1), dim3(64), 0, stream, own);
+      const int64_t want = ceil_div(n_edges, kBlock);
+      const unsigned grid = static_cast<unsigned>(want < 1 ? 1 : (want > 1024 ? 1024 : want));
+      hipLaunchKernelGGL(check_own_rows, dim3(grid), dim3(kBlock), 0, stream, src, n_edges, n_dst,
+                         n_edges, n_src, own);
+    }
     FaParams P{indptr, n_seg, dst, src, n_edges, n_dst, n_src, n_edges, nullptr, V, mask, attn,
                dout, dh, heads * dh, static_cast<int>(ceil_div(heads * dh, 4)), 0.f, p, nullptr,
-               nullptr, d_act, grad_V};
+               nullptr, d_act, grad_V, own};
     const int st = launch_fa_heads(P, heads, true, stream);
     if (st != -1000) return st;
   }

@@ -166,13 +166,18 @@ int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* d
  *   grad_V[src[e]-n_dst,h,:] = attn*keep*dout[dst,h,:]
  *   d_act[e,h] = attn*(da - sum_s attn*da), da = keep * dout[dst,h,:].V[...]
  * i.e. the gradient with respect to the LeakyReLU *output*; the caller applies
- * leaky_relu'(score). grad_V must be zeroed by the caller.
+ * leaky_relu'(score). grad_V must be zeroed by the caller; it is accumulated with atomics,
+ * except that with scratch (fa_fused_attn_bwd_scratch_bytes() bytes, or NULL) and rows of
+ * at most 128 values, a device check that every in-range V row is its own edge's
+ * (src[e] - n_dst == e, the sampler's layout) lets each row be stored once instead.
  * Replaces backward_fused_attn_cuda (fused_attention.cu:139-200, 330-446). */
+size_t fa_fused_attn_bwd_scratch_bytes(void);
 int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,
                           const int64_t* src, int64_t n_edges, int64_t n_dst, int64_t n_src,
                           const float* dout, const float* V, const float* attn,
                           const float* mask, int32_t heads, int32_t dh, float p,
-                          float* d_act, float* grad_V, hipStream_t stream);
+                          float* d_act, float* grad_V, void* scratch, size_t scratch_bytes,
+                          hipStream_t stream);
 
 /* ---------------------------------------------------------------------------------
  * Fused TGAT temporal attention (the hot path of layers.py:98-240, TGAT branch)

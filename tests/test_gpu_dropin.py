@@ -268,12 +268,22 @@ def test_edge_softmax_rows_outside_segments_are_zero(fa, dev):
 # fused LeakyReLU + softmax + dropout + aggregation
 # ---------------------------------------------------------------------------------------
 @pytest.mark.parametrize("p", [0.0, 0.3])
-def test_fused_attn(fa, dev, p):
+@pytest.mark.parametrize("H,dh", [(2, 50), (1, 127), (4, 32), (8, 7), (2, 100)])
+@pytest.mark.parametrize("rows", ["own", "shared"])
+def test_fused_attn(fa, dev, p, H, dh, rows):
+    """Rows of up to 128 values take the half-wave kernels (odd widths the element loads),
+    wider ones the one-wave kernels; degrees include 0, odd counts and more than 64. With
+    every V row its own edge's (the sampler's layout) grad_V is stored row by row; V rows
+    shared by several edges (and a source past n_src, ignored) take the atomic adds."""
     deg = DEGREE_SETS["ragged"]
     indptr, dst = _csr(deg)
-    N, E, H, dh = len(deg), dst.size, 2, 50
-    src = np.arange(N, N + E, dtype=np.int64)
+    N, E = len(deg), dst.size
     rng = np.random.default_rng(7)
+    if rows == "own":
+        src = np.arange(N, N + E, dtype=np.int64)
+    else:
+        src = N + rng.integers(0, E // 3, E).astype(np.int64)
+        src[5] = N + E + 3
     score = rng.standard_normal((E, H)).astype(np.float32)
     V = rng.standard_normal((E, H, dh)).astype(np.float32)
     dout = rng.standard_normal((N, H * dh)).astype(np.float32)

@@ -14,4 +14,4 @@ extern "C" const char* fa_status_string(int status) {
   return "unknown status";
 }
 
-extern "C" int fa_abi_version(void) { return 400; }
+extern "C" int fa_abi_version(void) { return 500; }

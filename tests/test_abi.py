@@ -63,7 +63,7 @@ def test_status_strings_and_version(lib):
         assert lib.fa_status_string(st)
     assert lib.fa_status_string(FA_OK) == b"success"
     assert lib.fa_status_string(-99) == b"unknown status"
-    assert lib.fa_abi_version() // 100 == 4
+    assert lib.fa_abi_version() // 100 == 5
 
 
 def test_kspace_width(lib):

@@ -143,6 +143,17 @@ __global__ __launch_bounds__(kBlock) void segment_sum(AggParams P) {
   }
 }
 
+// The value of lane `src` (any lane, per lane).
+__device__ __forceinline__ int64_t lane_i64_from(int64_t v, int src) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v & 0xffffffff)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v >> 32)));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Rows in flight per half-wave. More (8) measured slower at 100-float rows: the registers
+// they take cost occupancy that the deeper batch does not win back.
+constexpr int run_rows(int) { return 4; }
+
 template <int NS>
 __device__ __forceinline__ void flush_run(const AggParams& P, int64_t row, const float4 (&acc)[NS],
                                           float* stage) {
@@ -234,12 +245,6 @@ __global__ __launch_bounds__(kBlock) void check_sorted(AggParams P, int* flag) {
   if (any && lane_id() == __builtin_ctzll(any)) atomicOr(flag, 1);
 }
 
-// The value of lane `src` (any lane, per lane).
-__device__ __forceinline__ int64_t lane_i64_from(int64_t v, int src) {
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v & 0xffffffff)));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v >> 32)));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
 
 // Zero rows [r0, r1) of out (clamped to [0, n_out)) by a half-wave.
 template <int NS, bool VEC>
@@ -257,18 +262,20 @@ __device__ __forceinline__ void zero_rows(const AggParams& P, int64_t r0, int64_
 }
 
 constexpr int64_t kNoIndex = INT64_MIN;   // "no previous index"
-constexpr int kRunRows = 4;               // rows in flight per half-wave
+// Rows in flight per half-wave when every run is one edge long (register budget by slots).
+constexpr int copy_rows(int ns) { return ns <= 4 ? 4 : 2; }
 
 // One wave per 64 consecutive edges of [lo, hi); the wave owns the runs (maximal ranges of
 // equal output index) that start in its edges and takes them two at a time, one per
 // half-wave. A run's owner sums its rows (lane hl holds chunks hl, hl+32, ...; the run's
-// source ids loaded 32 at a time, four rows in flight), stores the output row, and zeroes
+// source ids loaded 32 at a time, run_rows rows in flight), stores the output row, and zeroes
 // the output rows between the previous run's index and its own. The rows before the first
 // index and after the last are zeroed by the whole grid. Indices outside [0, n_out) are not
 // written. With an unsorted index (flag set) the kernel zero-fills the output instead, for
 // the atomic kernel that follows.
 template <int NS, bool VEC>
 __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* flag) {
+  constexpr int RR = run_rows(NS);
   const int lane = lane_id();
   const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
   const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -295,6 +302,50 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
     const int64_t up = lane_i64_from(my, lane > 0 ? lane - 1 : 0);
     const bool start = lane < cnt && (lane == 0 ? (e0 == lo || my != prev_tile) : my != up);
     uint64_t m = __ballot(start);
+    {
+      // Every edge of the tile a run of its own (the last one too) and no gap below any of
+      // them: each output row is one source row, copied by half-waves, kCopyRows rows in
+      // flight per half.
+      const uint64_t all = cnt == kWave ? ~0ull : (1ull << cnt) - 1;
+      const int64_t last = lane_i64(my, cnt - 1);
+      const bool has_next = e0 + cnt < hi;
+      const int64_t next = has_next ? P.dst[e0 + cnt] : 0;
+      const int64_t prev = lane == 0 ? (e0 == lo ? kNoIndex : prev_tile) : up;
+      const bool gap = lane < cnt && prev != kNoIndex && my != kNoIndex && my - 1 > prev;
+      if (m == all && __ballot(gap) == 0 && (!has_next || next != last)) {
+        constexpr int R = copy_rows(NS);
+        const int64_t ids = P.src[e0 + (lane < cnt ? lane : cnt - 1)];
+        for (int j = 0; j < cnt; j += 2 * R) {
+          float4 r[R][NS];
+#pragma unroll
+          for (int q = 0; q < R; ++q) {
+            const int jj = j + 2 * q + half;
+            const int64_t sidx = lane_i64_from(ids, jj < cnt ? jj : 0);
+            const bool ok = jj < cnt && sidx >= 0 && sidx < P.n_x;
+            const rsrc_t rr = row_rsrc(P.x + (ok ? sidx : 0) * P.ldx, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+#pragma unroll
+            for (int k = 0; k < NS; ++k) {
+              const int c = hl + k * kHalf;
+              r[q][k] = c < P.chunks ? load_chunk<VEC>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < R; ++q) {
+            const int jj = j + 2 * q + half;
+            const int64_t row = lane_i64_from(my, jj < cnt ? jj : 0);
+            if (jj < cnt && row >= 0 && row < P.n_out) {
+              const rsrc_t orow = row_rsrc(P.out + row * P.ldo, 4u * static_cast<uint32_t>(P.dim));
+#pragma unroll
+              for (int k = 0; k < NS; ++k) {
+                const int c = hl + k * kHalf;
+                if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), r[q][k]);
+              }
+            }
+          }
+        }
+        continue;
+      }
+    }
     while (m) {
       // two runs: bit b0 for the first half-wave, b1 (if any) for the second
       const int b0 = __builtin_ctzll(m);
@@ -334,10 +385,10 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
         for (int64_t eb = e0 + b; eb < end; eb += kHalf) {
           const int n = static_cast<int>(end - eb < kHalf ? end - eb : kHalf);
           const int64_t ids = P.src[eb + (hl < n ? hl : 0)];  // this half's next 32 source ids
-          for (int j = 0; j < n; j += kRunRows) {
-            float4 r[kRunRows][NS];
+          for (int j = 0; j < n; j += RR) {
+            float4 r[RR][NS];
 #pragma unroll
-            for (int q = 0; q < kRunRows; ++q) {
+            for (int q = 0; q < RR; ++q) {
               // permutes stay inside this half-wave, whose lanes are all active
               const int64_t sidx = lane_i64_from(ids, half * kHalf + (j + q < n ? j + q : 0));
               const bool ok = j + q < n && sidx >= 0 && sidx < P.n_x;
@@ -349,7 +400,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
               }
             }
 #pragma unroll
-            for (int q = 0; q < kRunRows; ++q)
+            for (int q = 0; q < RR; ++q)
 #pragma unroll
               for (int k = 0; k < NS; ++k) {
                 acc[k].x += r[q][k].x;

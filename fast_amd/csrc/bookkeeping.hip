@@ -93,12 +93,25 @@ __global__ __launch_bounds__(kBlock) void scan_tile_write(const int32_t* in, int
   }
 }
 
+// Runs of equal ids among a wave's 64 consecutive ids are counted once: the first lane of a
+// run adds the run's length (sorted or clustered ids, the sampler's layout, then cost one
+// atomic per distinct id and wave instead of one per id; integer sums, so the result does
+// not depend on the order).
 __global__ __launch_bounds__(kBlock) void degree_count(const int32_t* ids, int64_t n_ids,
                                                       int32_t* deg, int64_t n_nodes) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i >= n_ids) return;
-  const int32_t v = ids[i];
-  if (v >= 0 && v < n_nodes) atomicAdd(deg + v, 1);
+  const int lane = lane_id();
+  const bool in = i < n_ids;
+  const int32_t v = in ? ids[i] : 0;
+  const int32_t up = __shfl(v, lane > 0 ? lane - 1 : 0, kWave);
+  const bool up_in = lane > 0 && i - 1 < n_ids;
+  // a lane past the end starts a run of its own, which ends the last real run
+  const bool head = !in || lane == 0 || !up_in || v != up;
+  const uint64_t heads = __ballot(head);
+  if (!in || !head || v < 0 || v >= n_nodes) return;
+  const uint64_t later = lane == kWave - 1 ? 0ull : heads & (~0ull << (lane + 1));
+  const int next = later ? __builtin_ctzll(later) : kWave;
+  atomicAdd(deg + v, next - lane);
 }
 
 __global__ __launch_bounds__(kBlock) void balance_mask(const int32_t* ptr, int64_t n,

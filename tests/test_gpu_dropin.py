@@ -51,10 +51,19 @@ def test_exclusive_sum_wraps(fa, dev):
     assert_equal(got, C.exclusive_sum(x), "exclusive_sum wrap")
 
 
-@pytest.mark.parametrize("n_ids,n_nodes", [(0, 5), (1000, 17), (300_000, 1000), (5000, 1)])
-def test_cal_deg(fa, dev, n_ids, n_nodes):
+@pytest.mark.parametrize("layout", ["random", "sorted", "runs"])
+@pytest.mark.parametrize("n_ids,n_nodes", [(0, 5), (1000, 17), (300_000, 1000), (5000, 1),
+                                           (1_192_133, 200_000)])
+def test_cal_deg(fa, dev, n_ids, n_nodes, layout):
+    """Bit-exact degrees; sorted ids and runs of repeated ids (counted once per run within a
+    wave, runs crossing wave boundaries, out-of-range ids inside runs) as the sampler lays
+    them out, and random ids."""
     rng = np.random.default_rng(n_ids)
     ids = rng.integers(-3, n_nodes + 3, size=n_ids).astype(np.int32)
+    if layout == "sorted":
+        ids = np.sort(ids)
+    elif layout == "runs":
+        ids = np.repeat(ids, rng.integers(1, 90, size=n_ids))[:n_ids]
     got = fa.cal_deg(torch.from_numpy(ids).to(dev), n_nodes)
     assert_equal(got, C.cal_deg(ids, n_nodes), "cal_deg")
 
@@ -189,6 +198,27 @@ def test_tgat_aggregation(fa, dev, name, dim):
     assert torch.count_nonzero(out[torch.from_numpy(empty).to(dev)]) == 0
 
 
+@pytest.mark.parametrize("dim", [7, 100, 300, 600])
+def test_segment_sum_edge_cases(fa, dev, dim):
+    """forward_tgat_shd over segments taken two at a time by half-waves: empty segments,
+    destinations below 0 and past n_out (skipped), segments of 1 to 100 edges side by side
+    (the halves step to the longer one's end), an odd segment count, offsets past the edge
+    count (clamped), missing source rows; rows no segment writes stay zero."""
+    rng = np.random.default_rng(dim)
+    lens = [3, 0, 1, 100, 33, 0, 32, 64, 2, 65, 7, 0, 5]
+    indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    E = int(indptr[-1])
+    indptr = np.concatenate([indptr, [E + 5]]).astype(np.int32)   # a segment past the edges
+    n_out = 20
+    seg_dst = np.array([0, 1, -2, 3, 4, 5, 25, 7, 8, 9, 10, 11, 19, 12])
+    dst = np.repeat(seg_dst[:len(lens)], lens).astype(np.int64)
+    src = rng.integers(-2, 260, size=E).astype(np.int64)           # some rows missing
+    x = rng.standard_normal((250, dim)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    out = fa.forward_tgat_shd(t(indptr), t(indptr), t(dst), t(src), t(x), n_out, 8, 32)[0]
+    assert_rel(out, C.segment_sum(indptr, dst, src, x, n_out), FP32_TOL, "forward_tgat_shd")
+
+
 def test_tgat_aggregation_unsorted(fa, dev):
     rng = np.random.default_rng(11)
     E, N, S = 5000, 300, 900
@@ -201,14 +231,18 @@ def test_tgat_aggregation_unsorted(fa, dev):
 
 
 @pytest.mark.parametrize("case", ["gaps", "out_of_range", "one_long_run", "tile_sorted_only",
-                                  "no_edges", "csr_subrange"])
-@pytest.mark.parametrize("dim", [7, 100])
+                                  "no_edges", "csr_subrange", "distinct", "distinct_gap",
+                                  "pair_at_tile_edge", "distinct_out_of_range"])
+@pytest.mark.parametrize("dim", [7, 100, 600])
 def test_tgat_aggregation_sorted_edge_cases(fa, dev, case, dim):
     """The run-owner path of the scatter (sorted output index, plain stores, every output row
     written) and its switch to the atomic path: rows before, between and after the runs come
     out zero, indices outside [0, n_out) are skipped, a run spanning many 64-edge tiles is one
     sum, an index sorted inside every tile but not across tiles takes the atomic path; against
-    the C restatement (which starts from zeros)."""
+    the C restatement (which starts from zeros). The "distinct" cases cover the tiles whose
+    every edge is a run of its own (copied row by row): with no gap, with a gap inside a tile,
+    with the last run of a tile going on into the next tile, and with indices below 0 and
+    past n_out."""
     rng = np.random.default_rng(dim + len(case))
     n_out, indptr = 40, None
     if case == "gaps":
@@ -221,6 +255,14 @@ def test_tgat_aggregation_sorted_edge_cases(fa, dev, case, dim):
         dst = np.concatenate([np.repeat([20, 21], 32), np.repeat([2, 3], 32), np.full(64, 20)])
     elif case == "no_edges":
         dst = np.zeros(0)
+    elif case == "distinct":
+        dst, n_out = np.arange(3, 133), 140
+    elif case == "distinct_gap":
+        dst, n_out = np.concatenate([np.arange(0, 50), np.arange(52, 120)]), 130
+    elif case == "pair_at_tile_edge":
+        dst, n_out = np.concatenate([np.arange(0, 64), [63], np.arange(64, 100)]), 100
+    elif case == "distinct_out_of_range":
+        dst = np.arange(-3, 140)
     else:
         dst = np.repeat(np.arange(0, 40, 3), 7)
         indptr = np.array([5, 20, 20, 61], dtype=np.int32)   # edges 5..60 only

@@ -126,6 +126,34 @@ def test_edge_softmax_fwd_bwd(fa, dev, name, heads):
                "backward_csr_edge_softmax")
 
 
+@pytest.mark.parametrize("layout", ["tiles", "wide", "mixed"])
+@pytest.mark.parametrize("heads", [1, 2, 8])
+def test_edge_softmax_tiles(fa, dev, layout, heads):
+    """Many segments per launch: empty segments among short ones, edges before the first
+    offset and after the last (zeros), runs of long segments (40 and 70 edges) and both
+    kinds in one launch; forward (both forms) and backward."""
+    rng = np.random.default_rng(heads + len(layout))
+    if layout == "tiles":
+        deg = rng.integers(0, 21, size=1000)
+    elif layout == "wide":
+        deg = np.full(600, 40)
+    else:   # tiles of short and of long segments in turn
+        deg = np.concatenate([rng.integers(0, 8, size=256), np.full(256, 70),
+                              rng.integers(0, 8, size=300)])
+    indptr = np.concatenate([[7], 7 + np.cumsum(deg)]).astype(np.int32)
+    E = int(indptr[-1]) + 5
+    x = (rng.standard_normal((E, heads)) * 3).astype(np.float32)
+    dy = rng.standard_normal((E, heads)).astype(np.float32)
+    ti, tx = torch.from_numpy(indptr).to(dev), torch.from_numpy(x).to(dev)
+    for mode, fwd in ((0, fa.forward_edge_softmax), (1, fa.forward_csr_edge_softmax)):
+        y = fwd(ti, ti, tx, 512, heads)[0] if mode == 0 else fwd(ti, ti, tx, 32, 16)[0]
+        assert_rel(y, C.edge_softmax_fwd(indptr, x, heads, mode), 1e-6, f"forward mode {mode}")
+        assert not y[:7].any() and not y[-5:].any()
+    dx = fa.backward_edge_softmax(ti, ti, torch.from_numpy(dy).to(dev), y, 512, heads)[0]
+    assert_rel(dx, C.edge_softmax_bwd(indptr, dy, y.cpu().numpy(), heads), 1e-6, "backward")
+    assert not dx[:7].any() and not dx[-5:].any()
+
+
 def test_edge_softmax_partial_heads(fa, dev):
     """num_heads below the input width: only the first num_heads columns (edge_softmax.cu:66)."""
     indptr, dst = _csr([3, 4, 0, 2])

@@ -1145,7 +1145,7 @@ struct PairBwd {
   float mh[H], il[H], T[H];   // row max, 1 / softmax denominator, dxbar . xbar
 };
 
-template <int H, int NS, bool BF>
+template <int H, int NS, bool BF, bool DN>
 __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx<NS>& L,
                                               const EdgeMeta<H, true>& M, int64_t c0, int p,
                                               int cnt, const float2* twb, float* tc, float* ts,
@@ -1198,7 +1198,7 @@ __device__ __forceinline__ void pair_bwd_step(const TgatParams& P, const PairCtx
     fma4(S.dq[h][NS - 1], bias_dz(P, L.bias_lane, sc, dz[h]), x[NS - 1]);
   }
   // node-row gradient of this half's edge: dx = sum_h ad_h dxbar_h + dz_h q~_h
-  if (P.d_node) {
+  if (DN && P.d_node) {
     float* drow = P.d_node + (c0 + jj) * P.ld_dnode;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
@@ -1238,10 +1238,16 @@ __device__ __forceinline__ float4 pick_f4(const float4& v, int j) {
 #ifndef FA_PAIR_BWD_WAVES
 #define FA_PAIR_BWD_WAVES 3
 #endif
-constexpr int pair_bwd_min_waves(int H, int NS) { return H * NS >= 6 ? FA_PAIR_BWD_WAVES : 4; }
+#ifndef FA_PAIR_BWD_WAVES_NODN
+#define FA_PAIR_BWD_WAVES_NODN 4
+#endif
+constexpr int pair_bwd_min_waves(int H, int NS, bool DN) {
+  return H * NS >= 6 ? (DN ? FA_PAIR_BWD_WAVES : FA_PAIR_BWD_WAVES_NODN) : 4;
+}
 
-template <int H, int NS, bool BF>
-__global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pair(TgatParams P) {
+// DN: the node-row gradient is written (else P.d_node is null and its code is left out).
+template <int H, int NS, bool BF, bool DN>
+__global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS, DN)) void tgat_bwd_pair(TgatParams P) {
   constexpr int QS = NS * kHalf + 1;
   extern __shared__ float lds[];
   const int wave = uniform(threadIdx.x / kWave);
@@ -1336,9 +1342,9 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS)) void tgat_bwd_pa
       // next pair's loads issued unconditionally (see the forward)
       for (int p = 0; p < np; p += 2) {
         pair_rows<NS, H, true, BF>(P, L, M, p + 1, cnt, xb);
-        pair_bwd_step<H, NS, BF>(P, L, M, c0, p, cnt, twb, tc, ts, qs, gs, xa, S);
+        pair_bwd_step<H, NS, BF, DN>(P, L, M, c0, p, cnt, twb, tc, ts, qs, gs, xa, S);
         pair_rows<NS, H, true, BF>(P, L, M, p + 2, cnt, xa);
-        if (p + 1 < np) pair_bwd_step<H, NS, BF>(P, L, M, c0, p + 1, cnt, twb, tc, ts, qs, gs, xb, S);
+        if (p + 1 < np) pair_bwd_step<H, NS, BF, DN>(P, L, M, c0, p + 1, cnt, twb, tc, ts, qs, gs, xb, S);
       }
       c0 += kWave;
       if (c0 >= e1) break;
@@ -1830,6 +1836,12 @@ size_t pair_bwd_lds_bytes(const TgatParams& P, int heads) {
 
 int bwd_grid(int64_t n_dst) { return stride_grid(n_dst); }
 
+template <int H, int NS>
+auto pair_bwd_kernel(const TgatParams& P) -> void (*)(TgatParams) {
+  if (P.d_node) return pair_bf16(P) ? tgat_bwd_pair<H, NS, true, true> : tgat_bwd_pair<H, NS, false, true>;
+  return pair_bf16(P) ? tgat_bwd_pair<H, NS, true, false> : tgat_bwd_pair<H, NS, false, false>;
+}
+
 // `grid` returns the workgroups launched (rows of the time-gradient partials).
 template <int H>
 int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
@@ -1847,9 +1859,9 @@ int launch_bwd_h(const TgatParams& P, int& grid, hipStream_t stream) {
     const int pns = static_cast<int>(ceil_div(P.cp, kHalf));
     lds = pair_bwd_lds_bytes(P, H);
     switch (pns) {
-      case 1: k = pair_bf16(P) ? tgat_bwd_pair<H, 1, true> : tgat_bwd_pair<H, 1, false>; break;
-      case 2: k = pair_bf16(P) ? tgat_bwd_pair<H, 2, true> : tgat_bwd_pair<H, 2, false>; break;
-      default: k = pair_bf16(P) ? tgat_bwd_pair<H, 3, true> : tgat_bwd_pair<H, 3, false>; break;
+      case 1: k = pair_bwd_kernel<H, 1>(P); break;
+      case 2: k = pair_bwd_kernel<H, 2>(P); break;
+      default: k = pair_bwd_kernel<H, 3>(P); break;
     }
   }
   grid = persistent_grid(P.n_dst, reinterpret_cast<const void*>(k), lds);

@@ -408,7 +408,7 @@ std::vector<at::Tensor> backward_fused_attn(at::Tensor d_output, at::Tensor V_va
   c10::hip::HIPGuardMasqueradingAsCUDA guard(output.device());
   const int64_t E = output.size(0), H = num_heads, dh = V_val.size(2);
   auto d_input = at::zeros({E, H}, output.options());
-  auto grad_V = at::zeros({E, H, dh}, output.options());
+  auto grad_V = at::empty({E, H, dh}, output.options());   // every row is written by the call
   const size_t sb = fa_fused_attn_bwd_scratch_bytes();
   auto scratch = at::empty({static_cast<int64_t>(sb)}, output.options().dtype(at::kByte));
   const int st = fa_fused_attn_bwd_f32(

@@ -174,6 +174,25 @@ __device__ __forceinline__ float4 chunk_load(rsrc_t r, uint32_t off) {
                      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
 }
 
+template <bool VEC>
+__device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4& x) {
+  if (VEC) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 w4;
+    w4[0] = __float_as_uint(x.x);
+    w4[1] = __float_as_uint(x.y);
+    w4[2] = __float_as_uint(x.z);
+    w4[3] = __float_as_uint(x.w);
+    __builtin_amdgcn_raw_buffer_store_b128(w4, r, static_cast<int>(off), 0, 0);
+    return;
+  }
+  const int o = static_cast<int>(off);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
+}
+
 __device__ __forceinline__ int64_t lane_i64(int64_t v, int j) {
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffff), j));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), j));
@@ -218,14 +237,18 @@ __device__ __forceinline__ float pick(const float (&w)[H], int h) {
   return r;
 }
 
-// keep factor of a kept entry: 1/(1-p) in double, as fused_attention.cu:285-287
-__device__ __forceinline__ float drop_weight(float a, float m, float p) {
-  return m > p ? static_cast<float>(static_cast<double>(a) / (1.0 - static_cast<double>(p))) : 0.f;
+// A kept entry's weight a/(1-p), formed in double as fused_attention.cu:285-287 does, with
+// the division by 1-p taken once per kernel: a * keep with keep = 1/(1-p) in double (the two
+// double results differ by at most an ulp of double, far below float's rounding).
+__device__ __forceinline__ double keep_scale(float p) { return 1.0 / (1.0 - static_cast<double>(p)); }
+__device__ __forceinline__ float drop_weight(float a, float m, float p, double keep) {
+  return m > p ? static_cast<float>(static_cast<double>(a) * keep) : 0.f;
 }
 
 template <int H, int NS, bool VEC>
 __global__ __launch_bounds__(kBlock) void fused_attn_fwd_k(FaParams P) {
   const int lane = lane_id();
+  const double keep = keep_scale(P.p);
   ChunkHeads<NS> C;
   chunk_heads<NS>(P, C);
   const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -269,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_k(FaParams P) {
       for (int h = 0; h < H; ++h) {
         const float a = expf(leaky(P.score[e * H + h], P.slope) - mx[h]) / sm[h];
         if (in) P.attn[e * H + h] = a;
-        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p) : a;
+        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p, keep) : a;
       }
       const int64_t my_src = P.src[e];
       if (!write_out || P.dim == 0) continue;
@@ -324,6 +347,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_k(FaParams P) {
 template <int H, bool VEC>
 __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
   const int lane = lane_id();
+  const double keep = keep_scale(P.p);
   const int half = lane >> 5, hl = lane & (kHalf - 1);
   int hc[4];   // head of each component of this lane's chunk (-1 past dim)
 #pragma unroll
@@ -367,12 +391,13 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
     const int64_t src0 = P.src[e00];
     float4 r[kRows];
     if (write_out) issue(src0, 0, cnt0, r);
-    float mx[H], sm[H];
+    float mx[H], sm[H], ex0[H];   // ex0: exp(l - max) of the first block, formed once
     if (le - lb <= kWave) {   // one block: the statistics from the registers
 #pragma unroll
       for (int h = 0; h < H; ++h) {
         mx[h] = wave_max(l0[h]);
-        sm[h] = wave_sum(in0 ? expf(l0[h] - mx[h]) : 0.f);
+        ex0[h] = expf(l0[h] - mx[h]);
+        sm[h] = wave_sum(in0 ? ex0[h] : 0.f);
       }
     } else {
 #pragma unroll
@@ -393,6 +418,8 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
           sm[h] += wave_sum(v);
         }
       }
+#pragma unroll
+      for (int h = 0; h < H; ++h) ex0[h] = expf(l0[h] - mx[h]);
     }
     float4 acc = f4_zero();
     for (int64_t e0 = lb; e0 < le; e0 += kWave) {
@@ -403,10 +430,10 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
       float w[H];
 #pragma unroll
       for (int h = 0; h < H; ++h) {
-        const float l = first ? l0[h] : leaky(P.score[e * H + h], P.slope);
-        const float a = expf(l - mx[h]) / sm[h];
+        const float ex = first ? ex0[h] : expf(leaky(P.score[e * H + h], P.slope) - mx[h]);
+        const float a = ex / sm[h];
         if (in) P.attn[e * H + h] = a;
-        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p) : a;
+        w[h] = P.mask ? drop_weight(a, P.mask[e * H + h], P.p, keep) : a;
         w[h] = in ? w[h] : 0.f;
       }
       if (!write_out) continue;
@@ -562,15 +589,50 @@ __global__ __launch_bounds__(64) void own_flag_set(int* flag) {
   if (threadIdx.x == 0) flag[0] = 1;
 }
 
+// Clears the flag unless every in-range V row is its own edge's and the segment offsets
+// never decrease (so no edge lies in two segments and each row has at most one writer).
 __global__ __launch_bounds__(kBlock) void check_own_rows(const int64_t* src, int64_t n_edges,
                                                          int64_t n_dst, int64_t n_v,
-                                                         int64_t n_src, int* flag) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < n_edges;
-       e += static_cast<int64_t>(gridDim.x) * kBlock) {
+                                                         int64_t n_src, const int32_t* indptr,
+                                                         int64_t n_seg, int* flag) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; e < n_edges; e += stride) {
     const int64_t sr = src[e];
     const int64_t row = sr - n_dst;
     if (row >= 0 && row < n_v && sr < n_src && row != e) flag[0] = 0;
   }
+  for (int64_t s = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; s < n_seg; s += stride)
+    if (indptr[s + 1] < indptr[s]) flag[0] = 0;
+}
+
+// The grad_V rows the backward does not store: every row when the rows are not each edge's
+// own (the atomic adds then start from zeros), else the rows of the edges outside
+// [indptr[0], indptr[n_seg]) (the backward stores every row inside, zeros for the edges
+// that contribute nothing). `own` NULL: every row.
+__global__ __launch_bounds__(kBlock) void grad_v_fill(const int* own, const int32_t* indptr,
+                                                      int64_t n_seg, int64_t n_edges, int64_t n_v,
+                                                      int64_t dim, float* grad_V) {
+  int64_t a = 0, b = 0;   // rows [a, b) are stored by the backward
+  if (own && own[0] != 0) {
+    a = indptr[0];
+    b = indptr[n_seg];
+    a = a < 0 ? 0 : (a > n_edges ? n_edges : a);
+    b = b < a ? a : (b > n_edges ? n_edges : b);
+    a = a > n_v ? n_v : a;
+    b = b > n_v ? n_v : b;
+  }
+  const int64_t head = a * dim, tail = (n_v - b) * dim;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  const bool vec = (dim & 3) == 0 && (reinterpret_cast<uintptr_t>(grad_V) & 15) == 0;
+  if (vec) {
+    float4* g4 = reinterpret_cast<float4*>(grad_V);
+    const int64_t h4 = head / 4, t4 = tail / 4, b4 = b * dim / 4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < h4 + t4; i += stride)
+      g4[i < h4 ? i : i - h4 + b4] = f4_zero();
+    return;
+  }
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < head + tail; i += stride)
+    grad_V[i < head ? i : i - head + b * dim] = 0.f;
 }
 
 // Backward for rows of at most 32 float4 chunks, in the half-wave layout of
@@ -618,7 +680,16 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
     le = le > P.n_edges ? P.n_edges : le;
     if (le <= lb) continue;
     const int64_t d = P.dst[lb];
-    if (d < 0 || d >= P.n_dst) continue;
+    if (d < 0 || d >= P.n_dst) {
+      // no gradient flows through this segment; with own rows its edges' rows are zeros
+      if (own)
+        for (int64_t j = lb + half; j < le; j += 2) {
+          const rsrc_t wr = row_rsrc(P.grad_V + (j < P.n_v ? j : 0) * P.dim,
+                                     j < P.n_v ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+          store_chunk<VEC>(wr, coff, f4_zero());
+        }
+      continue;
+    }
     const bool one = le - lb <= kWave;
     float4 g;   // this lane's chunk of the destination's dout row
     {
@@ -684,23 +755,13 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
           const int64_t row = row_of(my_src, j0, cnt);
           const float4 gv = make_float4(cx[0], cx[1], cx[2], cx[3]);
           if (own) {
-            const rsrc_t wr = row_rsrc(P.grad_V + (row >= 0 ? row : 0) * P.dim,
-                                       row >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
-            if (VEC) {
-              typedef unsigned int u4 __attribute__((ext_vector_type(4)));
-              u4 w4;
-              w4[0] = __float_as_uint(gv.x);
-              w4[1] = __float_as_uint(gv.y);
-              w4[2] = __float_as_uint(gv.z);
-              w4[3] = __float_as_uint(gv.w);
-              __builtin_amdgcn_raw_buffer_store_b128(w4, wr, static_cast<int>(coff), 0, 0);
-            } else {
-              const int o = static_cast<int>(coff);
-              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.x), wr, o, 0, 0);
-              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.y), wr, o + 4, 0, 0);
-              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.z), wr, o + 8, 0, 0);
-              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(gv.w), wr, o + 12, 0, 0);
-            }
+            // an edge without a V row in range still owns grad_V row e (no other edge
+            // writes it): zeros there
+            const int64_t eh = e0 + j0 + half;
+            const int64_t wrow = row >= 0 ? row : (j0 + half < cnt && eh < P.n_v ? eh : -1);
+            const rsrc_t wr = row_rsrc(P.grad_V + (wrow >= 0 ? wrow : 0) * P.dim,
+                                       wrow >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
+            store_chunk<VEC>(wr, coff, row >= 0 ? gv : f4_zero());
           } else {
             *reinterpret_cast<float4*>(stage + 4 * hl) = gv;
             lds_sync();
@@ -821,25 +882,40 @@ extern "C" int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const
   if (n_seg < 0 || n_edges < 0 || n_dst < 0 || heads < 0 || dh < 0) return FA_EINVAL;
   if (heads > kWave) return FA_EUNSUPPORTED;
   if (scratch && scratch_bytes < fa_fused_attn_bwd_scratch_bytes()) return FA_ESCRATCH;
-  if (n_seg == 0 || heads == 0) return FA_OK;
+  if (heads == 0) return FA_OK;
+  const int64_t dim = static_cast<int64_t>(heads) * dh;
+  auto fill = [&](const int* own) {   // every grad_V row the kernels below do not store
+    const int64_t n4 = ceil_div(n_edges * dim, 4 * kBlock);
+    const unsigned grid = static_cast<unsigned>(n4 < 1 ? 1 : (n4 > 2048 ? 2048 : n4));
+    hipLaunchKernelGGL(grad_v_fill, dim3(grid), dim3(kBlock), 0, stream, own, indptr, n_seg,
+                       n_edges, n_edges, dim, grad_V);
+  };
+  if (n_seg == 0) {   // no segment: grad_V is zeros
+    if (dim > 0 && n_edges > 0 && grad_V) {
+      fill(nullptr);
+      return launch_status();
+    }
+    return FA_OK;
+  }
   if (!indptr || !dst || !src || !attn || !d_act || (dh > 0 && (!V || !dout || !grad_V)))
     return FA_EINVAL;
-  if (static_cast<int64_t>(heads) * dh <= 4 * kWave * 4) {
+  if (dim <= 4 * kWave * 4 && (heads == 1 || heads == 2 || heads == 4 || heads == 8)) {
     int* own = nullptr;
-    if (scratch && dh > 0 && heads * dh <= 4 * kHalf) {   // the half-wave backward reads it
+    if (scratch && dh > 0 && dim <= 4 * kHalf) {   // the half-wave backward reads it
       own = static_cast<int*>(scratch);
       hipLaunchKernelGGL(own_flag_set, dim3(1), dim3(64), 0, stream, own);
-      const int64_t want = ceil_div(n_edges, kBlock);
+      const int64_t want = ceil_div(n_edges > n_seg ? n_edges : n_seg, kBlock);
       const unsigned grid = static_cast<unsigned>(want < 1 ? 1 : (want > 1024 ? 1024 : want));
       hipLaunchKernelGGL(check_own_rows, dim3(grid), dim3(kBlock), 0, stream, src, n_edges, n_dst,
-                         n_edges, n_src, own);
+                         n_edges, n_src, indptr, n_seg, own);
     }
+    if (dh > 0) fill(own);
     FaParams P{indptr, n_seg, dst, src, n_edges, n_dst, n_src, n_edges, nullptr, V, mask, attn,
                dout, dh, heads * dh, static_cast<int>(ceil_div(heads * dh, 4)), 0.f, p, nullptr,
                nullptr, d_act, grad_V, own};
-    const int st = launch_fa_heads(P, heads, true, stream);
-    if (st != -1000) return st;
+    return launch_fa_heads(P, heads, true, stream);
   }
+  if (dh > 0) fill(nullptr);
   hipLaunchKernelGGL(fused_attn_bwd_generic, dim3(ceil_div(n_seg, kWavesPerBlock)), dim3(kBlock), 0,
                      stream, indptr, n_seg, dst, src, n_edges, n_dst, n_src, dout, V, n_edges,
                      attn, mask, heads, dh, p, d_act, grad_V);

@@ -166,10 +166,14 @@ int fa_fused_attn_fwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* d
  *   grad_V[src[e]-n_dst,h,:] = attn*keep*dout[dst,h,:]
  *   d_act[e,h] = attn*(da - sum_s attn*da), da = keep * dout[dst,h,:].V[...]
  * i.e. the gradient with respect to the LeakyReLU *output*; the caller applies
- * leaky_relu'(score). grad_V must be zeroed by the caller; it is accumulated with atomics,
- * except that with scratch (fa_fused_attn_bwd_scratch_bytes() bytes, or NULL) and rows of
- * at most 128 values, a device check that every in-range V row is its own edge's
- * (src[e] - n_dst == e, the sampler's layout) lets each row be stored once instead.
+ * leaky_relu'(score). Every row of grad_V [n_edges][heads*dh] is written (it need not be
+ * zeroed): rows no edge contributes to are zeros. It is accumulated with atomics after a
+ * zero fill, except that with scratch (fa_fused_attn_bwd_scratch_bytes() bytes, or NULL),
+ * heads in {1, 2, 4, 8} and rows of at most 128 values, a device check that every in-range
+ * V row is its own edge's (src[e] - n_dst == e, the sampler's layout) and that the segment
+ * offsets never decrease lets each row be stored once instead (zeros for the rows of edges
+ * outside the segments, of segments whose destination is out of range and of edges whose
+ * source is out of range), with no fill in front.
  * Replaces backward_fused_attn_cuda (fused_attention.cu:139-200, 330-446). */
 size_t fa_fused_attn_bwd_scratch_bytes(void);
 int fa_fused_attn_bwd_f32(const int32_t* indptr, int64_t n_seg, const int64_t* dst,

@@ -371,6 +371,53 @@ def test_fused_attn(fa, dev, p, H, dh, rows):
     assert_rel(gV, gV_ref, FP32_TOL, "fused grad_V")
 
 
+@pytest.mark.parametrize("case", ["offset", "bad_dst", "bad_src", "decreasing", "no_segments"])
+@pytest.mark.parametrize("dh", [50, 127, 100])
+def test_fused_attn_bwd_writes_every_row(fa, dev, case, dh):
+    """backward_fused_attn's grad_V comes back without a prior zero fill: with each V row
+    its own edge's, rows are stored once, zeros for the edges before the first segment and
+    after the last, for segments whose destination is out of range and for edges whose
+    source is out of range; offsets that decrease turn the row stores off (atomic adds into
+    zeros). The memory handed back was filled with NaN by an earlier tensor, so a row left
+    unwritten shows."""
+    H = 2
+    deg = [3, 0, 5, 2, 7, 1, 4, 9]
+    indptr, dst = _csr(deg)
+    N = len(deg)
+    lead, trail = (3, 4) if case == "offset" else (0, 0)
+    E = lead + dst.size + trail
+    indptr = (indptr + lead).astype(np.int32)
+    dst = np.concatenate([np.zeros(lead, np.int64), dst, np.zeros(trail, np.int64)])
+    src = np.arange(N, N + E, dtype=np.int64)
+    if case == "bad_dst":
+        dst[indptr[1]:indptr[2]] = -1       # the second non-empty segment's destination
+        dst[indptr[3]:indptr[4]] = N + 5
+    elif case == "bad_src":
+        src[4] = N + E + 3                  # past n_src
+        src[9] = 2                          # below n_dst
+    elif case == "decreasing":
+        indptr = np.concatenate([indptr[:4], [2]]).astype(np.int32)
+    elif case == "no_segments":
+        indptr = indptr[:1]
+    rng = np.random.default_rng(dh + len(case))
+    score = rng.standard_normal((E, H)).astype(np.float32)
+    V = rng.standard_normal((E, H, dh)).astype(np.float32)
+    dout = rng.standard_normal((N, H * dh)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    out, attn, mask = fa.forward_fused_attn(t(score), t(V), t(indptr), t(indptr), t(dst), t(src),
+                                            N, H, 0.2, 0.3)
+    d_ref, gV_ref = C.fused_attn_bwd(indptr, dst, src, N, N + E, dout, V, attn.cpu().numpy(),
+                                     mask.cpu().numpy(), 0.3)
+    for _ in range(2):
+        junk = torch.full((E * H * dh + 4096,), float("nan"), device=dev)
+        del junk
+        d_act, gV = fa.backward_fused_attn(t(dout), t(V), attn, mask, t(indptr), t(indptr),
+                                           t(dst), t(src), N + E, H, 0.2, 0.3)
+        assert torch.isfinite(gV).all(), "grad_V rows left unwritten"
+        assert_rel(gV, gV_ref, FP32_TOL, f"grad_V {case}")
+        assert_rel(d_act, d_ref, FP32_TOL, f"d_act {case}")
+
+
 def test_inputs_must_be_on_gpu(fa):
     x = torch.zeros(4, 2)
     ip = torch.tensor([0, 2, 4], dtype=torch.int32)

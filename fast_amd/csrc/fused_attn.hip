@@ -734,10 +734,12 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
           }
           const float gx[4] = {g.x, g.y, g.z, g.w};
           const float vx[4] = {r[b].x, r[b].y, r[b].z, r[b].w};
-          float cx[4];
+          float cx[4], ak[H];
+#pragma unroll
+          for (int h = 0; h < H; ++h) ak[h] = ab[h] * kb[h];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            cx[i] = pick<H>(ab, hc[i]) * pick<H>(kb, hc[i]) * gx[i];
+            cx[i] = pick<H>(ak, hc[i]) * gx[i];
 #pragma unroll
             for (int h = 0; h < H; ++h) part[h] = hc[i] == h ? fmaf(gx[i], vx[i], part[h]) : part[h];
           }

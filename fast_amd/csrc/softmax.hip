@@ -143,8 +143,10 @@ __global__ __launch_bounds__(kBlock) void seg_softmax_fwd_rows(const int32_t* in
     mx = row_reduce<H, W, true>(mx);
     float sum = 0.f;
 #pragma unroll
-    for (int c = 0; c < kRowCache; ++c)
-      if (l + W * c < g.n) sum += expf(v[c] - mx);
+    for (int c = 0; c < kRowCache; ++c) {   // the cached values become their exponentials
+      v[c] = expf(v[c] - mx);
+      if (l + W * c < g.n) sum += v[c];
+    }
     for (int64_t i = l + W * kRowCache; i < g.n; i += W) sum += expf(xs[i] - mx);
     sum = row_reduce<H, W, false>(sum);
     const float inv = 1.f / sum;
@@ -152,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void seg_softmax_fwd_rows(const int32_t* in
 #pragma unroll
     for (int c = 0; c < kRowCache; ++c) {
       const int64_t i = l + W * c;
-      if (i < g.n) ys[i] = MODE == 0 ? expf(v[c] - mx) * inv : expf(v[c] - mx) / sum;
+      if (i < g.n) ys[i] = MODE == 0 ? v[c] * inv : v[c] / sum;
     }
     for (int64_t i = l + W * kRowCache; i < g.n; i += W)
       ys[i] = MODE == 0 ? expf(xs[i] - mx) * inv : expf(xs[i] - mx) / sum;

@@ -153,6 +153,12 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_generic(const int32_t* 
 // (4c + i) / dh.
 // ---------------------------------------------------------------------------------
 constexpr int kRows = 8;
+// Pairs of rows in flight per wave in the half-wave kernels (FA_FA_PAIR_ROWS pairs: two
+// rows per load instruction).
+#ifndef FA_FA_PAIR_ROWS
+#define FA_FA_PAIR_ROWS 4
+#endif
+constexpr int kPairRows = FA_FA_PAIR_ROWS;
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 
 __device__ __forceinline__ rsrc_t row_rsrc(const float* base, uint32_t bytes) {
@@ -356,13 +362,13 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
     hc[i] = col < P.dim ? col / P.dh : -1;
   }
   const uint32_t coff = 16u * static_cast<uint32_t>(hl);   // past the row for hl >= chunks
-  static_assert(kWave % (2 * kRows) == 0, "pairs stay inside a 64-edge block");
-  // V chunks of this half's edges of pairs j/2 .. j/2 + kRows - 1 of a block (entry
+  static_assert(kWave % (2 * kPairRows) == 0, "pairs stay inside a 64-edge block");
+  // V chunks of this half's edges of pairs j/2 .. j/2 + kPairRows - 1 of a block (entry
   // j + 2b + half; j + 2b is even, so a pair's lanes lie in the block; entries past cnt get
   // an empty descriptor)
-  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kRows]) {
+  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kPairRows]) {
 #pragma unroll
-    for (int b = 0; b < kRows; ++b) {
+    for (int b = 0; b < kPairRows; ++b) {
       const int j0 = j + 2 * b;
       const int64_t s0 = lane_i64(my_src, j0), s1 = lane_i64(my_src, j0 + 1);
       const int64_t row = (half ? s1 : s0) - P.n_dst;
@@ -389,7 +395,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
 #pragma unroll
     for (int h = 0; h < H; ++h) l0[h] = in0 ? leaky(P.score[e00 * H + h], P.slope) : kMaxSeed;
     const int64_t src0 = P.src[e00];
-    float4 r[kRows];
+    float4 r[kPairRows];
     if (write_out) issue(src0, 0, cnt0, r);
     float mx[H], sm[H], ex0[H];   // ex0: exp(l - max) of the first block, formed once
     if (le - lb <= kWave) {   // one block: the statistics from the registers
@@ -438,10 +444,10 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
       }
       if (!write_out) continue;
       const int64_t my_src = first ? src0 : P.src[e];
-      for (int j = 0; j < cnt; j += 2 * kRows) {
+      for (int j = 0; j < cnt; j += 2 * kPairRows) {
         if (!(first && j == 0)) issue(my_src, j, cnt, r);
 #pragma unroll
-        for (int b = 0; b < kRows; ++b) {
+        for (int b = 0; b < kPairRows; ++b) {
           if (j + 2 * b >= cnt) break;
           const int j0 = j + 2 * b;
           float wb[H];
@@ -656,7 +662,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
   const uint32_t coff = 16u * static_cast<uint32_t>(hl);
   const float keep = static_cast<float>(1.0 / (1.0 - static_cast<double>(P.p)));
   const bool own = P.own && P.own[0] != 0;
-  static_assert(kWave % (2 * kRows) == 0, "pairs stay inside a 64-edge block");
+  static_assert(kWave % (2 * kPairRows) == 0, "pairs stay inside a 64-edge block");
   // this half's row of pair entry j0 (-1 when missing or out of range)
   auto row_of = [&](int64_t my_src, int j0, int cnt) -> int64_t {
     const int64_t s0 = lane_i64(my_src, j0), s1 = lane_i64(my_src, j0 + 1);
@@ -664,9 +670,9 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
     const int64_t row = sr - P.n_dst;
     return (j0 + half < cnt && row >= 0 && row < P.n_v && sr < P.n_src) ? row : -1;
   };
-  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kRows]) {
+  auto issue = [&](int64_t my_src, int j, int cnt, float4 (&r)[kPairRows]) {
 #pragma unroll
-    for (int b = 0; b < kRows; ++b) {
+    for (int b = 0; b < kPairRows; ++b) {
       const int64_t row = row_of(my_src, j + 2 * b, cnt);
       const rsrc_t rr = row_rsrc(P.V + (row >= 0 ? row : 0) * P.dim, row >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
       r[b] = chunk_load<VEC>(rr, coff);
@@ -714,11 +720,11 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
         da[h] = 0.f;
       }
       const int64_t my_src = P.src[e];
-      float4 r[kRows];
-      for (int j = 0; j < cnt; j += 2 * kRows) {
+      float4 r[kPairRows];
+      for (int j = 0; j < cnt; j += 2 * kPairRows) {
         issue(my_src, j, cnt, r);
 #pragma unroll
-        for (int b = 0; b < kRows; ++b) {
+        for (int b = 0; b < kPairRows; ++b) {
           if (j + 2 * b >= cnt) break;
           const int j0 = j + 2 * b;
           float ab[H], kb[H], part[H];

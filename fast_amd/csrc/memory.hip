@@ -140,6 +140,18 @@ __global__ __launch_bounds__(kEltBlock) void time_rows(const float* ts, const fl
                                                        int64_t n, const float* w, const float* b,
                                                        int32_t dt, float* out, int64_t ld) {
   const int64_t total = n * dt;
+  if (total <= 0xffffffffLL) {   // 32-bit index arithmetic (no 64-bit division per element)
+    const uint32_t tot = static_cast<uint32_t>(total), d = static_cast<uint32_t>(dt);
+    const uint32_t stride = gridDim.x * kEltBlock;
+    for (uint32_t idx = blockIdx.x * kEltBlock + threadIdx.x; idx < tot; idx += stride) {
+      const uint32_t i = idx / d;
+      const uint32_t j = idx - i * d;
+      const float t = mem_ts ? ts[i] - mem_ts[i] : ts[i];
+      out[static_cast<int64_t>(i) * ld + j] = cos_time(t, w[j], b[j]);
+      if (idx > tot - stride) break;   // the next index would wrap past 2^32
+    }
+    return;
+  }
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kEltBlock + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * kEltBlock) {
     const int64_t i = idx / dt;

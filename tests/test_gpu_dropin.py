@@ -128,7 +128,7 @@ def test_edge_softmax_fwd_bwd(fa, dev, name, heads):
 
 @pytest.mark.parametrize("layout", ["tiles", "wide", "mixed"])
 @pytest.mark.parametrize("heads", [1, 2, 8])
-def test_edge_softmax_tiles(fa, dev, layout, heads):
+def test_edge_softmax_many_segments(fa, dev, layout, heads):
     """Many segments per launch: empty segments among short ones, edges before the first
     offset and after the last (zeros), runs of long segments (40 and 70 edges) and both
     kinds in one launch; forward (both forms) and backward."""

@@ -276,6 +276,10 @@ constexpr int copy_rows(int ns) { return ns <= 4 ? 4 : 2; }
 template <int NS, bool VEC>
 __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* flag) {
   constexpr int RR = run_rows(NS);
+  // the source ids of the wave's current tile, read by the lanes of whichever half-wave
+  // takes a run (LDS reads do not depend on the other half being active)
+  __shared__ int64_t tile_src[kWavesPerBlock][kWave];
+  const int wv = threadIdx.x / kWave;
   const int lane = lane_id();
   const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
   const int64_t waves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -302,6 +306,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
     const int64_t up = lane_i64_from(my, lane > 0 ? lane - 1 : 0);
     const bool start = lane < cnt && (lane == 0 ? (e0 == lo || my != prev_tile) : my != up);
     uint64_t m = __ballot(start);
+    const int64_t tsrc = P.src[e0 + (lane < cnt ? lane : cnt - 1)];
     {
       // Every edge of the tile a run of its own (the last one too) and no gap below any of
       // them: each output row is one source row, copied by half-waves, kCopyRows rows in
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
       const bool gap = lane < cnt && prev != kNoIndex && my != kNoIndex && my - 1 > prev;
       if (m == all && __ballot(gap) == 0 && (!has_next || next != last)) {
         constexpr int R = copy_rows(NS);
-        const int64_t ids = P.src[e0 + (lane < cnt ? lane : cnt - 1)];
+        const int64_t ids = tsrc;
         for (int j = 0; j < cnt; j += 2 * R) {
           float4 r[R][NS];
 #pragma unroll
@@ -346,6 +351,10 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
         continue;
       }
     }
+    lds_sync();   // the previous tile's reads of tile_src are done
+    tile_src[wv][lane] = tsrc;
+    lds_sync();
+    const int64_t tile_end = e0 + cnt;
     while (m) {
       // two runs: bit b0 for the first half-wave, b1 (if any) for the second
       const int b0 = __builtin_ctzll(m);
@@ -384,13 +393,19 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
         for (int k = 0; k < NS; ++k) acc[k] = f4_zero();
         for (int64_t eb = e0 + b; eb < end; eb += kHalf) {
           const int n = static_cast<int>(end - eb < kHalf ? end - eb : kHalf);
-          const int64_t ids = P.src[eb + (hl < n ? hl : 0)];  // this half's next 32 source ids
+          // edges inside the tile take their ids from tile_src; the tile's last run, where it
+          // goes on past the tile, loads this half's next 32 source ids
+          const bool in_tile = eb + n <= tile_end;
+          const int64_t ids = in_tile ? 0 : P.src[eb + (hl < n ? hl : 0)];
           for (int j = 0; j < n; j += RR) {
             float4 r[RR][NS];
 #pragma unroll
             for (int q = 0; q < RR; ++q) {
+              const int jj = j + q < n ? j + q : 0;
+              const int64_t from_tile = tile_src[wv][in_tile ? static_cast<int>(eb - e0) + jj : 0];
               // permutes stay inside this half-wave, whose lanes are all active
-              const int64_t sidx = lane_i64_from(ids, half * kHalf + (j + q < n ? j + q : 0));
+              const int64_t from_ids = lane_i64_from(ids, half * kHalf + jj);
+              const int64_t sidx = in_tile ? from_tile : from_ids;
               const bool ok = j + q < n && sidx >= 0 && sidx < P.n_x;
               const rsrc_t rr = row_rsrc(P.x + (ok ? sidx : 0) * P.ldx, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
 #pragma unroll

@@ -103,8 +103,13 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
                                            static_cast<int>(bytes), kRsrcWord3);
 }
 
+// AUX: the cache-policy bits of the access; kStream (non-temporal) marks the per-destination
+// K-space rows, read or written once per launch, so that they leave the caches first and
+// the gathered table rows, which repeat, stay.
+constexpr int kStream = 2;
+template <int AUX = 0>
 __device__ __forceinline__ float4 bload4(rsrc_t r, uint32_t off) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, AUX);
   return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                      __uint_as_float(v[3]));
 }
@@ -158,6 +163,7 @@ __device__ __forceinline__ void bstore4_dwords(rsrc_t r, uint32_t off, const flo
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
 }
 
+template <int AUX = 0>
 __device__ __forceinline__ void bstore4(rsrc_t r, uint32_t off, const float4& x) {
   typedef unsigned int u4 __attribute__((ext_vector_type(4)));
   u4 v;
@@ -165,7 +171,7 @@ __device__ __forceinline__ void bstore4(rsrc_t r, uint32_t off, const float4& x)
   v[1] = __float_as_uint(x.y);
   v[2] = __float_as_uint(x.z);
   v[3] = __float_as_uint(x.w);
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, AUX);
 }
 
 __device__ __forceinline__ int64_t clamp_edge(int64_t e, int64_t n_edges) {
@@ -391,7 +397,7 @@ __device__ __forceinline__ void load_rows(const float* base, int64_t rs, int64_t
   for (int h = 0; h < H; ++h) {
     const rsrc_t rr = make_rsrc(base + v * rs + h * hs, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
-    for (int k = 0; k < NS; ++k) r[h][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+    for (int k = 0; k < NS; ++k) r[h][k] = bload4<kStream>(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
   }
 }
 
@@ -412,7 +418,7 @@ __device__ __forceinline__ void load_q_rows(const TgatParams& P, int64_t v, floa
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
       const int c = lane + k * kWave;
-      r[h][k] = bload4(rr, q_chunk_used(P, c) ? 16u * static_cast<uint32_t>(c) : 0x7ffffff0u);
+      r[h][k] = bload4<kStream>(rr, q_chunk_used(P, c) ? 16u * static_cast<uint32_t>(c) : 0x7ffffff0u);
     }
   }
 }
@@ -425,7 +431,7 @@ __device__ __forceinline__ void store_rows(float* base, int64_t rs, int64_t hs, 
   for (int h = 0; h < H; ++h) {
     const rsrc_t rr = make_rsrc(base + v * rs + h * hs, 4u * static_cast<uint32_t>(kp));
 #pragma unroll
-    for (int k = 0; k < NS; ++k) bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), r[h][k]);
+    for (int k = 0; k < NS; ++k) bstore4<kStream>(rr, 16u * static_cast<uint32_t>(lane + k * kWave), r[h][k]);
   }
 }
 
@@ -1528,7 +1534,7 @@ __global__ __launch_bounds__(kBlock) void tgat_fwd_hs(TgatParams P) {
       const rsrc_t rr = make_rsrc(P.qt + v * P.qt_rs + h * P.qt_hs, 4u * static_cast<uint32_t>(P.kp));
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
-        q[g][k] = bload4(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
+        q[g][k] = bload4<kStream>(rr, 16u * static_cast<uint32_t>(lane + k * kWave));
         acc[g][k] = f4_zero();
       }
       m[g] = -INFINITY;
@@ -1576,7 +1582,7 @@ __global__ __launch_bounds__(kBlock) void tgat_fwd_hs(TgatParams P) {
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
         scale4(acc[g][k], inv);
-        bstore4(rr, 16u * static_cast<uint32_t>(lane + k * kWave), acc[g][k]);
+        bstore4<kStream>(rr, 16u * static_cast<uint32_t>(lane + k * kWave), acc[g][k]);
       }
       if (lane == 0) {
         P.stats[(v * H + h) * 2 + 0] = m[g];

@@ -163,6 +163,17 @@ __device__ __forceinline__ void bstore4_dwords(rsrc_t r, uint32_t off, const flo
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
 }
 
+// The same non-temporal policy for plain float4 pointers.
+typedef float nt4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load_nt(const float4* p) {
+  const nt4 v = __builtin_nontemporal_load(reinterpret_cast<const nt4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void store_nt(float4* p, const float4& x) {
+  const nt4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<nt4*>(p));
+}
+
 template <int AUX = 0>
 __device__ __forceinline__ void bstore4(rsrc_t r, uint32_t off, const float4& x) {
   typedef unsigned int u4 __attribute__((ext_vector_type(4)));
@@ -874,7 +885,7 @@ __global__ __launch_bounds__(kBlock, FA_PAIR_FWD_WAVES) void tgat_fwd_pair(TgatP
 #pragma unroll
       for (int r = 0; r < QR; ++r) {
         const int c = lane + r * kWave;
-        qv[h][r] = c < P.cp ? src[c] : f4_zero();
+        qv[h][r] = c < P.cp ? load_nt(src + c) : f4_zero();
       }
     }
     float4 xr[kPairDepth][NS];
@@ -931,7 +942,7 @@ __global__ __launch_bounds__(kBlock, FA_PAIR_FWD_WAVES) void tgat_fwd_pair(TgatP
         a.y = (a.y * r + b.y * ro) * inv;
         a.z = (a.z * r + b.z * ro) * inv;
         a.w = (a.w * r + b.w * ro) * inv;
-        if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = a;
+        if (half == 0 && L.live[k]) store_nt(reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)), a);
       }
       if (lane == h) {
         P.stats[(v * H + h) * 2 + 0] = mx;
@@ -1317,8 +1328,8 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS, DN)) void tgat_bw
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
           const int c = lane + r * kWave;
-          qv[r] = c < P.cp && q_chunk_used(P, c) ? qr[c] : f4_zero();
-          gv[r] = c < P.cp ? gr[c] : f4_zero();
+          qv[r] = c < P.cp && q_chunk_used(P, c) ? load_nt(qr + c) : f4_zero();
+          gv[r] = c < P.cp ? load_nt(gr + c) : f4_zero();
         }
 #pragma unroll
         for (int r = 0; r < QR; ++r) {
@@ -1367,7 +1378,7 @@ __global__ __launch_bounds__(kBlock, pair_bwd_min_waves(H, NS, DN)) void tgat_bw
         const float4 o = pick_f4(S.dq[h][k], other);
         const float4 a = S.dq[h][k];
         const float4 sum = make_float4(a.x + o.x, a.y + o.y, a.z + o.z, a.w + o.w);
-        if (half == 0 && L.live[k]) *reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)) = sum;
+        if (half == 0 && L.live[k]) store_nt(reinterpret_cast<float4*>(dst + 4 * (hl + k * kHalf)), sum);
       }
     }
   }

@@ -725,7 +725,7 @@ __device__ __forceinline__ void pair_load(const TgatParams& P, const PairCtx<NS>
       const uint2 w = *reinterpret_cast<const uint2*>(a);
       x[k] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), 0.f, 0.f);
     } else {
-      x[k] = *reinterpret_cast<const float4*>(a);
+      x[k] = load_nt(reinterpret_cast<const float4*>(a));
     }
   }
 }

@@ -24,21 +24,25 @@ __device__ __forceinline__ rsrc_t row_rsrc(const float* base, uint32_t bytes) {
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-template <bool VEC>
+// AUX: cache-policy bits; kStream (non-temporal) for rows read or written once, so that they
+// leave the caches first.
+constexpr int kStream = 2;
+
+template <bool VEC, int AUX = 0>
 __device__ __forceinline__ float4 load_chunk(rsrc_t r, uint32_t off) {
   if (VEC) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, AUX);
     return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                        __uint_as_float(v[3]));
   }
   const int o = static_cast<int>(off);
-  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
+  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, AUX)));
 }
 
-template <bool VEC>
+template <bool VEC, int AUX = 0>
 __device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4& x) {
   if (VEC) {
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
@@ -47,14 +51,14 @@ __device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4
     v[1] = __float_as_uint(x.y);
     v[2] = __float_as_uint(x.z);
     v[3] = __float_as_uint(x.w);
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, AUX);
     return;
   }
   const int o = static_cast<int>(off);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, AUX);
 }
 
 __device__ __forceinline__ int64_t lane_i64(int64_t v, int j) {
@@ -76,7 +80,7 @@ struct AggParams {
 };
 
 // Loads the rows of kBatchRows edges (ids broadcast from lanes j0.. of `ids`).
-template <int NS, bool VEC>
+template <int NS, bool VEC, int AUX = 0>
 __device__ __forceinline__ void load_batch(const AggParams& P, int64_t ids, int j0, int nb,
                                            float4 (&r)[kBatchRows][NS]) {
   const int lane = lane_id();
@@ -89,7 +93,7 @@ __device__ __forceinline__ void load_batch(const AggParams& P, int64_t ids, int 
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
         const int c = lane + k * kWave;
-        r[b][k] = c < P.chunks ? load_chunk<VEC>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
+        r[b][k] = c < P.chunks ? load_chunk<VEC, AUX>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
       }
     }
   }
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum(AggParams P) {
       for (int j = 0; j < cnt; j += kBatchRows) {
         const int nb = cnt - j < kBatchRows ? cnt - j : kBatchRows;
         float4 r[kBatchRows][NS];
-        load_batch<NS, VEC>(P, ids, j, nb, r);
+        load_batch<NS, VEC, kStream>(P, ids, j, nb, r);
 #pragma unroll
         for (int b = 0; b < kBatchRows; ++b)
           if (b < nb) add_chunks<NS>(acc, r[b]);
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(kBlock) void segment_sum(AggParams P) {
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
       const int c = lane + k * kWave;
-      if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
+      if (c < P.chunks) store_chunk<VEC, kStream>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
     }
   }
 }
@@ -256,7 +260,7 @@ __device__ __forceinline__ void zero_rows(const AggParams& P, int64_t r0, int64_
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
       const int c = hl + k * kHalf;
-      if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), f4_zero());
+      if (c < P.chunks) store_chunk<VEC, kStream>(orow, 16u * static_cast<uint32_t>(c), f4_zero());
     }
   }
 }
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
 #pragma unroll
               for (int k = 0; k < NS; ++k) {
                 const int c = hl + k * kHalf;
-                if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), r[q][k]);
+                if (c < P.chunks) store_chunk<VEC, kStream>(orow, 16u * static_cast<uint32_t>(c), r[q][k]);
               }
             }
           }
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
 #pragma unroll
               for (int k = 0; k < NS; ++k) {
                 const int c = hl + k * kHalf;
-                r[q][k] = c < P.chunks ? load_chunk<VEC>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
+                r[q][k] = c < P.chunks ? load_chunk<VEC, kStream>(rr, 16u * static_cast<uint32_t>(c)) : f4_zero();
               }
             }
 #pragma unroll
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
           const int c = hl + k * kHalf;
-          if (c < P.chunks) store_chunk<VEC>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
+          if (c < P.chunks) store_chunk<VEC, kStream>(orow, 16u * static_cast<uint32_t>(c), acc[k]);
         }
       }
     }

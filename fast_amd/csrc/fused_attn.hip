@@ -166,21 +166,24 @@ __device__ __forceinline__ rsrc_t row_rsrc(const float* base, uint32_t bytes) {
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-template <bool VEC>
+// AUX: cache-policy bits; kStream (non-temporal) for rows read or written once.
+constexpr int kStream = 2;
+
+template <bool VEC, int AUX = 0>
 __device__ __forceinline__ float4 chunk_load(rsrc_t r, uint32_t off) {
   if (VEC) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, AUX);
     return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
                        __uint_as_float(v[3]));
   }
   const int o = static_cast<int>(off);
-  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, 0)),
-                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, 0)));
+  return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 4, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 8, 0, AUX)),
+                     __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, o + 12, 0, AUX)));
 }
 
-template <bool VEC>
+template <bool VEC, int AUX = 0>
 __device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4& x) {
   if (VEC) {
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
@@ -189,14 +192,14 @@ __device__ __forceinline__ void store_chunk(rsrc_t r, uint32_t off, const float4
     w4[1] = __float_as_uint(x.y);
     w4[2] = __float_as_uint(x.z);
     w4[3] = __float_as_uint(x.w);
-    __builtin_amdgcn_raw_buffer_store_b128(w4, r, static_cast<int>(off), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(w4, r, static_cast<int>(off), 0, AUX);
     return;
   }
   const int o = static_cast<int>(off);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, 0);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.x), r, o, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.y), r, o + 4, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.z), r, o + 8, 0, AUX);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x.w), r, o + 12, 0, AUX);
 }
 
 __device__ __forceinline__ int64_t lane_i64(int64_t v, int j) {
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_fwd_half(FaParams P) {
       const int64_t row = (half ? s1 : s0) - P.n_dst;
       const bool ok = j0 + half < cnt && row >= 0 && row < P.n_v;
       const rsrc_t rr = row_rsrc(P.V + (ok ? row : 0) * P.dim, ok ? 4u * static_cast<uint32_t>(P.dim) : 0u);
-      r[b] = chunk_load<VEC>(rr, coff);
+      r[b] = chunk_load<VEC, kStream>(rr, coff);
     }
   };
   const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -675,7 +678,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
     for (int b = 0; b < kPairRows; ++b) {
       const int64_t row = row_of(my_src, j + 2 * b, cnt);
       const rsrc_t rr = row_rsrc(P.V + (row >= 0 ? row : 0) * P.dim, row >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
-      r[b] = chunk_load<VEC>(rr, coff);
+      r[b] = chunk_load<VEC, kStream>(rr, coff);
     }
   };
   const int64_t total = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -692,7 +695,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
         for (int64_t j = lb + half; j < le; j += 2) {
           const rsrc_t wr = row_rsrc(P.grad_V + (j < P.n_v ? j : 0) * P.dim,
                                      j < P.n_v ? 4u * static_cast<uint32_t>(P.dim) : 0u);
-          store_chunk<VEC>(wr, coff, f4_zero());
+          store_chunk<VEC, kStream>(wr, coff, f4_zero());
         }
       continue;
     }
@@ -700,7 +703,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
     float4 g;   // this lane's chunk of the destination's dout row
     {
       const rsrc_t dr = row_rsrc(P.dout + d * P.dim, 4u * static_cast<uint32_t>(P.dim));
-      g = chunk_load<VEC>(dr, coff);
+      g = chunk_load<VEC, kStream>(dr, coff);
     }
     float tsum[H];
 #pragma unroll
@@ -769,7 +772,7 @@ __global__ __launch_bounds__(kBlock) void fused_attn_bwd_half(FaParams P) {
             const int64_t wrow = row >= 0 ? row : (j0 + half < cnt && eh < P.n_v ? eh : -1);
             const rsrc_t wr = row_rsrc(P.grad_V + (wrow >= 0 ? wrow : 0) * P.dim,
                                        wrow >= 0 ? 4u * static_cast<uint32_t>(P.dim) : 0u);
-            store_chunk<VEC>(wr, coff, row >= 0 ? gv : f4_zero());
+            store_chunk<VEC, kStream>(wr, coff, row >= 0 ? gv : f4_zero());
           } else {
             *reinterpret_cast<float4*>(stage + 4 * hl) = gv;
             lds_sync();

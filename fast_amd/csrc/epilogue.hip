@@ -87,6 +87,19 @@ constexpr int kEpiRows = 2;   // rows per half-wave and iteration
 
 __device__ __forceinline__ float4 f4_load(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
+// Non-temporal access for rows read or written once here and not again soon (the w_out
+// products, the saved pre-norm rows, the upstream gradient), so that they leave the caches
+// first; the layer output and the input gradient, read next, keep the default policy.
+typedef float nt4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 f4_load_nt(const float* p) {
+  const nt4 v = __builtin_nontemporal_load(reinterpret_cast<const nt4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void f4_store_nt(float* p, const float4& x) {
+  const nt4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<nt4*>(p));
+}
+
 __global__ __launch_bounds__(kBlock) void epilogue_fwd_h(EpiParams P) {
   const int lane = lane_id();
   const int half = lane >= kHalf ? 1 : 0, hl = lane & (kHalf - 1);
@@ -108,9 +121,9 @@ __global__ __launch_bounds__(kBlock) void epilogue_fwd_h(EpiParams P) {
       const int64_t r = r0 + i * slots;
       float4 a = f4_zero();
       if (on && r < P.n) {
-        a = f4_load(P.r1 + r * P.ld1 + c);
+        a = f4_load_nt(P.r1 + r * P.ld1 + c);
         if (P.r2) {
-          const float4 b = f4_load(P.r2 + r * P.ld2 + c);
+          const float4 b = f4_load_nt(P.r2 + r * P.ld2 + c);
           a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
         }
       }
@@ -135,7 +148,7 @@ __global__ __launch_bounds__(kBlock) void epilogue_fwd_h(EpiParams P) {
       const float4 dv = on ? make_float4(a.x - mean, a.y - mean, a.z - mean, a.w - mean) : f4_zero();
       const float rstd = 1.f / sqrtf(half_sum(dv.x * dv.x + dv.y * dv.y + dv.z * dv.z + dv.w * dv.w) * inv_d + P.eps);
       if (on && r < P.n) {
-        *reinterpret_cast<float4*>(P.y + r * P.d + c) = a;
+        f4_store_nt(P.y + r * P.d + c, a);
         *reinterpret_cast<float4*>(P.out + r * P.d + c) =
             make_float4(dv.x * rstd * gm.x + bt.x, dv.y * rstd * gm.y + bt.y,
                         dv.z * rstd * gm.z + bt.z, dv.w * rstd * gm.w + bt.w);
@@ -242,8 +255,8 @@ __global__ __launch_bounds__(kBlock) void epilogue_bwd_h(EpiBwdParams P) {
     const int64_t r = rb + half;
     const bool ok = on && r < P.n;
     const float mean = r < P.n ? P.stats[2 * r] : 0.f, rstd = r < P.n ? P.stats[2 * r + 1] : 0.f;
-    const float4 dy = ok ? f4_load(P.dout + r * P.d + c) : f4_zero();
-    const float4 yy = ok ? f4_load(P.y + r * P.d + c) : f4_zero();
+    const float4 dy = ok ? f4_load_nt(P.dout + r * P.d + c) : f4_zero();
+    const float4 yy = ok ? f4_load_nt(P.y + r * P.d + c) : f4_zero();
     const float4 yh = ok ? make_float4((yy.x - mean) * rstd, (yy.y - mean) * rstd, (yy.z - mean) * rstd,
                                        (yy.w - mean) * rstd)
                          : f4_zero();

@@ -272,7 +272,8 @@ constexpr int copy_rows(int ns) { return ns <= 4 ? 4 : 2; }
 // One wave per 64 consecutive edges of [lo, hi); the wave owns the runs (maximal ranges of
 // equal output index) that start in its edges and takes them two at a time, one per
 // half-wave. A run's owner sums its rows (lane hl holds chunks hl, hl+32, ...; the run's
-// source ids loaded 32 at a time, run_rows rows in flight), stores the output row, and zeroes
+// source ids from the tile's ids staged in LDS, or loaded 32 at a time past the tile;
+// run_rows rows in flight), stores the output row, and zeroes
 // the output rows between the previous run's index and its own. The rows before the first
 // index and after the last are zeroed by the whole grid. Indices outside [0, n_out) are not
 // written. With an unsorted index (flag set) the kernel zero-fills the output instead, for
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(kBlock) void run_scatter(AggParams P, const int* fl
     const int64_t tsrc = P.src[e0 + (lane < cnt ? lane : cnt - 1)];
     {
       // Every edge of the tile a run of its own (the last one too) and no gap below any of
-      // them: each output row is one source row, copied by half-waves, kCopyRows rows in
+      // them: each output row is one source row, copied by half-waves, copy_rows(NS) rows in
       // flight per half.
       const uint64_t all = cnt == kWave ? ~0ull : (1ull << cnt) - 1;
       const int64_t last = lane_i64(my, cnt - 1);
